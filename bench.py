@@ -1,0 +1,204 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X W8A16 hi/lo integer GEMM (BASELINE.json metric).
+
+One "step" is one launch of the headline GEMM: config C2, the GEGLU FF up-projection of a 64x64
+latent at batch 8 (A int16 [32768 x 320], W int8 [2560 x 320] with interleaved a/g rows, per-column
+requantisation, GEGLU epilogue to int32 [32768 x 1280] + per-row max). Inputs are seeded synthetic
+data resident in HBM before the timed region. `value` is effective int8 TOPS = 4*M*N*K / time (two
+int8 passes, 2 ops per MAC, real M, N, K).
+
+Also reported on the same JSON line: the roofline of that kernel (MFMA peak 5.0 POPS dense int8),
+the 194-GEMM UNet set (config C5) as one hipGraph in ms per replay, every other config's time, and
+the CPU baseline (the oracle restatement of the reference's integer semantics, timed on this host).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-unet] [--no-cpu] [--no-configs]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAK_INT8_TOPS = 5000.0      # MI355X dense int8 MFMA, 5.0 POPS
+PEAK_HBM_GBS = 8000.0        # MI355X HBM3E, 8 TB/s
+METRIC = "effective W8A16 TOPS & % int8 MFMA peak; UNet GEMM-set ms at batch 8"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def time_launches(fn, stream, steps, warmup):
+    """Average duration of `fn` (which launches on `stream`) over `steps` back-to-back launches,
+    from HIP events recorded on that stream."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for _ in range(steps):
+        fn()
+    t1.record(stream)
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1) / steps
+
+
+def pmc_traffic():
+    """HBM bytes per launch of the C2 kernel from the committed rocprofv3 PMC summary, if present."""
+    p = ROOT / "profiles" / "c2_geglu_pmc.json"
+    if p.exists():
+        try:
+            d = json.loads(p.read_text())
+            return d.get("hbm_bytes_per_launch"), d.get("source")
+        except Exception:
+            return None, None
+    return None, None
+
+
+def cpu_baseline(L, h, reps=3):
+    import numpy as np
+
+    import oracle
+
+    threads = oracle.lib().orc_get_threads()
+    times = []
+    for _ in range(reps):
+        t = time.perf_counter()
+        oracle.layer_reference(L, h)
+        times.append(time.perf_counter() - t)
+    tmed = float(np.median(times))
+    # one thread on a 2048-row sample
+    oracle.set_threads(1)
+    rows = 2048
+    t = time.perf_counter()
+    oracle.layer_reference(L, h, rows=(0, rows))
+    t1 = time.perf_counter() - t
+    oracle.set_threads(0)
+    return {
+        "value": round(L.ops / tmed / 1e12, 4), "unit": "TOPS", "cores": threads, "kind": "port",
+        "sample": f"full C2 GEMM ({L.M}x{L.K}x{L.N}, GEGLU + rowmax) by the C oracle (oracle/oracle.c, OpenMP), median of {reps}",
+        "ms": round(tmed * 1e3, 2),
+        "one_thread": {"value": round(L.ops * rows / L.M / t1 / 1e12, 5), "unit": "TOPS", "cores": 1,
+                        "sample": f"first {rows} rows of C2"},
+        "cpu": _cpu_model(),
+    }
+
+
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-unet", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-configs", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (the GEMM shards by rows with no "
+              "communication; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from vela_amd import configs as cf
+    from vela_amd import gemm as vg
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(2)
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.Stream(device=dev)
+
+    # ---- headline: C2 GEGLU
+    L = cf.c2(cf.EPI_GEGLU)
+    log(f"[bench] {L.name}: generating inputs")
+    prob = cf.DeviceProblem(L)
+    prob.reset()
+    torch.cuda.synchronize()
+    ms = time_launches(lambda: prob.run(stream=stream), stream, args.steps, args.warmup)
+    tops = L.ops / (ms * 1e-3) / 1e12
+    log(f"[bench] {L.name}: {ms * 1e3:.1f} us/launch, {tops:.1f} TOPS ({100 * tops / PEAK_INT8_TOPS:.1f}% of int8 peak)")
+    traffic, traffic_src = pmc_traffic()
+
+    out = {
+        "metric": METRIC,
+        "value": round(tops, 2),
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (seeded: Laplace(1500) int16 activations, Gaussian(40) int8 weights)",
+        "config": {"workload": "C2: W8A16 GEGLU up-proj, A int16 [32768x320] x W int8 [320x2560] -> int32 [32768x1280] + rowmax",
+                   "M": L.M, "K": L.K, "N": L.N, "epilogue": "GEGLU + rowmax", "source": "SRC_I16"},
+        "pct_int8_peak": round(100 * tops / PEAK_INT8_TOPS, 2),
+        "roofline": {"bound": "mfma", "achieved": round(tops, 2), "peak": PEAK_INT8_TOPS, "unit": "TOP/s",
+                     "frac": round(tops / PEAK_INT8_TOPS, 4),
+                     "traffic": traffic, "traffic_source": traffic_src,
+                     "algorithmic_ops_per_launch": L.ops, "algorithmic_bytes_per_launch": L.hbm_bytes,
+                     "hbm_gbs_algorithmic": round(L.hbm_bytes / (ms * 1e-3) / 1e9, 1), "hbm_peak_gbs": PEAK_HBM_GBS},
+    }
+
+    # ---- the other configurations (one line each in "configs")
+    if not args.no_configs:
+        table = {}
+        for Lc in [cf.c1(), cf.c2(cf.EPI_PLAIN), cf.c3(), *cf.c4()]:
+            p = cf.DeviceProblem(Lc)
+            p.reset()
+            torch.cuda.synchronize()
+            t = time_launches(lambda: p.run(stream=stream), stream, max(5, args.steps), 3)
+            table[Lc.name] = {"us": round(t * 1e3, 2), "tops": round(Lc.ops / (t * 1e-3) / 1e12, 2),
+                              "pct_int8_peak": round(100 * Lc.ops / (t * 1e-3) / 1e12 / PEAK_INT8_TOPS, 2),
+                              "gbs_algorithmic": round(Lc.hbm_bytes / (t * 1e-3) / 1e9, 1)}
+            log(f"[bench] {Lc.name}: {table[Lc.name]}")
+            del p
+        out["configs"] = table
+
+    # ---- C5: the UNet GEMM set as one graph
+    if not args.no_unet:
+        from vela_amd.unet import GemmSet
+
+        log("[bench] C5: building the 194-GEMM UNet set")
+        gs = GemmSet()
+        gs.capture()
+        t = time_launches(gs.replay, gs.stream, max(5, args.steps // 2), 2)
+        out["unet_gemm_set_ms"] = round(t, 4)
+        out["unet_gemm_set"] = {"gemms": len(gs.layers), "ms": round(t, 4), "tops": round(gs.ops / (t * 1e-3) / 1e12, 2),
+                                "pct_int8_peak": round(100 * gs.ops / (t * 1e-3) / 1e12 / PEAK_INT8_TOPS, 2),
+                                "ideal_mfma_ms": round(gs.ops / (PEAK_INT8_TOPS * 1e12) * 1e3, 4)}
+        log(f"[bench] C5: {out['unet_gemm_set']}")
+        del gs
+
+    # ---- CPU baseline (rank 0, N = 1)
+    if not args.no_cpu:
+        log("[bench] CPU baseline (oracle)")
+        out["cpu_baseline"] = cpu_baseline(L, prob.h)
+        out["gpu_over_cpu"] = round(tops / out["cpu_baseline"]["value"], 1)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,144 @@
+/*
+ * vgemm -- MI355X (gfx950) W8A16 hi/lo-split integer GEMM: the C ABI of libvgemm.so.
+ *
+ * Drop-in for the GEMM path of emanwrxsti/vela (supr-meow-vela). Each entry point names the
+ * reference interface it replaces (file:line in that repository). All pointers are device pointers
+ * unless stated; `stream` is a hipStream_t (NULL = the null stream). Every call is asynchronous on
+ * the stream, allocates no device memory and is legal inside hipStreamBeginCapture. Return value:
+ * VGEMM_OK, or a negative code with a message in vgemm_last_error() (thread-local).
+ *
+ * Arithmetic contract (src/gemm_hl.h:1-3):
+ *   q   = 256*hi + lo + 128                      (the 16-bit activation; hi = q>>8, lo = (q&255)-128)
+ *   acc = sum_k q[r,k] * W[n,k] = 256*Chi + Clo + 128*wsum[n]
+ *   Y[r,n] = sat32(rshr(acc * m[n], s[n] - e[r]) + b[n])     (+ residual, saturated)
+ * with cst[n] = int4 {m, s, b, wsum} and rshr/sat32 as in src/intops.cuh:9-17. Outputs are bit-exact.
+ */
+#ifndef VGEMM_H
+#define VGEMM_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    VGEMM_OK = 0,
+    VGEMM_ERR_ARG = -1,      /* invalid argument or unsupported shape (reference: std::runtime_error) */
+    VGEMM_ERR_HIP = -2,      /* a HIP runtime call failed */
+    VGEMM_ERR_UNSUPPORTED = -3
+};
+
+/* Epilogues: meow::GemmEpi values (src/gemm_hl.h:8). */
+enum { VGEMM_EPI_PLAIN = 0, VGEMM_EPI_SPLIT3 = 1, VGEMM_EPI_GEGLU = 2, VGEMM_EPI_GELU = 3, VGEMM_EPI_QKV = 4 };
+
+/* A sources: meow::GemmSrc values (src/gemm_hl.h:9) plus two int16 sources of this library:
+ *   VGEMM_SRC_I16    : int16 q [rows x ld16] -- the hi/lo planes of SRC_I8 stored as one 16-bit
+ *                      value (half the bytes of the int32 activations, the same bytes as the planes);
+ *                      split into signed hi / offset lo int8 on load. e[row] as for SRC_I8.
+ *   VGEMM_SRC_CONV16 : SRC_CONV32 semantics on an NHWC int16 image. */
+enum { VGEMM_SRC_I8 = 0, VGEMM_SRC_X32 = 1, VGEMM_SRC_CONV32 = 2, VGEMM_SRC_I16 = 3, VGEMM_SRC_CONV16 = 4 };
+
+/* A operand: meow::ASrc (src/gemm_hl.h:12-17), same fields in the same order, plus q16/ld16/img16. */
+typedef struct VgemmASrc {
+    int src;
+    const int8_t* hi; const int8_t* lo; int ld8; const int32_t* e;         /* SRC_I8 (e may be NULL = 0) */
+    const int32_t* x; int ldx; const uint32_t* rowmax; int K;              /* SRC_X32 (K = real columns) */
+    const int32_t* img; int H, W, C, stride, Ho, Wo;                       /* SRC_CONV32 (K = 9C, C % 16 == 0) */
+    const int16_t* q16; int ld16;                                          /* SRC_I16 (K % 8, ld16 % 8) */
+    const int16_t* img16;                                                  /* SRC_CONV16 (C % 16 == 0) */
+} VgemmASrc;
+
+/* Epilogue description: meow::AEpi (src/gemm_hl.h:18-26) in the same order, plus an optional
+ * split-K workspace (ws, ws_bytes; none = no split-K). The QKV and GroupNorm-statistics fields are
+ * accepted and rejected with VGEMM_ERR_UNSUPPORTED when used. */
+typedef struct VgemmAEpi {
+    int epi; int32_t* Y; int ldy; const int32_t* residual;
+    int Cs; int32_t* Y1; int32_t* Y2; const int32_t* Lphi;
+    uint32_t* rowmax;                   /* optional: atomicMax of |y| per output row (caller zeroes it) */
+    void* gnstat; int gnT;              /* GroupNorm statistics: not supported */
+    int heads, T, TpQ, TpK, C;          /* EPI_QKV: not supported */
+    int8_t *qhi, *qlo, *khi, *klo; int32_t *qe, *ke;
+    int64_t *qhs, *qls, *qts, *khs, *kls, *kts;
+    void* ws; size_t ws_bytes;          /* optional split-K workspace (device memory) */
+} VgemmAEpi;
+
+/* Fill an ASrc / AEpi with the reference's default member values (src = SRC_I8, stride = 1, rest 0). */
+void vgemm_asrc_init(VgemmASrc* a);
+void vgemm_aepi_init(VgemmAEpi* e);
+
+/* meow::k_gemm_hl2 (src/gemm_hl.h:27, src/gemm_hl.cu:350-370). W [Np x Kp] int8 (ld ldw), row n =
+ * output column n; rows of A >= Mreal and columns >= Nreal are neither read as data nor written. */
+int vgemm_hl2(void* stream, const VgemmASrc* A, int Mp, int Mreal, const int8_t* W, int ldw, int Np, int Nreal,
+              int Kp, const int32_t* cst, const VgemmAEpi* E);
+
+/* meow::k_gemm_hl (src/gemm_hl.h:30-33, src/gemm_hl.cu:371-376): SRC_I8 planes + epilogue. */
+int vgemm_hl(void* stream, const int8_t* Ahi, const int8_t* Alo, int lda, int Mp, int Mreal,
+             const int8_t* W, int ldw, int Np, int Nreal, int Kp, const int32_t* cst, const int32_t* e,
+             int32_t* Y, int ldy, const int32_t* residual, int epi, int Cs, int32_t* Y1, int32_t* Y2,
+             const int32_t* Lphi);
+
+/* meow::k_conv_e (src/gemm_hl.h:29, src/gemm_hl.cu:335-349): e[row] = row_exp(max over the 3x3
+ * window of pm), rows = B*Ho*Wo. */
+int vgemm_conv_e(void* stream, const uint32_t* pm, int B, int H, int W, int stride, int32_t* e);
+
+/* meow::gemm_hl_supported (src/gemm_hl.h:34, src/gemm_hl.cu:344): Mp % 64, Np % 64, Kp % 16. */
+int vgemm_supported(int Mp, int Np, int Kp);
+
+/* meow::g_gemm_hl_variant (src/gemm_hl.h:35, src/gemm_hl.cu:345): tile override, -1 = automatic.
+ * This library's variants: 0 = 128x128 tiles, 1 = 64x128, 2 = 128x64 (rows x columns). Values outside
+ * the table fall back to automatic selection. */
+void vgemm_set_variant(int v);
+int vgemm_get_variant(void);
+
+/* Split-K: force the number of K partitions for calls that pass a workspace (0 = automatic). */
+void vgemm_set_splitk(int s);
+/* Workspace bytes vgemm_hl2 uses for this shape at the current settings (0 = no split-K). */
+size_t vgemm_workspace_bytes(int Mp, int Mreal, int Np, int Nreal, int Kp, int epi);
+
+/* meow::Gemm (src/gemm.h:12-23, src/gemm.cu:7-70): C[M,N] = A[M,K] * W[N,K]^T, int8 x int8 -> int32,
+ * row-major, optional strided batch. K % 16 == 0, N % 4 == 0, 16-byte aligned pointers.
+ * The handle replaces the cuBLASLt plan cache; this library keeps no plans and needs no workspace. */
+int vgemm_i8_create(size_t ws_bytes, void** handle);
+int vgemm_i8_destroy(void* handle);
+int vgemm_i8_run(void* handle, void* stream, const int8_t* A, int lda, long long strideA, const int8_t* W, int ldw,
+                 long long strideW, int32_t* C, int ldc, long long strideC, int M, int N, int K, int batch);
+
+/* A-operand producers and cuBLASLt-path epilogues (src/kernels.h:11-21, 68-70). */
+/* meow::k_quant_rows (src/kernels.h:12-13): per-row quantisation of X[M,K] into hi/lo [Mp32 x Kp] + e. */
+int vgemm_quant_rows(void* stream, const int32_t* X, int M, int K, int ldx, int8_t* hi, int8_t* lo, int32_t* e, int Kp);
+/* meow::k_epilogue without GroupNorm statistics (src/kernels.h:14-17). */
+int vgemm_epilogue(void* stream, const int32_t* Chi, const int32_t* Clo, int M, int N, int ldc, const int32_t* cst,
+                   const int32_t* e, int32_t* Y, int ldy, const int32_t* residual);
+/* meow::k_pixmax (src/kernels.h:18-19). */
+int vgemm_pixmax(void* stream, const int32_t* X, int rows, int C, uint32_t* pm);
+/* meow::k_im2col3 (src/kernels.h:20-21). */
+int vgemm_im2col3(void* stream, const int32_t* X, const uint32_t* pm, int B, int H, int W, int C, int stride,
+                  int8_t* hi, int8_t* lo, int32_t* e, int Kp);
+/* meow::k_epilogue_split (src/kernels.h:68-69). */
+int vgemm_epilogue_split(void* stream, const int32_t* Chi, const int32_t* Clo, int M, int N, int ldc, const int32_t* cst,
+                         const int32_t* e, int Cs, int32_t* Y0, int32_t* Y1, int32_t* Y2);
+/* meow::k_epilogue_geglu_q (src/kernels.h:70). */
+int vgemm_epilogue_geglu_q(void* stream, const int32_t* Chi, const int32_t* Clo, int M, int F, int ldc, const int32_t* cst,
+                           const int32_t* e, const int32_t* Lphi, int8_t* hi, int8_t* lo, int32_t* eo, int Kp);
+
+/* Graph capture of a GEMM sequence (src/engine.cu:625-630, 661-667 capture the forward). begin/end
+ * wrap hipStreamBeginCapture (thread-local mode) / hipStreamEndCapture + hipGraphInstantiate. */
+int vgemm_graph_begin(void* stream);
+int vgemm_graph_end(void* stream, void** exec);
+int vgemm_graph_launch(void* exec, void* stream);
+int vgemm_graph_destroy(void* exec);
+
+/* Fill `count` uint32 words with `value` by a kernel (capture-safe replacement for the
+ * cudaMemsetAsync that zeroes rowmax buffers, src/engine.cu:161). */
+int vgemm_fill_u32(void* stream, uint32_t* p, size_t count, uint32_t value);
+
+/* Last error message of this thread ("" if none). */
+const char* vgemm_last_error(void);
+/* Library version string. */
+const char* vgemm_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,310 @@
+"""TEST INFRASTRUCTURE ONLY: ctypes wrapper of oracle/liboracle.so, the CPU restatement of the
+reference's W8A16 hi/lo GEMM semantics (oracle/oracle.c).
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import this package, and only
+to check (or time, as the CPU baseline) the product; vela_amd/ never does.
+"""
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+import numpy as np
+
+PATH = Path(__file__).resolve().parent / "liboracle.so"
+P, I, LL, SZ, I64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_longlong, ctypes.c_size_t, ctypes.c_int64
+
+SRC_I8, SRC_X32, SRC_CONV32, SRC_I16, SRC_CONV16 = 0, 1, 2, 3, 4
+EPI_PLAIN, EPI_SPLIT3, EPI_GEGLU, EPI_GELU = 0, 1, 2, 3
+
+
+class OrcGemm(ctypes.Structure):
+    _fields_ = [
+        ("src", I),
+        ("hi", P), ("lo", P), ("ld8", I),
+        ("e", P),
+        ("x", P), ("ldx", I), ("xrowmax", P),
+        ("q16", P), ("ld16", I),
+        ("img", P), ("img16", P),
+        ("K", I), ("H", I), ("W", I), ("C", I), ("stride", I), ("Ho", I), ("Wo", I),
+        ("Mreal", I), ("Nreal", I), ("Kp", I),
+        ("w", P), ("ldw", I),
+        ("cst", P),
+        ("epi", I),
+        ("Y", P), ("ldy", I), ("residual", P),
+        ("Cs", I), ("Y1", P), ("Y2", P),
+        ("Lphi", P),
+        ("rowmax", P),
+    ]
+
+
+_SIGS = {
+    "orc_set_threads": (None, [I]),
+    "orc_get_threads": (I, []),
+    "orc_sat32": (I64, [I64]),
+    "orc_rshr": (I64, [I64, I64]),
+    "orc_row_exp": (I, [I64]),
+    "orc_quant16": (I64, [I64, I]),
+    "orc_quant16_32": (ctypes.c_int32, [ctypes.c_int32, I]),
+    "orc_lut16i": (ctypes.c_int32, [I64, P]),
+    "orc_epi1": (ctypes.c_int32, [ctypes.c_int32, ctypes.c_int32, P, ctypes.c_int32]),
+    "orc_geglu": (ctypes.c_int32, [ctypes.c_int32, ctypes.c_int32, P]),
+    "orc_gelu": (ctypes.c_int32, [ctypes.c_int32, P]),
+    "orc_rshr_n": (None, [P, P, P, SZ]),
+    "orc_row_exp_n": (None, [P, P, SZ]),
+    "orc_quant16_32_n": (None, [P, P, P, SZ]),
+    "orc_lut16i_n": (None, [P, P, P, SZ]),
+    "orc_epi1_n": (None, [P, P, P, P, P, SZ]),
+    "orc_quant_rows": (None, [P, I, I, I, P, P, P, I]),
+    "orc_pixmax": (None, [P, I, I, P]),
+    "orc_im2col3": (None, [P, P, I, I, I, I, I, P, P, P, I]),
+    "orc_conv_e": (None, [P, I, I, I, I, P]),
+    "orc_epilogue": (None, [P, P, I, I, I, P, P, P, I, P]),
+    "orc_epilogue_split": (None, [P, P, I, I, I, P, P, I, P, P, P]),
+    "orc_epilogue_geglu_q": (None, [P, P, I, I, I, P, P, P, P, P, P, I]),
+    "orc_a_row": (I, [ctypes.POINTER(OrcGemm), I, P, P, P]),
+    "orc_gemm_hl_rows": (I, [ctypes.POINTER(OrcGemm), I, I]),
+    "orc_gemm_hl": (I, [ctypes.POINTER(OrcGemm)]),
+    "orc_gemm_planes": (I, [ctypes.POINTER(OrcGemm), P, P, I]),
+    "orc_i8gemm": (None, [P, I, LL, P, I, LL, P, I, LL, I, I, I, I]),
+    "orc_prep_weight": (None, [P, I, I, I, P, P, P, I, I, P, P]),
+    "orc_interleave2": (None, [P, P, P, P, I, I, P, P]),
+}
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not PATH.exists():
+            raise RuntimeError(f"{PATH} is not built: run `python -m vela_amd.build`")
+        L = ctypes.CDLL(str(PATH))
+        for name, (res, args) in _SIGS.items():
+            getattr(L, name).restype = res
+            getattr(L, name).argtypes = args
+        _lib = L
+    return _lib
+
+
+def a(x):
+    """Address of a C-contiguous numpy array (None -> NULL)."""
+    if x is None:
+        return None
+    assert x.flags.c_contiguous, "oracle inputs must be C-contiguous"
+    return x.ctypes.data
+
+
+def set_threads(n: int) -> None:
+    lib().orc_set_threads(n)
+
+
+# ---------------------------------------------------------------- vectorised primitives
+
+def rshr(v, s):
+    v = np.ascontiguousarray(v, np.int64); s = np.ascontiguousarray(np.broadcast_to(s, v.shape), np.int64)
+    out = np.empty_like(v); lib().orc_rshr_n(a(v), a(s), a(out), v.size); return out
+
+
+def row_exp(m):
+    m = np.ascontiguousarray(m, np.int64); out = np.empty(m.shape, np.int32); lib().orc_row_exp_n(a(m), a(out), m.size); return out
+
+
+def quant16_32(v, e):
+    v = np.ascontiguousarray(v, np.int32); e = np.ascontiguousarray(np.broadcast_to(e, v.shape), np.int32)
+    out = np.empty_like(v); lib().orc_quant16_32_n(a(v), a(e), a(out), v.size); return out
+
+
+def lut16i(x, L):
+    x = np.ascontiguousarray(x, np.int64); L = np.ascontiguousarray(L, np.int32)
+    out = np.empty(x.shape, np.int32); lib().orc_lut16i_n(a(x), a(L), a(out), x.size); return out
+
+
+def epi1(chi, clo, cst4, er):
+    chi = np.ascontiguousarray(chi, np.int32); clo = np.ascontiguousarray(clo, np.int32)
+    cst4 = np.ascontiguousarray(cst4, np.int32).reshape(-1, 4); er = np.ascontiguousarray(np.broadcast_to(er, chi.shape), np.int32)
+    out = np.empty_like(chi); lib().orc_epi1_n(a(chi), a(clo), a(cst4), a(er), a(out), chi.size); return out
+
+
+# ---------------------------------------------------------------- GEMM
+
+def gemm(src, *, Mreal, Nreal, Kp, w, cst, epi=EPI_PLAIN, e=None, hi=None, lo=None, q16=None, x=None, xrowmax=None,
+         img=None, K=0, H=0, W=0, C=0, stride=1, Lphi=None, residual=None, Y=None, ldy=None, Cs=0, Y1=None, Y2=None,
+         rowmax=None, rows=None):
+    """Run the oracle GEMM. Returns Y (allocated if not given). `rows` = (r0, r1) limits the rows."""
+    g = OrcGemm()
+    g.src = src
+    keep = []
+
+    def put(x_, dt):
+        if x_ is None:
+            return None
+        y = np.ascontiguousarray(x_, dt)
+        keep.append(y)
+        return a(y)
+
+    g.e = put(e, np.int32)
+    if src == SRC_I8:
+        g.hi, g.lo, g.ld8 = put(hi, np.int8), put(lo, np.int8), hi.shape[-1]
+    elif src == SRC_I16:
+        g.q16, g.ld16, g.K = put(q16, np.int16), q16.shape[-1], K or q16.shape[-1]
+    elif src == SRC_X32:
+        g.x, g.ldx, g.xrowmax, g.K = put(x, np.int32), x.shape[-1], put(xrowmax, np.uint32), K or x.shape[-1]
+    elif src in (SRC_CONV32, SRC_CONV16):
+        if src == SRC_CONV32:
+            g.img = put(img, np.int32)
+        else:
+            g.img16 = put(img, np.int16)
+        g.H, g.W, g.C, g.stride = H, W, C, stride
+        g.Ho, g.Wo, g.K = (H - 1) // stride + 1, (W - 1) // stride + 1, 9 * C
+    g.Mreal, g.Nreal, g.Kp = Mreal, Nreal, Kp
+    g.w, g.ldw = put(w, np.int8), w.shape[-1]
+    g.cst = put(cst, np.int32)
+    g.epi = epi
+    nout = Nreal // 2 if epi == EPI_GEGLU else Nreal
+    if Y is None and epi != EPI_SPLIT3:
+        Y = np.zeros((Mreal, ldy or nout), np.int32)
+    if Y is not None:
+        assert Y.flags.c_contiguous and Y.dtype == np.int32
+        g.Y, g.ldy = a(Y), ldy or Y.shape[-1]
+    g.residual = put(residual, np.int32)
+    g.Cs = Cs
+    if Y1 is not None:
+        g.Y1 = a(Y1)
+    if Y2 is not None:
+        g.Y2 = a(Y2)
+    g.Lphi = put(Lphi, np.int32)
+    if rowmax is not None:
+        assert rowmax.flags.c_contiguous and rowmax.dtype in (np.uint32, np.int32)
+        g.rowmax = a(rowmax)
+    r0, r1 = rows if rows is not None else (0, Mreal)
+    rc = lib().orc_gemm_hl_rows(ctypes.byref(g), r0, r1)
+    if rc:
+        raise ValueError("oracle rejected the GEMM description")
+    return Y
+
+
+def planes(src, *, Mreal, Nreal, Kp, w, **kw):
+    """Per-plane int32 sums Chi, Clo [Mreal x Nreal]."""
+    g = OrcGemm()
+    keep = []
+    # reuse gemm()'s packing by building the struct the same way
+    Chi = np.zeros((Mreal, Nreal), np.int32)
+    Clo = np.zeros((Mreal, Nreal), np.int32)
+    g.src = src
+    e = kw.get("e")
+    if e is not None:
+        e = np.ascontiguousarray(e, np.int32); keep.append(e); g.e = a(e)
+    if src == SRC_I8:
+        hi = np.ascontiguousarray(kw["hi"], np.int8); lo = np.ascontiguousarray(kw["lo"], np.int8); keep += [hi, lo]
+        g.hi, g.lo, g.ld8 = a(hi), a(lo), hi.shape[-1]
+    elif src == SRC_I16:
+        q = np.ascontiguousarray(kw["q16"], np.int16); keep.append(q)
+        g.q16, g.ld16, g.K = a(q), q.shape[-1], kw.get("K") or q.shape[-1]
+    else:
+        raise ValueError("planes() takes SRC_I8 / SRC_I16")
+    w = np.ascontiguousarray(w, np.int8); keep.append(w)
+    g.w, g.ldw = a(w), w.shape[-1]
+    g.Mreal, g.Nreal, g.Kp = Mreal, Nreal, Kp
+    if lib().orc_gemm_planes(ctypes.byref(g), a(Chi), a(Clo), Nreal):
+        raise ValueError("oracle rejected the GEMM description")
+    return Chi, Clo
+
+
+def i8gemm(A, W, M, N, K, batch=1, sA=0, sW=0, sC=0, lda=None, ldw=None, ldc=None):
+    A = np.ascontiguousarray(A, np.int8); W = np.ascontiguousarray(W, np.int8)
+    lda = lda or K; ldw = ldw or K; ldc = ldc or N
+    C = np.zeros(max(sC * batch, M * ldc) if batch > 1 else M * ldc, np.int32)
+    lib().orc_i8gemm(a(A), lda, sA, a(W), ldw, sW, a(C), ldc, sC, M, N, K, batch)
+    return C
+
+
+# ---------------------------------------------------------------- producers
+
+def quant_rows(X, M, K, ldx, Kp):
+    X = np.ascontiguousarray(X, np.int32)
+    Mp = (M + 31) // 32 * 32
+    hi = np.zeros((Mp, Kp), np.int8); lo = np.zeros((Mp, Kp), np.int8); e = np.zeros(Mp, np.int32)
+    lib().orc_quant_rows(a(X), M, K, ldx, a(hi), a(lo), a(e), Kp)
+    return hi, lo, e
+
+
+def pixmax(X, rows, C):
+    X = np.ascontiguousarray(X, np.int32); pm = np.zeros(rows, np.uint32)
+    lib().orc_pixmax(a(X), rows, C, a(pm)); return pm
+
+
+def im2col3(X, pm, B, H, W, C, stride, Kp):
+    X = np.ascontiguousarray(X, np.int32); pm = np.ascontiguousarray(pm, np.uint32)
+    Ho, Wo = (H - 1) // stride + 1, (W - 1) // stride + 1
+    rows = B * Ho * Wo; Mp = (rows + 31) // 32 * 32
+    hi = np.zeros((Mp, Kp), np.int8); lo = np.zeros((Mp, Kp), np.int8); e = np.zeros(Mp, np.int32)
+    lib().orc_im2col3(a(X), a(pm), B, H, W, C, stride, a(hi), a(lo), a(e), Kp)
+    return hi, lo, e
+
+
+def conv_e(pm, B, H, W, stride):
+    pm = np.ascontiguousarray(pm, np.uint32)
+    rows = B * ((H - 1) // stride + 1) * ((W - 1) // stride + 1)
+    e = np.zeros(rows, np.int32); lib().orc_conv_e(a(pm), B, H, W, stride, a(e)); return e
+
+
+def epilogue(Chi, Clo, M, N, ldc, cst, e, ldy, R=None):
+    Chi = np.ascontiguousarray(Chi, np.int32); Clo = np.ascontiguousarray(Clo, np.int32)
+    cst = np.ascontiguousarray(cst, np.int32); e = np.ascontiguousarray(e, np.int32)
+    Y = np.zeros((M, ldy), np.int32)
+    Rr = None if R is None else np.ascontiguousarray(R, np.int32)
+    lib().orc_epilogue(a(Chi), a(Clo), M, N, ldc, a(cst), a(e), a(Y), ldy, a(Rr))
+    return Y
+
+
+def epilogue_split(Chi, Clo, M, N, ldc, cst, e, Cs):
+    Chi = np.ascontiguousarray(Chi, np.int32); Clo = np.ascontiguousarray(Clo, np.int32)
+    cst = np.ascontiguousarray(cst, np.int32); e = np.ascontiguousarray(e, np.int32)
+    Y0, Y1, Y2 = (np.zeros((M, Cs), np.int32) for _ in range(3))
+    lib().orc_epilogue_split(a(Chi), a(Clo), M, N, ldc, a(cst), a(e), Cs, a(Y0), a(Y1), a(Y2))
+    return Y0, Y1, Y2
+
+
+def epilogue_geglu_q(Chi, Clo, M, F, ldc, cst, e, L, Kp):
+    Chi = np.ascontiguousarray(Chi, np.int32); Clo = np.ascontiguousarray(Clo, np.int32)
+    cst = np.ascontiguousarray(cst, np.int32); e = np.ascontiguousarray(e, np.int32); L = np.ascontiguousarray(L, np.int32)
+    hi = np.zeros((M, Kp), np.int8); lo = np.zeros((M, Kp), np.int8); eo = np.zeros(M, np.int32)
+    lib().orc_epilogue_geglu_q(a(Chi), a(Clo), M, F, ldc, a(cst), a(e), a(L), a(hi), a(lo), a(eo), Kp)
+    return hi, lo, eo
+
+
+def prep_weight(w, N, K, conv3, m, s, b, Np, Kp):
+    w = np.ascontiguousarray(w, np.int8)
+    m, s, b = (np.ascontiguousarray(v, np.int32) for v in (m, s, b))
+    wout = np.zeros((Np, Kp), np.int8); cst = np.zeros((Np, 4), np.int32)
+    lib().orc_prep_weight(a(w), N, K, int(conv3), a(m), a(s), a(b), Np, Kp, a(wout), a(cst))
+    return wout, cst
+
+
+def interleave2(wa, ca, wg, cg, N, Kp):
+    wa, wg = np.ascontiguousarray(wa, np.int8), np.ascontiguousarray(wg, np.int8)
+    ca, cg = np.ascontiguousarray(ca, np.int32), np.ascontiguousarray(cg, np.int32)
+    Np = (2 * N + 63) // 64 * 64
+    wout = np.zeros((Np, Kp), np.int8); cout = np.zeros((Np, 4), np.int32)
+    lib().orc_interleave2(a(wa), a(ca), a(wg), a(cg), N, Kp, a(wout), a(cout))
+    return wout, cout
+
+
+# ---------------------------------------------------------------- convenience for vela_amd.configs layers
+
+def layer_reference(L, h, rows=None, seed_y=None):
+    """Oracle output of a vela_amd.configs.Layer with host inputs h (rows = (r0, r1) subset).
+    Returns (Y, rowmax); rows outside the subset stay zero (or the residual seed)."""
+    nout = L.Nout
+    Y = np.zeros((L.M, nout), np.int32) if seed_y is None else np.array(seed_y, np.int32, copy=True)
+    if L.residual:
+        Y[...] = h["res"]
+    rowmax = np.zeros(L.M, np.uint32) if L.rowmax else None
+    kw = dict(Mreal=L.M, Nreal=L.N, Kp=L.Kp, w=h["w"], cst=h["cst"], epi=L.epi, e=h.get("e"), Lphi=h.get("lphi"),
+              Y=Y, ldy=nout, residual=Y if L.residual else None, rowmax=rowmax, rows=rows)
+    if L.src == SRC_CONV16:
+        gemm(SRC_CONV16, img=h["img"], H=L.H, W=L.W, C=L.C, stride=L.stride, **kw)
+    else:
+        gemm(SRC_I16, q16=h["a"], K=h["a"].shape[1], **kw)
+    return Y, rowmax

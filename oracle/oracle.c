@@ -1,0 +1,472 @@
+/*
+ * TEST INFRASTRUCTURE ONLY -- CPU restatement of the reference's W8A16 hi/lo integer GEMM path
+ * (emanwrxsti/vela: src/intops.cuh, src/gemm_hl.cu, src/kernels.cu, src/engine.cu).
+ *
+ * Used as the correctness oracle by tests/ and __graft_entry__.smoke(), and timed by bench.py's
+ * cpu_baseline leg ("port": the reference has no CPU GEMM of its own). The MI355X product path in
+ * vela_amd/ never calls into this file.
+ *
+ * Structure deliberately follows the reference's arithmetic, not the GPU kernel's: the A operand is
+ * materialised as int8 hi/lo planes per row, each plane is dotted with W in int32, and the exact
+ * int64 epilogue epi1 reconstructs acc = 256*Chi + Clo + 128*wsum (src/gemm_hl.cu:40-43).
+ *
+ * How each function is pinned (tests/test_oracle_*.py): closed forms and brute force for the
+ * primitives, the reference's own edge lists (src/test_attn_score.cu:14, src/test_im2col.cu:13-20),
+ * an independent int64 q.W matmul with exact rational rounding for the GEMM, the m=1,s=0,b=0
+ * special case (a plain integer matmul), and hand-computed fixtures in tests/golden/.
+ */
+#include "oracle.h"
+
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+static int g_threads = 0;
+void orc_set_threads(int n) { g_threads = n; }
+int orc_get_threads(void) {
+#ifdef _OPENMP
+    return g_threads > 0 ? g_threads : omp_get_max_threads();
+#else
+    return 1;
+#endif
+}
+
+/* ------------------------------------------------------------------ primitives: src/intops.cuh */
+
+/* src/intops.cuh:9 */
+int64_t orc_sat32(int64_t v) { return v < INT64_C(-2147483648) ? INT64_C(-2147483648) : (v > INT64_C(2147483647) ? INT64_C(2147483647) : v); }
+
+/* src/intops.cuh:11-17. The rounding add wraps on overflow (as the device's 64-bit add does). */
+int64_t orc_rshr(int64_t v, int64_t s) {
+    if (s >= 0) {
+        const int p = s > 62 ? 62 : (int)s;
+        const int64_t half = (INT64_C(1) << p) >> 1;
+        const int64_t t = (int64_t)((uint64_t)v + (uint64_t)half);
+        return orc_sat32(t >> p);
+    }
+    const int neg = -s > 31 ? 31 : (int)(-s);
+    const int64_t lim = INT64_C(1) << (62 - neg);
+    const int64_t r = v < -lim ? -lim : (v > lim ? lim : v);
+    return orc_sat32(r * (INT64_C(1) << neg));
+}
+
+/* src/intops.cuh:37-38: e = #{k in [15,32): m >= 2^k} */
+int orc_row_exp(int64_t m) {
+    int e = 0;
+    for (int k = 15; k < 32; ++k) e += (m >= (INT64_C(1) << k));
+    return e;
+}
+
+/* src/intops.cuh:39 */
+int64_t orc_quant16(int64_t v, int e) {
+    const int64_t q = orc_rshr(v, e);
+    return q < -32767 ? -32767 : (q > 32767 ? 32767 : q);
+}
+
+/* src/intops.cuh:40-41 (e in [0,17]) */
+int32_t orc_quant16_32(int32_t v, int e) {
+    const int32_t q = e ? ((v >> e) + ((v >> (e - 1)) & 1)) : v;
+    return q < -32767 ? -32767 : (q > 32767 ? 32767 : q);
+}
+
+/* src/intops.cuh:42-50; the int32 interpolation wraps like the device's 32-bit arithmetic */
+int32_t orc_lut16i(int64_t x, const int32_t* L) {
+    const int64_t z = x + (INT64_C(16) << 16);
+    if (z < 0) return 0;
+    if (z >= (INT64_C(32) << 16)) return 65536;
+    const int i = (int)(z >> 10), f = (int)(z & 1023);
+    const int32_t a = L[i], b = L[i + 1];
+    const int32_t prod = (int32_t)(((uint32_t)b - (uint32_t)a) * (uint32_t)f);
+    return (int32_t)((uint32_t)a + (uint32_t)(prod >> 10));
+}
+
+/* src/intops.cuh:65-66 */
+void orc_split16(int64_t a, int8_t* hi, int8_t* lo) {
+    *hi = (int8_t)(a >> 8);
+    *lo = (int8_t)((a & 255) - 128);
+}
+
+/* src/gemm_hl.cu:40-43 (== src/kernels.cu:36-39, 59-62); c4 = {m, s, b, wsum}. acc*m wraps. */
+int32_t orc_epi1(int32_t chi, int32_t clo, const int32_t* c4, int32_t er) {
+    const int64_t acc = 256 * (int64_t)chi + (int64_t)clo + 128 * (int64_t)c4[3];
+    const int64_t v = (int64_t)((uint64_t)acc * (uint64_t)(int64_t)c4[0]);
+    return (int32_t)orc_sat32(orc_rshr(v, (int64_t)c4[1] - (int64_t)er) + c4[2]);
+}
+
+/* GEGLU of one interleaved pair: src/gemm_hl.cu:292-293 (== src/kernels.cu:510-513) */
+int32_t orc_geglu(int32_t a, int32_t g, const int32_t* L) {
+    const int64_t ge = orc_sat32(orc_rshr((int64_t)g * orc_lut16i(g, L), 16));
+    return (int32_t)orc_sat32(orc_rshr((int64_t)a * ge, 16));
+}
+
+/* GELU epilogue: src/gemm_hl.cu:280 */
+int32_t orc_gelu(int32_t y, const int32_t* L) { return (int32_t)orc_sat32(orc_rshr((int64_t)y * orc_lut16i(y, L), 16)); }
+
+void orc_rshr_n(const int64_t* v, const int64_t* s, int64_t* out, size_t n) { for (size_t i = 0; i < n; ++i) out[i] = orc_rshr(v[i], s[i]); }
+void orc_row_exp_n(const int64_t* m, int32_t* out, size_t n) { for (size_t i = 0; i < n; ++i) out[i] = orc_row_exp(m[i]); }
+void orc_quant16_32_n(const int32_t* v, const int32_t* e, int32_t* out, size_t n) { for (size_t i = 0; i < n; ++i) out[i] = orc_quant16_32(v[i], e[i]); }
+void orc_lut16i_n(const int64_t* x, const int32_t* L, int32_t* out, size_t n) { for (size_t i = 0; i < n; ++i) out[i] = orc_lut16i(x[i], L); }
+void orc_epi1_n(const int32_t* chi, const int32_t* clo, const int32_t* c4, const int32_t* er, int32_t* out, size_t n) {
+    for (size_t i = 0; i < n; ++i) out[i] = orc_epi1(chi[i], clo[i], c4 + 4 * i, er[i]);
+}
+
+static inline uint32_t uabs32(int32_t v) { return v < 0 ? (uint32_t)(-(int64_t)v) : (uint32_t)v; }
+static inline int8_t qhi(int32_t q) { return (int8_t)(q >> 8); }
+static inline int8_t qlo(int32_t q) { return (int8_t)((q & 255) - 128); }
+
+/* ------------------------------------------------------------------ producers: src/kernels.cu */
+
+/* k_quant_rows: src/kernels.cu:42-57, 488-497, 727-731. Rows [M, align32(M)) become the pad value
+ * 0 = (hi 0, lo -128); their e is left untouched. */
+void orc_quant_rows(const int32_t* X, int M, int K, int ldx, int8_t* hi, int8_t* lo, int32_t* e, int Kp) {
+    const int Mp = (M + 31) / 32 * 32;
+#pragma omp parallel for schedule(static) num_threads(orc_get_threads())
+    for (int r = 0; r < Mp; ++r) {
+        int8_t* h = hi + (size_t)r * Kp;
+        int8_t* l = lo + (size_t)r * Kp;
+        if (r >= M) {
+            for (int k = 0; k < Kp; ++k) { h[k] = 0; l[k] = -128; }
+            continue;
+        }
+        const int32_t* x = X + (size_t)r * ldx;
+        uint32_t m = 0;
+        for (int k = 0; k < K; ++k) { const uint32_t a = uabs32(x[k]); m = a > m ? a : m; }
+        const int ee = orc_row_exp(m);
+        e[r] = ee;
+        for (int k = 0; k < Kp; ++k) {
+            const int32_t q = k < K ? orc_quant16_32(x[k], ee) : 0;
+            h[k] = qhi(q); l[k] = qlo(q);
+        }
+    }
+}
+
+/* k_pixmax: src/kernels.cu:106-115 */
+void orc_pixmax(const int32_t* X, int rows, int C, uint32_t* pm) {
+#pragma omp parallel for schedule(static) num_threads(orc_get_threads())
+    for (int r = 0; r < rows; ++r) {
+        uint32_t m = 0;
+        for (int c = 0; c < C; ++c) { const uint32_t a = uabs32(X[(size_t)r * C + c]); m = a > m ? a : m; }
+        pm[r] = m;
+    }
+}
+
+static inline uint32_t window_max(const uint32_t* pm, int b, int H, int W, int stride, int oy, int ox) {
+    uint32_t m = 0;
+    for (int ky = 0; ky < 3; ++ky)
+        for (int kx = 0; kx < 3; ++kx) {
+            const int iy = oy * stride - 1 + ky, ix = ox * stride - 1 + kx;
+            if (iy >= 0 && iy < H && ix >= 0 && ix < W) {
+                const uint32_t v = pm[((size_t)b * H + iy) * W + ix];
+                m = v > m ? v : m;
+            }
+        }
+    return m;
+}
+
+/* k_im2col3: src/kernels.cu:117-170, 740-744. K index is tap-major (k = tap*C + c, tap = 3*ky + kx);
+ * pad columns [9C, Kp) hold the value 0 = (0,-128); pad rows [rows, align32(rows)) are memset to
+ * hi 0x00 / lo 0x80. */
+void orc_im2col3(const int32_t* X, const uint32_t* pm, int B, int H, int W, int C, int stride,
+                 int8_t* hi, int8_t* lo, int32_t* e, int Kp) {
+    const int Ho = (H - 1) / stride + 1, Wo = (W - 1) / stride + 1, rows = B * Ho * Wo;
+    const int Mp = (rows + 31) / 32 * 32, K = 9 * C;
+#pragma omp parallel for schedule(static) num_threads(orc_get_threads())
+    for (int r = 0; r < Mp; ++r) {
+        int8_t* h = hi + (size_t)r * Kp;
+        int8_t* l = lo + (size_t)r * Kp;
+        if (r >= rows) { memset(h, 0, (size_t)Kp); memset(l, 0x80, (size_t)Kp); continue; }
+        const int b = r / (Ho * Wo), p = r % (Ho * Wo), oy = p / Wo, ox = p % Wo;
+        const int ee = orc_row_exp(window_max(pm, b, H, W, stride, oy, ox));
+        e[r] = ee;
+        for (int tap = 0; tap < 9; ++tap) {
+            const int iy = oy * stride - 1 + tap / 3, ix = ox * stride - 1 + tap % 3;
+            const int in = iy >= 0 && iy < H && ix >= 0 && ix < W;
+            const int32_t* xp = in ? X + (((size_t)b * H + iy) * W + ix) * C : NULL;
+            for (int c = 0; c < C; ++c) {
+                const int32_t q = in ? orc_quant16_32(xp[c], ee) : 0;
+                h[tap * C + c] = qhi(q); l[tap * C + c] = qlo(q);
+            }
+        }
+        for (int k = K; k < Kp; ++k) { h[k] = 0; l[k] = -128; }
+    }
+}
+
+/* k_conv_e: src/gemm_hl.cu:335-341, 346-349 */
+void orc_conv_e(const uint32_t* pm, int B, int H, int W, int stride, int32_t* e) {
+    const int Ho = (H - 1) / stride + 1, Wo = (W - 1) / stride + 1, rows = B * Ho * Wo;
+#pragma omp parallel for schedule(static) num_threads(orc_get_threads())
+    for (int r = 0; r < rows; ++r) {
+        const int b = r / (Ho * Wo), p = r % (Ho * Wo), oy = p / Wo, ox = p % Wo;
+        e[r] = orc_row_exp(window_max(pm, b, H, W, stride, oy, ox));
+    }
+}
+
+/* k_epilogue (without GroupNorm statistics): src/kernels.cu:70-95 */
+void orc_epilogue(const int32_t* Chi, const int32_t* Clo, int M, int N, int ldc, const int32_t* cst,
+                  const int32_t* e, int32_t* Y, int ldy, const int32_t* R) {
+#pragma omp parallel for schedule(static) num_threads(orc_get_threads())
+    for (int r = 0; r < M; ++r)
+        for (int n = 0; n < N; ++n) {
+            int32_t y = orc_epi1(Chi[(size_t)r * ldc + n], Clo[(size_t)r * ldc + n], cst + 4 * n, e[r]);
+            if (R) y = (int32_t)orc_sat32((int64_t)y + R[(size_t)r * ldy + n]);
+            Y[(size_t)r * ldy + n] = y;
+        }
+}
+
+/* k_epilogue_split: src/kernels.cu:97-104 */
+void orc_epilogue_split(const int32_t* Chi, const int32_t* Clo, int M, int N, int ldc, const int32_t* cst,
+                        const int32_t* e, int Cs, int32_t* Y0, int32_t* Y1, int32_t* Y2) {
+#pragma omp parallel for schedule(static) num_threads(orc_get_threads())
+    for (int r = 0; r < M; ++r)
+        for (int n = 0; n < N; ++n) {
+            const int part = n >= 2 * Cs ? 2 : (n >= Cs ? 1 : 0);
+            int32_t* Y = part == 0 ? Y0 : (part == 1 ? Y1 : Y2);
+            Y[(size_t)r * Cs + (n - part * Cs)] = orc_epi1(Chi[(size_t)r * ldc + n], Clo[(size_t)r * ldc + n], cst + 4 * n, e[r]);
+        }
+}
+
+/* k_epilogue_geglu_q: src/kernels.cu:499-534 + quant_row_out (:250-259). Columns [0,F) are a,
+ * [F,2F) are g; output row-quantised to hi/lo [*, Kp] + e, pad columns (0,-128). */
+void orc_epilogue_geglu_q(const int32_t* Chi, const int32_t* Clo, int M, int F, int ldc, const int32_t* cst,
+                          const int32_t* e, const int32_t* L, int8_t* hi, int8_t* lo, int32_t* eo, int Kp) {
+#pragma omp parallel num_threads(orc_get_threads())
+    {
+        int32_t* v = (int32_t*)malloc(sizeof(int32_t) * (size_t)(F > 0 ? F : 1));
+#pragma omp for schedule(static)
+        for (int r = 0; r < M; ++r) {
+            const size_t base = (size_t)r * ldc;
+            uint32_t m = 0;
+            for (int c = 0; c < F; ++c) {
+                const int32_t a = orc_epi1(Chi[base + c], Clo[base + c], cst + 4 * c, e[r]);
+                const int32_t g = orc_epi1(Chi[base + F + c], Clo[base + F + c], cst + 4 * (F + c), e[r]);
+                v[c] = orc_geglu(a, g, L);
+                const uint32_t u = uabs32(v[c]);
+                m = u > m ? u : m;
+            }
+            const int ee = orc_row_exp(m);
+            eo[r] = ee;
+            int8_t* h = hi + (size_t)r * Kp;
+            int8_t* l = lo + (size_t)r * Kp;
+            for (int c = 0; c < F; ++c) { const int32_t q = orc_quant16_32(v[c], ee); h[c] = qhi(q); l[c] = qlo(q); }
+            for (int c = F; c < Kp; ++c) { h[c] = 0; l[c] = -128; }
+        }
+        free(v);
+    }
+}
+
+/* ------------------------------------------------------------------ the GEMMs */
+
+/* One row of A as hi/lo planes. SRC_I8: src/gemm_hl.cu:87-97. SRC_X32: src/gemm_hl.cu:99-121
+ * (e = row_exp(rowmax), q = quant16_32). SRC_CONV32: src/gemm_hl.cu:104-114 (implicit 3x3/pad-1
+ * im2col, tap-major K, outside the image -> 0). SRC_I16 holds q = 256*hi + lo + 128 directly;
+ * SRC_CONV16 is SRC_CONV32 on an int16 image. Columns k >= K are the value 0. */
+int orc_a_row(const OrcGemm* g, int r, int8_t* hi, int8_t* lo, int32_t* e) {
+    const int Kp = g->Kp;
+    switch (g->src) {
+    case ORC_SRC_I8:
+        memcpy(hi, g->hi + (size_t)r * g->ld8, (size_t)Kp);
+        memcpy(lo, g->lo + (size_t)r * g->ld8, (size_t)Kp);
+        *e = g->e ? g->e[r] : 0;
+        return 0;
+    case ORC_SRC_I16: {
+        const int16_t* q = g->q16 + (size_t)r * g->ld16;
+        for (int k = 0; k < Kp; ++k) { const int32_t v = k < g->K ? q[k] : 0; hi[k] = qhi(v); lo[k] = qlo(v); }
+        *e = g->e ? g->e[r] : 0;
+        return 0;
+    }
+    case ORC_SRC_X32: {
+        const int ee = orc_row_exp(g->xrowmax[r]);
+        const int32_t* x = g->x + (size_t)r * g->ldx;
+        for (int k = 0; k < Kp; ++k) { const int32_t q = k < g->K ? orc_quant16_32(x[k], ee) : 0; hi[k] = qhi(q); lo[k] = qlo(q); }
+        *e = ee;
+        return 0;
+    }
+    case ORC_SRC_CONV32:
+    case ORC_SRC_CONV16: {
+        const int C = g->C, HoWo = g->Ho * g->Wo;
+        const int b = r / HoWo, p = r % HoWo, oy = p / g->Wo, ox = p % g->Wo;
+        const int ee = g->e ? g->e[r] : 0;
+        for (int k = 0; k < Kp; ++k) {
+            int32_t q = 0;
+            if (k < g->K) {
+                const int tap = k / C, c = k % C;
+                const int iy = oy * g->stride - 1 + tap / 3, ix = ox * g->stride - 1 + tap % 3;
+                if (iy >= 0 && iy < g->H && ix >= 0 && ix < g->W) {
+                    const size_t at = (((size_t)b * g->H + iy) * g->W + ix) * C + c;
+                    const int32_t x = g->src == ORC_SRC_CONV32 ? g->img[at] : (int32_t)g->img16[at];
+                    q = orc_quant16_32(x, ee);
+                }
+            }
+            hi[k] = qhi(q); lo[k] = qlo(q);
+        }
+        *e = ee;
+        return 0;
+    }
+    default:
+        return -1;
+    }
+}
+
+/* Per-plane int32 dot products of one materialised row against columns [n0, n1) of W. |Chi|,|Clo|
+ * <= 2^14 * Kp, exact in int32 for Kp < 2^17 (src/gemm_hl.cu:138-161 computes the same sums). */
+static void row_planes(const int8_t* hi, const int8_t* lo, const int8_t* W, int ldw, int Kp, int n0, int n1,
+                       int32_t* chi, int32_t* clo) {
+    int n = n0;
+    for (; n + 4 <= n1; n += 4) {
+        const int8_t* w0 = W + (size_t)n * ldw;
+        const int8_t* w1 = w0 + ldw;
+        const int8_t* w2 = w1 + ldw;
+        const int8_t* w3 = w2 + ldw;
+        int32_t h0 = 0, h1 = 0, h2 = 0, h3 = 0, l0 = 0, l1 = 0, l2 = 0, l3 = 0;
+        for (int k = 0; k < Kp; ++k) {
+            const int32_t a = hi[k], b = lo[k];
+            h0 += a * w0[k]; h1 += a * w1[k]; h2 += a * w2[k]; h3 += a * w3[k];
+            l0 += b * w0[k]; l1 += b * w1[k]; l2 += b * w2[k]; l3 += b * w3[k];
+        }
+        chi[n] = h0; chi[n + 1] = h1; chi[n + 2] = h2; chi[n + 3] = h3;
+        clo[n] = l0; clo[n + 1] = l1; clo[n + 2] = l2; clo[n + 3] = l3;
+    }
+    for (; n < n1; ++n) {
+        const int8_t* w = W + (size_t)n * ldw;
+        int32_t h = 0, l = 0;
+        for (int k = 0; k < Kp; ++k) { h += hi[k] * w[k]; l += lo[k] * w[k]; }
+        chi[n] = h; clo[n] = l;
+    }
+}
+
+static int check_gemm(const OrcGemm* g) {
+    if (g->Kp <= 0 || g->Mreal < 0 || g->Nreal < 0) return -1;
+    if (g->epi == ORC_EPI_GEGLU && (g->Nreal & 1)) return -1;
+    if (g->src < 0 || g->src > ORC_SRC_CONV16) return -1;
+    return 0;
+}
+
+/* The fused-epilogue GEMM of src/gemm_hl.cu:65-310 for EPI_PLAIN (+residual, +rowmax), EPI_GELU,
+ * EPI_SPLIT3 and EPI_GEGLU (+rowmax), for output rows [r0, r1). Column pairs follow :269-297. */
+int orc_gemm_hl_rows(const OrcGemm* g, int r0, int r1) {
+    if (check_gemm(g)) return -1;
+    if (r1 <= 0 || r1 > g->Mreal) r1 = g->Mreal;
+    if (r0 < 0) r0 = 0;
+    const int Kp = g->Kp, N = g->Nreal;
+    int bad = 0;
+#pragma omp parallel num_threads(orc_get_threads()) reduction(| : bad)
+    {
+        int8_t* hi = (int8_t*)malloc((size_t)Kp);
+        int8_t* lo = (int8_t*)malloc((size_t)Kp);
+        int32_t* chi = (int32_t*)malloc(sizeof(int32_t) * (size_t)(N > 0 ? N : 1));
+        int32_t* clo = (int32_t*)malloc(sizeof(int32_t) * (size_t)(N > 0 ? N : 1));
+#pragma omp for schedule(dynamic, 16)
+        for (int r = r0; r < r1; ++r) {
+            int32_t er = 0;
+            if (orc_a_row(g, r, hi, lo, &er)) { bad = 1; continue; }
+            row_planes(hi, lo, g->w, g->ldw, Kp, 0, N, chi, clo);
+            uint32_t mx = 0;
+            if (g->epi == ORC_EPI_GEGLU) {
+                for (int n = 0; n + 1 < N; n += 2) {
+                    const int32_t a = orc_epi1(chi[n], clo[n], g->cst + 4 * n, er);
+                    const int32_t gg = orc_epi1(chi[n + 1], clo[n + 1], g->cst + 4 * (n + 1), er);
+                    const int32_t v = orc_geglu(a, gg, g->Lphi);
+                    g->Y[(size_t)r * g->ldy + (n >> 1)] = v;
+                    const uint32_t u = uabs32(v); mx = u > mx ? u : mx;
+                }
+            } else if (g->epi == ORC_EPI_SPLIT3) {
+                for (int n = 0; n < N; ++n) {
+                    const int part = n >= 2 * g->Cs ? 2 : (n >= g->Cs ? 1 : 0);
+                    int32_t* Y = part == 0 ? g->Y : (part == 1 ? g->Y1 : g->Y2);
+                    Y[(size_t)r * g->Cs + (n - part * g->Cs)] = orc_epi1(chi[n], clo[n], g->cst + 4 * n, er);
+                }
+            } else {
+                for (int n = 0; n < N; ++n) {
+                    int32_t y = orc_epi1(chi[n], clo[n], g->cst + 4 * n, er);
+                    if (g->epi == ORC_EPI_GELU) y = orc_gelu(y, g->Lphi);
+                    if (g->residual) y = (int32_t)orc_sat32((int64_t)y + g->residual[(size_t)r * g->ldy + n]);
+                    g->Y[(size_t)r * g->ldy + n] = y;
+                    const uint32_t u = uabs32(y); mx = u > mx ? u : mx;
+                }
+            }
+            if (g->rowmax && g->epi != ORC_EPI_SPLIT3 && mx > g->rowmax[r]) g->rowmax[r] = mx;
+        }
+        free(hi); free(lo); free(chi); free(clo);
+    }
+    return bad ? -1 : 0;
+}
+
+int orc_gemm_hl(const OrcGemm* g) { return orc_gemm_hl_rows(g, 0, g->Mreal); }
+
+int orc_gemm_planes(const OrcGemm* g, int32_t* Chi, int32_t* Clo, int ldc) {
+    if (check_gemm(g)) return -1;
+    const int Kp = g->Kp;
+    int bad = 0;
+#pragma omp parallel num_threads(orc_get_threads()) reduction(| : bad)
+    {
+        int8_t* hi = (int8_t*)malloc((size_t)Kp);
+        int8_t* lo = (int8_t*)malloc((size_t)Kp);
+#pragma omp for schedule(dynamic, 16)
+        for (int r = 0; r < g->Mreal; ++r) {
+            int32_t er;
+            if (orc_a_row(g, r, hi, lo, &er)) { bad = 1; continue; }
+            row_planes(hi, lo, g->w, g->ldw, Kp, 0, g->Nreal, Chi + (size_t)r * ldc, Clo + (size_t)r * ldc);
+        }
+        free(hi); free(lo);
+    }
+    return bad ? -1 : 0;
+}
+
+/* Gemm::run: C[M,N] = A[M,K] * W[N,K]^T, int32 accumulate (src/gemm.cu:22-29), strided batch (:30-35) */
+void orc_i8gemm(const int8_t* A, int lda, long long sA, const int8_t* W, int ldw, long long sW,
+                int32_t* C, int ldc, long long sC, int M, int N, int K, int batch) {
+    for (int bt = 0; bt < batch; ++bt) {
+        const int8_t* Ab = A + bt * sA;
+        const int8_t* Wb = W + bt * sW;
+        int32_t* Cb = C + bt * sC;
+#pragma omp parallel for schedule(static) num_threads(orc_get_threads())
+        for (int m = 0; m < M; ++m) {
+            const int8_t* a = Ab + (size_t)m * lda;
+            for (int n = 0; n < N; ++n) {
+                const int8_t* w = Wb + (size_t)n * ldw;
+                int32_t s = 0;
+                for (int k = 0; k < K; ++k) s += a[k] * w[k];
+                Cb[(size_t)m * ldc + n] = s;
+            }
+        }
+    }
+}
+
+/* ------------------------------------------------------------------ weight preparation */
+
+/* DevModel::load: src/engine.cu:26-44. W [N x K] (K = 9C for a 3x3 conv in PyTorch's c-major
+ * order) -> wout [Np x Kp] zero padded, tap-major for convs (kk = (k%9)*C + k/9), cst[n] = {m, s, b,
+ * wsum over the real K}; pad columns get {1, 0, 0, 0} (src/engine.cu:29). */
+void orc_prep_weight(const int8_t* w, int N, int K, int conv3, const int32_t* m, const int32_t* s,
+                     const int32_t* b, int Np, int Kp, int8_t* wout, int32_t* cst_out) {
+    const int C = conv3 ? K / 9 : 0;
+    memset(wout, 0, (size_t)Np * Kp);
+    for (int n = 0; n < Np; ++n) {
+        int32_t* c = cst_out + 4 * n;
+        if (n >= N) { c[0] = 1; c[1] = 0; c[2] = 0; c[3] = 0; continue; }
+        int64_t sum = 0;
+        for (int k = 0; k < K; ++k) {
+            const int kk = conv3 ? (k % 9) * C + k / 9 : k;
+            wout[(size_t)n * Kp + kk] = w[(size_t)n * K + k];
+            sum += w[(size_t)n * K + k];
+        }
+        c[0] = m[n]; c[1] = s[n]; c[2] = b[n]; c[3] = (int32_t)sum;
+    }
+}
+
+/* mergeLins(interleave = true) with two parts: src/engine.cu:71-101. wa, wg [N x Kp] (first N rows
+ * used), ca, cg [4N]. wout [Np x Kp] with Np = align64(2N); row 2i = a_i, 2i+1 = g_i. */
+void orc_interleave2(const int8_t* wa, const int32_t* ca, const int8_t* wg, const int32_t* cg, int N, int Kp,
+                     int8_t* wout, int32_t* cout) {
+    const int Np = (2 * N + 63) / 64 * 64;
+    memset(wout, 0, (size_t)Np * Kp);
+    for (int n = 0; n < Np; ++n) { cout[4 * n] = 1; cout[4 * n + 1] = 0; cout[4 * n + 2] = 0; cout[4 * n + 3] = 0; }
+    for (int i = 0; i < N; ++i) {
+        memcpy(wout + (size_t)(2 * i) * Kp, wa + (size_t)i * Kp, (size_t)Kp);
+        memcpy(wout + (size_t)(2 * i + 1) * Kp, wg + (size_t)i * Kp, (size_t)Kp);
+        memcpy(cout + 8 * i, ca + 4 * i, 16);
+        memcpy(cout + 8 * i + 4, cg + 4 * i, 16);
+    }
+}

@@ -1,0 +1,105 @@
+/*
+ * TEST INFRASTRUCTURE ONLY -- CPU restatement of the reference's W8A16 hi/lo integer GEMM path.
+ *
+ * This header and oracle.c are the correctness oracle (and the timed CPU baseline) for the MI355X
+ * library in vela_amd/. Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load
+ * the built liboracle.so, and only as the checker. The product path never calls it.
+ *
+ * Every function cites the reference (emanwrxsti/vela, paths relative to the repository root) whose
+ * behaviour it restates. Integer overflow that is undefined behaviour in the reference's C++ (int64
+ * products, int32 LUT interpolation) is restated with two's-complement wrapping, which is what the
+ * GPU hardware executing the reference produces.
+ */
+#ifndef VELA_ORACLE_H
+#define VELA_ORACLE_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Source and epilogue codes: the reference's GemmSrc / GemmEpi values (src/gemm_hl.h:8-9) plus the
+ * two int16 sources of this build (SRC_I16 = packed 16-bit view of the hi/lo planes, SRC_CONV16 =
+ * NHWC int16 image with the SRC_CONV32 semantics). */
+enum { ORC_SRC_I8 = 0, ORC_SRC_X32 = 1, ORC_SRC_CONV32 = 2, ORC_SRC_I16 = 3, ORC_SRC_CONV16 = 4 };
+enum { ORC_EPI_PLAIN = 0, ORC_EPI_SPLIT3 = 1, ORC_EPI_GEGLU = 2, ORC_EPI_GELU = 3 };
+
+typedef struct OrcGemm {
+    /* A operand (src/gemm_hl.h:12-17) */
+    int src;
+    const int8_t* hi; const int8_t* lo; int ld8;   /* SRC_I8 planes */
+    const int32_t* e;                                /* per-row shift: SRC_I8 / SRC_I16 / SRC_CONV* (NULL = 0) */
+    const int32_t* x; int ldx; const uint32_t* xrowmax; /* SRC_X32 */
+    const int16_t* q16; int ld16;                    /* SRC_I16 */
+    const int32_t* img; const int16_t* img16;        /* SRC_CONV32 / SRC_CONV16, NHWC */
+    int K, H, W, C, stride, Ho, Wo;
+    /* problem */
+    int Mreal, Nreal, Kp;
+    const int8_t* w; int ldw;                        /* W [Np x Kp], row n = output column n */
+    const int32_t* cst;                              /* int4 {m, s, b, wsum} per column */
+    /* epilogue (src/gemm_hl.h:18-22) */
+    int epi;
+    int32_t* Y; int ldy; const int32_t* residual;
+    int Cs; int32_t* Y1; int32_t* Y2;
+    const int32_t* Lphi;
+    uint32_t* rowmax;
+} OrcGemm;
+
+void orc_set_threads(int n);
+int orc_get_threads(void);
+
+/* ---- exact integer primitives: src/intops.cuh */
+int64_t orc_sat32(int64_t v);
+int64_t orc_rshr(int64_t v, int64_t s);
+int orc_row_exp(int64_t m);
+int64_t orc_quant16(int64_t v, int e);
+int32_t orc_quant16_32(int32_t v, int e);
+int32_t orc_lut16i(int64_t x, const int32_t* L);
+void orc_split16(int64_t a, int8_t* hi, int8_t* lo);
+int32_t orc_epi1(int32_t chi, int32_t clo, const int32_t* c4, int32_t er);
+int32_t orc_geglu(int32_t a, int32_t g, const int32_t* L);
+int32_t orc_gelu(int32_t y, const int32_t* L);
+/* element-wise batch forms of the primitives, for the known-answer tests */
+void orc_rshr_n(const int64_t* v, const int64_t* s, int64_t* out, size_t n);
+void orc_row_exp_n(const int64_t* m, int32_t* out, size_t n);
+void orc_quant16_32_n(const int32_t* v, const int32_t* e, int32_t* out, size_t n);
+void orc_lut16i_n(const int64_t* x, const int32_t* L, int32_t* out, size_t n);
+void orc_epi1_n(const int32_t* chi, const int32_t* clo, const int32_t* c4, const int32_t* er, int32_t* out, size_t n);
+
+/* ---- A-operand producers and cuBLASLt-path epilogues: src/kernels.cu, src/gemm_hl.cu */
+void orc_quant_rows(const int32_t* X, int M, int K, int ldx, int8_t* hi, int8_t* lo, int32_t* e, int Kp);
+void orc_pixmax(const int32_t* X, int rows, int C, uint32_t* pm);
+void orc_im2col3(const int32_t* X, const uint32_t* pm, int B, int H, int W, int C, int stride,
+                 int8_t* hi, int8_t* lo, int32_t* e, int Kp);
+void orc_conv_e(const uint32_t* pm, int B, int H, int W, int stride, int32_t* e);
+void orc_epilogue(const int32_t* Chi, const int32_t* Clo, int M, int N, int ldc, const int32_t* cst,
+                  const int32_t* e, int32_t* Y, int ldy, const int32_t* R);
+void orc_epilogue_split(const int32_t* Chi, const int32_t* Clo, int M, int N, int ldc, const int32_t* cst,
+                        const int32_t* e, int Cs, int32_t* Y0, int32_t* Y1, int32_t* Y2);
+void orc_epilogue_geglu_q(const int32_t* Chi, const int32_t* Clo, int M, int F, int ldc, const int32_t* cst,
+                          const int32_t* e, const int32_t* L, int8_t* hi, int8_t* lo, int32_t* eo, int Kp);
+
+/* ---- the GEMMs */
+/* one row of the A operand as hi/lo planes (Kp bytes each) and its shift e; returns 0 or -1 */
+int orc_a_row(const OrcGemm* g, int r, int8_t* hi, int8_t* lo, int32_t* e);
+/* the hi/lo GEMM with its fused epilogue (src/gemm_hl.cu:65-310); rows [r0, r1) only (r1 <= 0: all) */
+int orc_gemm_hl_rows(const OrcGemm* g, int r0, int r1);
+int orc_gemm_hl(const OrcGemm* g);
+/* per-plane int32 dot products only: Chi/Clo [Mreal x ldc] */
+int orc_gemm_planes(const OrcGemm* g, int32_t* Chi, int32_t* Clo, int ldc);
+/* C = A * W^T, int8 x int8 -> int32, strided batch (src/gemm.cu:46-70) */
+void orc_i8gemm(const int8_t* A, int lda, long long sA, const int8_t* W, int ldw, long long sW,
+                int32_t* C, int ldc, long long sC, int M, int N, int K, int batch);
+
+/* ---- weight preparation: src/engine.cu:26-44 (tap-major permutation, wsum, cst) */
+void orc_prep_weight(const int8_t* w, int N, int K, int conv3, const int32_t* m, const int32_t* s,
+                     const int32_t* b, int Np, int Kp, int8_t* wout, int32_t* cst_out);
+/* interleave two linears row-wise (a0, g0, a1, g1, ...): src/engine.cu:81-88 */
+void orc_interleave2(const int8_t* wa, const int32_t* ca, const int8_t* wg, const int32_t* cg, int N, int Kp,
+                     int8_t* wout, int32_t* cout);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

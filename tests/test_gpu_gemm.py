@@ -1,0 +1,277 @@
+"""GPU parity of the hi/lo GEMM (vgemm_hl2 / vgemm_hl through the C ABI) against the CPU oracle.
+
+Mirrors the reference's own GEMM tests: src/test_gemm_hl.cu:53-86 (random int8 planes, e in [0,12),
+m in [2^14, 2^15), s in [20, 30), b in [-50000, 50000), a random residual, every tile variant) and
+:10-52 (int32 sources of random bit width 1..31, so saturation and e up to 17 occur, against the
+planar path). Here every result is compared byte for byte with oracle/ instead of with cuBLASLt.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from tests.conftest import assert_equal, to_np
+from vela_amd import configs as cf
+from vela_amd import gemm as vg
+
+pytestmark = pytest.mark.gpu
+
+
+def rng(seed):
+    return np.random.default_rng(seed)
+
+
+def make_w_cst(r, N, K, Np, Kp, s_range=(20, 29), m_range=(1 << 14, 1 << 15), wlo=-128):
+    w = np.zeros((Np, Kp), np.int8)
+    w[:N, :K] = r.integers(wlo, 128, (N, K))
+    cst = np.zeros((Np, 4), np.int32)
+    cst[:, 0] = 1
+    cst[:N, 0] = r.integers(m_range[0], m_range[1], N, dtype=np.int64)
+    cst[:N, 1] = r.integers(s_range[0], s_range[1] + 1, N)
+    cst[:N, 2] = r.integers(-50000, 50000, N)
+    cst[:N, 3] = w[:N].astype(np.int64).sum(1)
+    return w, cst
+
+
+def rand_bits(r, shape):
+    bits = r.integers(1, 32, shape)
+    v = r.integers(0, 1 << 31, shape, dtype=np.int64) & ((np.int64(1) << bits) - 1)
+    return (v - (np.int64(1) << (bits - 1))).astype(np.int32)
+
+
+def dev(x):
+    return None if x is None else torch.from_numpy(np.ascontiguousarray(x)).cuda()
+
+
+class Case:
+    """Host inputs + oracle + device run of one vgemm_hl2 call."""
+
+    def __init__(self, src, M, N, K, epi=vg.EPI_PLAIN, seed=0, residual=False, rowmax=False, e_max=0, s_range=(20, 29),
+                 m_range=(1 << 14, 1 << 15), conv=None, lut=None, Cs=0):
+        r = rng(seed)
+        self.src, self.M, self.N, self.K, self.epi = src, M, N, K, epi
+        self.Kp = cf.align(K, 16)
+        self.Np = cf.align(N, 64)
+        self.Mp = cf.align(M, 64)
+        self.conv = conv
+        self.w, self.cst = make_w_cst(r, N, K, self.Np, self.Kp, s_range, m_range)
+        self.e = r.integers(0, e_max + 1, M).astype(np.int32) if e_max else None
+        self.kw = {}
+        if src == vg.SRC_I8:
+            self.hi = r.integers(-128, 128, (self.Mp, self.Kp)).astype(np.int8)
+            self.lo = r.integers(-128, 128, (self.Mp, self.Kp)).astype(np.int8)
+            self.kw = dict(hi=self.hi, lo=self.lo)
+        elif src == vg.SRC_I16:
+            self.q = r.integers(-32768, 32768, (M, K)).astype(np.int16)
+            self.kw = dict(q16=self.q, K=K)
+        elif src == vg.SRC_X32:
+            self.x = rand_bits(r, (M, K))
+            self.xrm = np.abs(self.x.astype(np.int64)).max(1).astype(np.uint32)
+            self.kw = dict(x=self.x, xrowmax=self.xrm, K=K)
+        else:
+            B, H, W, C, stride = conv
+            if src == vg.SRC_CONV32:
+                self.img = rand_bits(r, (B, H, W, C))
+            else:
+                self.img = r.integers(-32768, 32768, (B, H, W, C)).astype(np.int16)
+            pm = oracle.pixmax(self.img.astype(np.int32).reshape(-1, C), B * H * W, C)
+            self.e = oracle.conv_e(pm, B, H, W, stride)
+            self.kw = dict(img=self.img, H=H, W=W, C=C, stride=stride)
+        self.lut = lut if lut is not None else cf.phi_lut()
+        self.Cs = Cs
+        nout = N // 2 if epi == vg.EPI_GEGLU else N
+        self.nout = nout
+        self.res = r.integers(-(2**31), 2**31, (M, nout), dtype=np.int64).astype(np.int32) if residual else None
+        self.rowmax = rowmax
+
+    def reference(self):
+        kw = dict(self.kw)
+        if self.epi == vg.EPI_SPLIT3:
+            Y0, Y1, Y2 = (np.zeros((self.M, self.Cs), np.int32) for _ in range(3))
+            oracle.gemm(self.src, Mreal=self.M, Nreal=self.N, Kp=self.Kp, w=self.w, cst=self.cst, epi=self.epi, e=self.e,
+                        Lphi=self.lut, Y=Y0, ldy=self.Cs, Cs=self.Cs, Y1=Y1, Y2=Y2, **kw)
+            return (Y0, Y1, Y2), None
+        Y = np.zeros((self.M, self.nout), np.int32) if self.res is None else self.res.copy()
+        rm = np.zeros(self.M, np.uint32) if self.rowmax else None
+        oracle.gemm(self.src, Mreal=self.M, Nreal=self.N, Kp=self.Kp, w=self.w, cst=self.cst, epi=self.epi, e=self.e,
+                    Lphi=self.lut, Y=Y, residual=Y if self.res is not None else None, rowmax=rm, **kw)
+        return Y, rm
+
+    def run_gpu(self, ws_bytes=0):
+        A = vg.ASrc(src=self.src)
+        keep = {}
+        keep["e"] = dev(self.e)
+        A.e = vg.ptr(keep["e"])
+        if self.src == vg.SRC_I8:
+            keep["hi"], keep["lo"] = dev(self.hi), dev(self.lo)
+            A.hi, A.lo, A.ld8 = vg.ptr(keep["hi"]), vg.ptr(keep["lo"]), self.Kp
+        elif self.src == vg.SRC_I16:
+            keep["q"] = dev(self.q)
+            A.q16, A.ld16, A.K = vg.ptr(keep["q"]), self.K, self.K
+        elif self.src == vg.SRC_X32:
+            keep["x"], keep["rm"] = dev(self.x), dev(self.xrm.view(np.int32))
+            A.x, A.ldx, A.rowmax, A.K = vg.ptr(keep["x"]), self.K, vg.ptr(keep["rm"]), self.K
+        else:
+            B, H, W, C, stride = self.conv
+            keep["img"] = dev(self.img)
+            if self.src == vg.SRC_CONV32:
+                A.img = vg.ptr(keep["img"])
+            else:
+                A.img16 = vg.ptr(keep["img"])
+            A.H, A.W, A.C, A.stride = H, W, C, stride
+            A.Ho, A.Wo, A.K = (H - 1) // stride + 1, (W - 1) // stride + 1, 9 * C
+        w, cst = dev(self.w), dev(self.cst)
+        lut = dev(self.lut)
+        E = vg.AEpi(epi=self.epi, Lphi=vg.ptr(lut))
+        if self.epi == vg.EPI_SPLIT3:
+            Ys = [torch.zeros((self.M, self.Cs), dtype=torch.int32, device="cuda") for _ in range(3)]
+            E.Y, E.Y1, E.Y2, E.Cs, E.ldy = vg.ptr(Ys[0]), vg.ptr(Ys[1]), vg.ptr(Ys[2]), self.Cs, self.Cs
+        else:
+            Y = dev(self.res) if self.res is not None else torch.zeros((self.M, self.nout), dtype=torch.int32, device="cuda")
+            E.Y, E.ldy = vg.ptr(Y), self.nout
+            if self.res is not None:
+                E.residual = vg.ptr(Y)    # aliases Y, as src/engine.cu:431 does
+        rm = torch.zeros(self.M, dtype=torch.int32, device="cuda") if self.rowmax else None
+        E.rowmax = vg.ptr(rm)
+        ws = None
+        if ws_bytes:
+            ws = torch.empty(ws_bytes // 4 + 16, dtype=torch.int32, device="cuda")
+            E.ws, E.ws_bytes = vg.ptr(ws), ws_bytes
+        vg.k_gemm_hl2(A, self.Mp, self.M, w, self.Kp, self.Np, self.N, self.Kp, cst, E)
+        torch.cuda.synchronize()
+        if self.epi == vg.EPI_SPLIT3:
+            return tuple(to_np(y) for y in Ys), None
+        return to_np(Y), (to_np(rm).view(np.uint32) if rm is not None else None)
+
+    def check(self, ws_bytes=0, what=""):
+        got, grm = self.run_gpu(ws_bytes)
+        want, wrm = self.reference()
+        if self.epi == vg.EPI_SPLIT3:
+            for i in range(3):
+                assert_equal(got[i], want[i], f"{what} Y{i}")
+        else:
+            assert_equal(got, want, f"{what} Y")
+        if wrm is not None:
+            assert_equal(grm, wrm, f"{what} rowmax")
+
+
+@pytest.fixture(autouse=True)
+def _reset_knobs(gpu):
+    vg.set_variant(-1)
+    vg.set_splitk(0)
+    yield
+    vg.set_variant(-1)
+    vg.set_splitk(0)
+
+
+SHAPES = [(64, 64, 64), (100, 80, 48), (300, 200, 320), (257, 130, 96), (640, 320, 1280)]
+
+
+@pytest.mark.parametrize("variant", [0, 1, 2])
+@pytest.mark.parametrize("shape", SHAPES)
+def test_i8_planes_plain_residual(variant, shape):
+    """src/test_gemm_hl.cu:55-80 scaled down: random planes, e in [0,12), s in [20,30), residual."""
+    vg.set_variant(variant)
+    M, N, K = shape
+    Case(vg.SRC_I8, M, N, K, seed=hash(shape) % 1000 + variant, residual=True, e_max=11).check(what=f"I8 {shape} v{variant}")
+
+
+@pytest.mark.parametrize("variant", [0, 1, 2])
+@pytest.mark.parametrize("shape", SHAPES)
+def test_i16_plain(variant, shape):
+    vg.set_variant(variant)
+    M, N, K = shape
+    K = cf.align(K, 8)
+    Case(vg.SRC_I16, M, N, K, seed=7 + variant, s_range=(16, 24)).check(what=f"I16 {shape} v{variant}")
+
+
+@pytest.mark.parametrize("epi", [vg.EPI_PLAIN, vg.EPI_GEGLU, vg.EPI_GELU])
+@pytest.mark.parametrize("variant", [0, 1, 2])
+def test_i16_epilogues_rowmax(epi, variant):
+    vg.set_variant(variant)
+    Case(vg.SRC_I16, 384, 256, 320, epi=epi, seed=11, rowmax=True, e_max=3, s_range=(16, 24)).check(what=f"epi {epi} v{variant}")
+
+
+@pytest.mark.parametrize("variant", [0, 1, 2])
+def test_split3(variant):
+    vg.set_variant(variant)
+    Case(vg.SRC_I16, 200, 3 * 96, 128, epi=vg.EPI_SPLIT3, seed=12, Cs=96).check(what=f"split3 v{variant}")
+
+
+@pytest.mark.parametrize("variant", [0, 1])
+@pytest.mark.parametrize("shape", [(96, 64, 1024), (130, 320, 960), (64, 128, 64)])
+def test_x32_source(variant, shape):
+    """SRC_X32: int32 rows of random bit width 1..31 quantised on load (src/test_gemm_hl.cu:16,31-36)."""
+    vg.set_variant(variant)
+    M, N, K = shape
+    Case(vg.SRC_X32, M, N, K, seed=13).check(what=f"X32 {shape}")
+
+
+@pytest.mark.parametrize("src", [vg.SRC_CONV32, vg.SRC_CONV16])
+@pytest.mark.parametrize("geom", [(2, 8, 8, 32, 1), (1, 7, 5, 64, 2), (2, 6, 6, 320, 1), (1, 9, 11, 16, 2)])
+def test_conv_sources(src, geom):
+    """Implicit 3x3 im2col (src/test_gemm_hl.cu:12,25-29 cases scaled down), e from conv_e(pixmax)."""
+    B, H, W, C, stride = geom
+    Ho, Wo = (H - 1) // stride + 1, (W - 1) // stride + 1
+    Case(src, B * Ho * Wo, 96, 9 * C, seed=14, conv=geom, residual=True).check(what=f"conv {src} {geom}")
+
+
+@pytest.mark.parametrize("src", [vg.SRC_I8, vg.SRC_I16])
+def test_exact_slow_path(src):
+    """Shifts s - e outside [1, 52] (left shifts, s = 0, deep right shifts) and |acc * m| beyond 2^52
+    force the int64 epilogue; m up to 2^31 - 1 makes acc * m wrap exactly as the reference's int64."""
+    K = 512
+    for seed, s_range, m_range in [(1, (-6, 3), (1, 1 << 10)), (2, (50, 70), (1 << 14, 1 << 15)), (3, (20, 40), ((1 << 30), (1 << 31) - 1))]:
+        Case(src, 200, 128, K, seed=seed, s_range=s_range, m_range=m_range, e_max=5, residual=True).check(what=f"slow {seed}")
+
+
+def test_lut_outside_range_takes_exact_path():
+    """A GELU table with entries outside [0, 65536] (the FP64 path's precondition) uses the exact path."""
+    lut = rng(5).integers(-70000, 140000, 2049).astype(np.int32)
+    for epi in (vg.EPI_GEGLU, vg.EPI_GELU):
+        Case(vg.SRC_I16, 256, 128, 64, epi=epi, seed=15, lut=lut, rowmax=True).check(what=f"lut epi {epi}")
+
+
+@pytest.mark.parametrize("splits", [2, 3, 7])
+@pytest.mark.parametrize("epi", [vg.EPI_PLAIN, vg.EPI_GEGLU])
+def test_splitk(splits, epi):
+    """Split-K partials through a workspace reduce to the same bytes."""
+    vg.set_splitk(splits)
+    c = Case(vg.SRC_I16, 200, 192, 1536, epi=epi, seed=16, rowmax=True, residual=epi == vg.EPI_PLAIN)
+    nb = vg.workspace_bytes(c.Mp, c.M, c.Np, c.N, c.Kp, epi)
+    assert nb > 0
+    c.check(ws_bytes=nb, what=f"splitk {splits}")
+
+
+def test_conv_splitk():
+    vg.set_splitk(4)
+    c = Case(vg.SRC_CONV16, 2 * 8 * 8, 128, 9 * 256, seed=17, conv=(2, 8, 8, 256, 1), residual=True)
+    c.check(ws_bytes=vg.workspace_bytes(c.Mp, c.M, c.Np, c.N, c.Kp, 0), what="conv splitk")
+
+
+def test_k_gemm_hl_wrapper():
+    """meow::k_gemm_hl: the SRC_I8 convenience entry point with default arguments."""
+    c = Case(vg.SRC_I8, 130, 64, 96, seed=18, e_max=4)
+    want, _ = c.reference()
+    hi, lo, w, cst, e = dev(c.hi), dev(c.lo), dev(c.w), dev(c.cst), dev(c.e)
+    Y = torch.zeros((c.M, c.N), dtype=torch.int32, device="cuda")
+    vg.k_gemm_hl(hi, lo, c.Kp, c.Mp, c.M, w, c.Kp, c.Np, c.N, c.Kp, cst, e, Y, c.N)
+    torch.cuda.synchronize()
+    assert_equal(to_np(Y), want, "k_gemm_hl")
+
+
+def test_shape_errors():
+    """Unsupported shapes raise like src/gemm_hl.cu:351,357 (gemm_hl: unsupported shape / conv source)."""
+    c = Case(vg.SRC_I8, 64, 64, 64, seed=19)
+    w, cst = dev(c.w), dev(c.cst)
+    Y = torch.zeros((64, 64), dtype=torch.int32, device="cuda")
+    A = vg.ASrc(src=vg.SRC_I8, hi=vg.ptr(dev(c.hi)), lo=vg.ptr(dev(c.lo)), ld8=c.Kp)
+    E = vg.AEpi(Y=vg.ptr(Y), ldy=64)
+    with pytest.raises(vg.VgemmError, match="unsupported shape"):
+        vg.k_gemm_hl2(A, 63, 63, w, c.Kp, 64, 64, c.Kp, cst, E)
+    A2 = vg.ASrc(src=vg.SRC_CONV32, img=vg.ptr(Y), H=4, W=4, C=8, K=72, Ho=4, Wo=4)
+    with pytest.raises(vg.VgemmError, match="conv source"):
+        vg.k_gemm_hl2(A2, 64, 16, w, c.Kp, 64, 64, c.Kp, cst, E)
+    E.epi = vg.EPI_QKV
+    with pytest.raises(vg.VgemmError, match="EPI_QKV"):
+        vg.k_gemm_hl2(A, 64, 64, w, c.Kp, 64, 64, c.Kp, cst, E)

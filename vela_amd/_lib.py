@@ -1,0 +1,121 @@
+"""Loader for the in-tree libvgemm.so (the HIP kernels behind the C ABI of include/vgemm.h).
+
+torch is imported first so that the HIP runtime torch ships (SONAME libamdhip64.so.7) is the one
+libvgemm.so binds to: device pointers and streams from torch are then valid in the library. There is
+no fallback: if the library is missing or does not load, every call raises.
+"""
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+import torch  # noqa: F401  (must precede the dlopen below)
+
+LIB_PATH = Path(__file__).resolve().parent / "libvgemm.so"
+
+P = ctypes.c_void_p
+I = ctypes.c_int
+LL = ctypes.c_longlong
+SZ = ctypes.c_size_t
+U32 = ctypes.c_uint32
+
+
+class ASrc(ctypes.Structure):
+    """VgemmASrc (include/vgemm.h) == meow::ASrc (src/gemm_hl.h:12-17) plus the int16 sources."""
+
+    _fields_ = [
+        ("src", I),
+        ("hi", P), ("lo", P), ("ld8", I), ("e", P),
+        ("x", P), ("ldx", I), ("rowmax", P), ("K", I),
+        ("img", P), ("H", I), ("W", I), ("C", I), ("stride", I), ("Ho", I), ("Wo", I),
+        ("q16", P), ("ld16", I),
+        ("img16", P),
+    ]
+
+    def __init__(self, **kw):
+        super().__init__()
+        self.src = 0
+        self.stride = 1
+        for k, v in kw.items():
+            setattr(self, k, v)
+
+
+class AEpi(ctypes.Structure):
+    """VgemmAEpi (include/vgemm.h) == meow::AEpi (src/gemm_hl.h:18-26) plus the split-K workspace."""
+
+    _fields_ = [
+        ("epi", I), ("Y", P), ("ldy", I), ("residual", P),
+        ("Cs", I), ("Y1", P), ("Y2", P), ("Lphi", P),
+        ("rowmax", P),
+        ("gnstat", P), ("gnT", I),
+        ("heads", I), ("T", I), ("TpQ", I), ("TpK", I), ("C", I),
+        ("qhi", P), ("qlo", P), ("khi", P), ("klo", P), ("qe", P), ("ke", P),
+        ("qhs", P), ("qls", P), ("qts", P), ("khs", P), ("kls", P), ("kts", P),
+        ("ws", P), ("ws_bytes", SZ),
+    ]
+
+    def __init__(self, **kw):
+        super().__init__()
+        for k, v in kw.items():
+            setattr(self, k, v)
+
+
+# (name, restype, argtypes) of every entry point declared in include/vgemm.h
+SIGNATURES = [
+    ("vgemm_asrc_init", None, [ctypes.POINTER(ASrc)]),
+    ("vgemm_aepi_init", None, [ctypes.POINTER(AEpi)]),
+    ("vgemm_hl2", I, [P, ctypes.POINTER(ASrc), I, I, P, I, I, I, I, P, ctypes.POINTER(AEpi)]),
+    ("vgemm_hl", I, [P, P, P, I, I, I, P, I, I, I, I, P, P, P, I, P, I, I, P, P, P]),
+    ("vgemm_conv_e", I, [P, P, I, I, I, I, P]),
+    ("vgemm_supported", I, [I, I, I]),
+    ("vgemm_set_variant", None, [I]),
+    ("vgemm_get_variant", I, []),
+    ("vgemm_set_splitk", None, [I]),
+    ("vgemm_workspace_bytes", SZ, [I, I, I, I, I, I]),
+    ("vgemm_i8_create", I, [SZ, ctypes.POINTER(P)]),
+    ("vgemm_i8_destroy", I, [P]),
+    ("vgemm_i8_run", I, [P, P, P, I, LL, P, I, LL, P, I, LL, I, I, I, I]),
+    ("vgemm_quant_rows", I, [P, P, I, I, I, P, P, P, I]),
+    ("vgemm_epilogue", I, [P, P, P, I, I, I, P, P, P, I, P]),
+    ("vgemm_pixmax", I, [P, P, I, I, P]),
+    ("vgemm_im2col3", I, [P, P, P, I, I, I, I, I, P, P, P, I]),
+    ("vgemm_epilogue_split", I, [P, P, P, I, I, I, P, P, I, P, P, P]),
+    ("vgemm_epilogue_geglu_q", I, [P, P, P, I, I, I, P, P, P, P, P, P, I]),
+    ("vgemm_graph_begin", I, [P]),
+    ("vgemm_graph_end", I, [P, ctypes.POINTER(P)]),
+    ("vgemm_graph_launch", I, [P, P]),
+    ("vgemm_graph_destroy", I, [P]),
+    ("vgemm_fill_u32", I, [P, P, SZ, U32]),
+    ("vgemm_last_error", ctypes.c_char_p, []),
+    ("vgemm_version", ctypes.c_char_p, []),
+]
+
+_lib = None
+
+
+def load() -> ctypes.CDLL:
+    """Load libvgemm.so (once) and set every prototype; raise if it is not built."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(f"{LIB_PATH} is not built: run `python -m vela_amd.build` (there is no fallback path)")
+        lib = ctypes.CDLL(str(LIB_PATH))
+        for name, res, args in SIGNATURES:
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+    return _lib
+
+
+class VgemmError(RuntimeError):
+    """A non-zero vgemm return code (the reference throws std::runtime_error at these points)."""
+
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"vgemm error {code}: {msg}")
+        self.code = code
+
+
+def check(rc: int) -> None:
+    if rc != 0:
+        raise VgemmError(rc, load().vgemm_last_error().decode())

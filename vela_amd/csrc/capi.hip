@@ -1,0 +1,398 @@
+// C ABI of libvgemm.so (include/vgemm.h): argument checks, tile/split-K selection and dispatch.
+// Shape checks and messages follow the reference (src/gemm_hl.cu:344-370, src/gemm.cu:41,
+// src/kernels.cu:733); a failed check returns VGEMM_ERR_ARG where the reference throws.
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "../../include/vgemm.h"
+#include "vk_common.h"
+
+namespace vk {
+hipError_t launch_gemm_i8(int variant, int epi, const GemmParams& p, int batch, hipStream_t st);
+hipError_t launch_gemm_x32(int variant, int epi, const GemmParams& p, int batch, hipStream_t st);
+hipError_t launch_gemm_conv32(int variant, int epi, const GemmParams& p, int batch, hipStream_t st);
+hipError_t launch_gemm_i16(int variant, int epi, const GemmParams& p, int batch, hipStream_t st);
+hipError_t launch_gemm_conv16(int variant, int epi, const GemmParams& p, int batch, hipStream_t st);
+hipError_t launch_gemm_raw(int variant, const GemmParams& p, int batch, hipStream_t st);
+hipError_t launch_splitk_epilogue(int epi, const GemmParams& p, hipStream_t st);
+hipError_t launch_quant_rows(hipStream_t st, const int32_t* X, int M, int K, int ldx, int8_t* hi, int8_t* lo, int32_t* e, int Kp);
+hipError_t launch_pixmax(hipStream_t st, const int32_t* X, int rows, int C, uint32_t* pm);
+hipError_t launch_conv_e(hipStream_t st, const uint32_t* pm, int B, int H, int W, int stride, int32_t* e);
+hipError_t launch_im2col3(hipStream_t st, const int32_t* X, const uint32_t* pm, int B, int H, int W, int C, int stride, int8_t* hi, int8_t* lo,
+                          int32_t* e, int Kp);
+hipError_t launch_epilogue(hipStream_t st, const int32_t* Chi, const int32_t* Clo, int M, int N, int ldc, const int4* cst, const int32_t* e,
+                           int32_t* Y, int ldy, const int32_t* R);
+hipError_t launch_epilogue_split(hipStream_t st, const int32_t* Chi, const int32_t* Clo, int M, int N, int ldc, const int4* cst,
+                                 const int32_t* e, int Cs, int32_t* Y0, int32_t* Y1, int32_t* Y2);
+hipError_t launch_epilogue_geglu_q(hipStream_t st, const int32_t* Chi, const int32_t* Clo, int M, int F, int ldc, const int4* cst,
+                                   const int32_t* e, const int32_t* L, int8_t* hi, int8_t* lo, int32_t* eo, int Kp);
+hipError_t launch_fill_u32(hipStream_t st, uint32_t* p, size_t n, uint32_t value);
+}  // namespace vk
+
+namespace {
+
+thread_local std::string g_err;
+int g_variant = -1;   // meow::g_gemm_hl_variant: process-wide, written by tests only
+int g_splitk = 0;
+
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+int ok() {
+    g_err.clear();
+    return VGEMM_OK;
+}
+
+int hip_status(hipError_t e, const char* what) {
+    if (e != hipSuccess) return fail(VGEMM_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+    return ok();
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// Byte extent a buffer load may touch; the kernels address operands with 32-bit offsets and use
+// offset 2^31 as the "outside" marker, so every extent must stay below 2^31.
+constexpr long long MAX_EXTENT = (1LL << 31) - 64;
+
+struct Tiles { int BM, BN; };
+constexpr Tiles TILES[3] = {{128, 128}, {64, 128}, {128, 64}};
+constexpr int NCU = 256;   // MI355X compute units
+
+int cdiv(long long a, long long b) { return int((a + b - 1) / b); }
+
+// Tile variant: fewest rounds of the 256 CUs weighted by tile area (one 128x128 block per CU,
+// two of the half-size tiles).
+int pick_variant(int M, int N) {
+    int best = 0;
+    double bestCost = 1e300;
+    for (int v = 0; v < 3; ++v) {
+        const long long tiles = (long long)cdiv(M, TILES[v].BM) * cdiv(N, TILES[v].BN);
+        const int slots = v == 0 ? NCU : 2 * NCU;
+        const double rounds = double((tiles + slots - 1) / slots);
+        const double cost = rounds * TILES[v].BM * TILES[v].BN / (v == 0 ? 1.0 : 2.0);
+        if (cost < bestCost - 1e-9) { bestCost = cost; best = v; }
+    }
+    return best;
+}
+
+// Split-K partitions: only for deep K whose tile count leaves CUs idle.
+int pick_splitk(int variant, int M, int N, int Kp) {
+    const int nK = (Kp + 63) / 64;
+    const long long tiles = (long long)cdiv(M, TILES[variant].BM) * cdiv(N, TILES[variant].BN);
+    if (g_splitk > 0) return g_splitk < nK ? g_splitk : nK;
+    if (nK < 16 || tiles >= NCU) return 1;
+    int s = int((NCU + tiles - 1) / tiles);
+    if (s > nK / 8) s = nK / 8;
+    return s < 1 ? 1 : s;
+}
+
+size_t ws_bytes_for(int variant, int M, int N, int splits) {
+    if (splits <= 1) return 0;
+    const size_t rows = size_t(cdiv(M, TILES[variant].BM)) * TILES[variant].BM;
+    const size_t cols = size_t(cdiv(N, TILES[variant].BN)) * TILES[variant].BN;
+    return size_t(splits) * 2 * rows * cols * 4;
+}
+
+int launch_src(int src, int variant, int epi, const vk::GemmParams& p, hipStream_t st) {
+    hipError_t e;
+    switch (src) {
+    case VGEMM_SRC_I8: e = vk::launch_gemm_i8(variant, epi, p, 1, st); break;
+    case VGEMM_SRC_X32: e = vk::launch_gemm_x32(variant, epi, p, 1, st); break;
+    case VGEMM_SRC_CONV32: e = vk::launch_gemm_conv32(variant, epi, p, 1, st); break;
+    case VGEMM_SRC_I16: e = vk::launch_gemm_i16(variant, epi, p, 1, st); break;
+    case VGEMM_SRC_CONV16: e = vk::launch_gemm_conv16(variant, epi, p, 1, st); break;
+    default: return fail(VGEMM_ERR_ARG, "gemm_hl: unknown A source %d", src);
+    }
+    return hip_status(e, "gemm_hl launch");
+}
+
+}  // namespace
+
+extern "C" {
+
+void vgemm_asrc_init(VgemmASrc* a) {
+    std::memset(a, 0, sizeof *a);
+    a->src = VGEMM_SRC_I8;
+    a->stride = 1;
+}
+
+void vgemm_aepi_init(VgemmAEpi* e) {
+    std::memset(e, 0, sizeof *e);
+    e->epi = VGEMM_EPI_PLAIN;
+}
+
+int vgemm_supported(int Mp, int Np, int Kp) { return Mp > 0 && Np > 0 && Kp > 0 && Mp % 64 == 0 && Np % 64 == 0 && Kp % 16 == 0; }
+
+void vgemm_set_variant(int v) { g_variant = v; }
+int vgemm_get_variant(void) { return g_variant; }
+void vgemm_set_splitk(int s) { g_splitk = s < 0 ? 0 : s; }
+
+size_t vgemm_workspace_bytes(int Mp, int Mreal, int Np, int Nreal, int Kp, int epi) {
+    (void)Mp; (void)Np; (void)epi;
+    int v = g_variant >= 0 && g_variant < 3 ? g_variant : pick_variant(Mreal, Nreal);
+    return ws_bytes_for(v, Mreal, Nreal, pick_splitk(v, Mreal, Nreal, Kp));
+}
+
+int vgemm_hl2(void* stream, const VgemmASrc* A, int Mp, int Mreal, const int8_t* W, int ldw, int Np, int Nreal, int Kp,
+              const int32_t* cst, const VgemmAEpi* E) {
+    if (!A || !E) return fail(VGEMM_ERR_ARG, "gemm_hl: null ASrc/AEpi");
+    if (!vgemm_supported(Mp, Np, Kp)) return fail(VGEMM_ERR_ARG, "gemm_hl: unsupported shape (Mp %d, Np %d, Kp %d)", Mp, Np, Kp);
+    if (Mreal < 0 || Mreal > Mp || Nreal < 0 || Nreal > Np) return fail(VGEMM_ERR_ARG, "gemm_hl: Mreal/Nreal outside Mp/Np");
+    if (!W || !cst || ldw < Kp || ldw % 16 || !aligned16(W)) return fail(VGEMM_ERR_ARG, "gemm_hl: W must be 16-byte aligned with ldw >= Kp, ldw %% 16 == 0");
+    if (E->epi == VGEMM_EPI_QKV) return fail(VGEMM_ERR_UNSUPPORTED, "gemm_hl: EPI_QKV is not implemented");
+    if (E->gnstat) return fail(VGEMM_ERR_UNSUPPORTED, "gemm_hl: GroupNorm statistics are not implemented");
+    if (E->epi < 0 || E->epi > VGEMM_EPI_GELU) return fail(VGEMM_ERR_ARG, "gemm_hl: unknown epilogue %d", E->epi);
+    if (!E->Y) return fail(VGEMM_ERR_ARG, "gemm_hl: null Y");
+    if (Mreal == 0 || Nreal == 0) return ok();
+
+    vk::GemmParams p;
+    std::memset(&p, 0, sizeof p);
+    p.Mreal = Mreal; p.Nreal = Nreal; p.Kp = Kp;
+    p.w = W; p.ldw = ldw; p.cst = reinterpret_cast<const int4*>(cst);
+    const long long wext = (long long)(Nreal - 1) * ldw + Kp;
+    if (wext > MAX_EXTENT) return fail(VGEMM_ERR_UNSUPPORTED, "gemm_hl: W larger than 2 GiB");
+    p.w_bytes = unsigned(wext);
+    p.e = A->e;
+    p.stride = 1;
+
+    long long aext = 0;
+    switch (A->src) {
+    case VGEMM_SRC_I8:
+        if (!A->hi || !A->lo || A->ld8 < Kp || A->ld8 % 16 || !aligned16(A->hi) || !aligned16(A->lo))
+            return fail(VGEMM_ERR_ARG, "gemm_hl: SRC_I8 planes must be 16-byte aligned with ld8 >= Kp, ld8 %% 16 == 0");
+        p.a0 = A->hi; p.a1 = A->lo; p.lda = A->ld8;
+        aext = (long long)(Mreal - 1) * A->ld8 + Kp;
+        p.a1_bytes = unsigned(aext > MAX_EXTENT ? 0 : aext);
+        break;
+    case VGEMM_SRC_I16:
+        if (!A->q16 || A->K <= 0 || A->K > Kp || A->K % 8 || A->ld16 < A->K || A->ld16 % 8 || !aligned16(A->q16))
+            return fail(VGEMM_ERR_ARG, "gemm_hl: SRC_I16 needs K %% 8 == 0, K <= Kp, ld16 >= K, ld16 %% 8 == 0, 16-byte alignment");
+        p.a0 = A->q16; p.lda = A->ld16; p.K = A->K;
+        aext = ((long long)(Mreal - 1) * A->ld16 + A->K) * 2;
+        break;
+    case VGEMM_SRC_X32:
+        if (!A->x || !A->rowmax || A->K <= 0 || A->K > Kp || A->K % 4 || A->ldx < A->K || A->ldx % 4 || !aligned16(A->x))
+            return fail(VGEMM_ERR_ARG, "gemm_hl: SRC_X32 needs x, rowmax, K %% 4 == 0, K <= Kp, ldx >= K, ldx %% 4 == 0, 16-byte alignment");
+        p.a0 = A->x; p.lda = A->ldx; p.K = A->K; p.xrowmax = A->rowmax; p.e = nullptr;
+        aext = ((long long)(Mreal - 1) * A->ldx + A->K) * 4;
+        break;
+    case VGEMM_SRC_CONV32:
+    case VGEMM_SRC_CONV16: {
+        const void* img = A->src == VGEMM_SRC_CONV32 ? static_cast<const void*>(A->img) : static_cast<const void*>(A->img16);
+        if (!img || !aligned16(img)) return fail(VGEMM_ERR_ARG, "gemm_hl conv source: null or unaligned image");
+        if (A->C <= 0 || A->C % 16 || A->K != 9 * A->C) return fail(VGEMM_ERR_ARG, "gemm_hl conv source: C %% 16 or K");
+        if (A->K > Kp || A->H <= 0 || A->W <= 0 || A->stride <= 0) return fail(VGEMM_ERR_ARG, "gemm_hl conv source: H/W/stride/Kp");
+        const int Ho = (A->H - 1) / A->stride + 1, Wo = (A->W - 1) / A->stride + 1;
+        if (A->Ho != Ho || A->Wo != Wo) return fail(VGEMM_ERR_ARG, "gemm_hl conv source: Ho/Wo must be (H-1)/stride+1, (W-1)/stride+1");
+        const long long B = (Mreal + (long long)Ho * Wo - 1) / ((long long)Ho * Wo);
+        p.a0 = img; p.K = A->K; p.H = A->H; p.W = A->W; p.C = A->C; p.stride = A->stride; p.Ho = Ho; p.Wo = Wo;
+        aext = B * A->H * A->W * (long long)A->C * (A->src == VGEMM_SRC_CONV32 ? 4 : 2);
+        break;
+    }
+    default:
+        return fail(VGEMM_ERR_ARG, "gemm_hl: unknown A source %d", A->src);
+    }
+    if (aext > MAX_EXTENT) return fail(VGEMM_ERR_UNSUPPORTED, "gemm_hl: A operand larger than 2 GiB");
+    p.a0_bytes = unsigned(aext);
+
+    const int epi = E->epi;
+    p.Y = E->Y; p.ldy = E->ldy; p.R = E->residual; p.Lphi = E->Lphi; p.rowmax = E->rowmax;
+    p.Cs = E->Cs; p.Y1 = E->Y1; p.Y2 = E->Y2;
+    bool vec = aligned16(E->Y);
+    switch (epi) {
+    case VGEMM_EPI_PLAIN:
+    case VGEMM_EPI_GELU:
+        if (E->ldy < Nreal) return fail(VGEMM_ERR_ARG, "gemm_hl: ldy < Nreal");
+        if (epi == VGEMM_EPI_GELU && !E->Lphi) return fail(VGEMM_ERR_ARG, "gemm_hl: EPI_GELU needs Lphi");
+        vec = vec && E->ldy % 4 == 0 && (!E->residual || aligned16(E->residual));
+        break;
+    case VGEMM_EPI_GEGLU:
+        if (Nreal % 2) return fail(VGEMM_ERR_ARG, "gemm_hl: EPI_GEGLU needs an even Nreal (interleaved a/g columns)");
+        if (!E->Lphi) return fail(VGEMM_ERR_ARG, "gemm_hl: EPI_GEGLU needs Lphi");
+        if (E->ldy < Nreal / 2) return fail(VGEMM_ERR_ARG, "gemm_hl: ldy < Nreal/2");
+        if (E->residual) return fail(VGEMM_ERR_ARG, "gemm_hl: EPI_GEGLU takes no residual");
+        vec = vec && E->ldy % 4 == 0;
+        break;
+    case VGEMM_EPI_SPLIT3:
+        if (E->Cs <= 0 || E->Cs % 4 || Nreal > 3 * E->Cs) return fail(VGEMM_ERR_ARG, "gemm_hl: EPI_SPLIT3 needs Cs %% 4 == 0 and Nreal <= 3*Cs");
+        if ((Nreal > E->Cs && !E->Y1) || (Nreal > 2 * E->Cs && !E->Y2)) return fail(VGEMM_ERR_ARG, "gemm_hl: EPI_SPLIT3 needs Y1/Y2");
+        if (E->rowmax || E->residual) return fail(VGEMM_ERR_ARG, "gemm_hl: EPI_SPLIT3 takes no residual or rowmax");
+        vec = vec && (!E->Y1 || aligned16(E->Y1)) && (!E->Y2 || aligned16(E->Y2));
+        break;
+    }
+    p.vec_store = vec ? 1 : 0;
+
+    int variant = g_variant >= 0 && g_variant < 3 ? g_variant : pick_variant(Mreal, Nreal);
+    const int BM = TILES[variant].BM, BN = TILES[variant].BN;
+    p.mtiles = cdiv(Mreal, BM);
+    p.ntiles = cdiv(Nreal, BN);
+    const int nK = (Kp + 63) / 64;
+    int splits = E->ws ? pick_splitk(variant, Mreal, Nreal, Kp) : 1;
+    if (splits > 1 && ws_bytes_for(variant, Mreal, Nreal, splits) > E->ws_bytes) splits = 1;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (splits <= 1) {
+        p.ksplit = 1; p.kper = nK;
+        return launch_src(A->src, variant, epi, p, st);
+    }
+    if (!aligned16(E->ws)) return fail(VGEMM_ERR_ARG, "gemm_hl: workspace must be 16-byte aligned");
+    p.ksplit = splits;
+    p.kper = (nK + splits - 1) / splits;
+    p.ksplit = (nK + p.kper - 1) / p.kper;
+    p.ws = static_cast<int32_t*>(E->ws);
+    p.ws_rows = p.mtiles * BM;
+    p.ws_ld = p.ntiles * BN;
+    const int rc = launch_src(A->src, variant, vk::EPI_PARTIAL, p, st);
+    if (rc) return rc;
+    return hip_status(vk::launch_splitk_epilogue(epi, p, st), "gemm_hl split-K epilogue");
+}
+
+int vgemm_hl(void* stream, const int8_t* Ahi, const int8_t* Alo, int lda, int Mp, int Mreal, const int8_t* W, int ldw, int Np, int Nreal,
+             int Kp, const int32_t* cst, const int32_t* e, int32_t* Y, int ldy, const int32_t* residual, int epi, int Cs, int32_t* Y1,
+             int32_t* Y2, const int32_t* Lphi) {
+    VgemmASrc A;
+    vgemm_asrc_init(&A);
+    A.src = VGEMM_SRC_I8; A.hi = Ahi; A.lo = Alo; A.ld8 = lda; A.e = e;
+    VgemmAEpi E;
+    vgemm_aepi_init(&E);
+    E.epi = epi; E.Y = Y; E.ldy = ldy; E.residual = residual; E.Cs = Cs; E.Y1 = Y1; E.Y2 = Y2; E.Lphi = Lphi;
+    return vgemm_hl2(stream, &A, Mp, Mreal, W, ldw, Np, Nreal, Kp, cst, &E);
+}
+
+int vgemm_conv_e(void* stream, const uint32_t* pm, int B, int H, int W, int stride, int32_t* e) {
+    if (!pm || !e || B <= 0 || H <= 0 || W <= 0 || stride <= 0) return fail(VGEMM_ERR_ARG, "conv_e: bad arguments");
+    return hip_status(vk::launch_conv_e(static_cast<hipStream_t>(stream), pm, B, H, W, stride, e), "conv_e launch");
+}
+
+// ---- meow::Gemm replacement
+struct VgemmI8Handle { size_t ws; };
+
+int vgemm_i8_create(size_t ws_bytes, void** handle) {
+    if (!handle) return fail(VGEMM_ERR_ARG, "i8gemm: null handle pointer");
+    *handle = new VgemmI8Handle{ws_bytes};
+    return ok();
+}
+
+int vgemm_i8_destroy(void* handle) {
+    delete static_cast<VgemmI8Handle*>(handle);
+    return ok();
+}
+
+int vgemm_i8_run(void* handle, void* stream, const int8_t* A, int lda, long long strideA, const int8_t* W, int ldw, long long strideW,
+                 int32_t* C, int ldc, long long strideC, int M, int N, int K, int batch) {
+    if (!handle) return fail(VGEMM_ERR_ARG, "i8gemm: null handle");
+    if (!A || !W || !C) return fail(VGEMM_ERR_ARG, "i8gemm: null pointer");
+    if (M <= 0 || N <= 0 || K <= 0 || batch <= 0) return fail(VGEMM_ERR_ARG, "i8gemm: no int8 GEMM for M=%d N=%d K=%d batch=%d", M, N, K, batch);
+    if (K % 16 || N % 4) return fail(VGEMM_ERR_ARG, "i8gemm: K %% 16 == 0 and N %% 4 == 0 required (M=%d N=%d K=%d)", M, N, K);
+    if (lda < K || ldw < K || ldc < N || lda % 16 || ldw % 16 || !aligned16(A) || !aligned16(W) || !aligned16(C))
+        return fail(VGEMM_ERR_ARG, "i8gemm: leading dimensions must cover K/N, be multiples of 16 bytes, pointers 16-byte aligned");
+    if (batch > 1 && (strideA % 16 || strideW % 16 || strideC % 4)) return fail(VGEMM_ERR_ARG, "i8gemm: batch strides must keep 16-byte alignment");
+    const long long aext = (long long)(M - 1) * lda + K, wext = (long long)(N - 1) * ldw + K;
+    if (aext > MAX_EXTENT || wext > MAX_EXTENT) return fail(VGEMM_ERR_UNSUPPORTED, "i8gemm: operand larger than 2 GiB");
+    if (batch > 65535) return fail(VGEMM_ERR_UNSUPPORTED, "i8gemm: batch > 65535");
+    vk::GemmParams p;
+    std::memset(&p, 0, sizeof p);
+    p.a0 = A; p.a0_bytes = unsigned(aext); p.lda = lda;
+    p.w = W; p.w_bytes = unsigned(wext); p.ldw = ldw;
+    p.Y = C; p.ldy = ldc; p.vec_store = ldc % 4 == 0 ? 1 : 0;
+    p.Mreal = M; p.Nreal = N; p.Kp = K; p.K = K;
+    p.sA = strideA; p.sW = strideW; p.sC = strideC;
+    const int variant = g_variant >= 0 && g_variant < 3 ? g_variant : pick_variant(M, N);
+    p.mtiles = cdiv(M, TILES[variant].BM);
+    p.ntiles = cdiv(N, TILES[variant].BN);
+    p.ksplit = 1; p.kper = (K + 63) / 64;
+    p.stride = 1;
+    return hip_status(vk::launch_gemm_raw(variant, p, batch, static_cast<hipStream_t>(stream)), "i8gemm launch");
+}
+
+// ---- producers
+int vgemm_quant_rows(void* stream, const int32_t* X, int M, int K, int ldx, int8_t* hi, int8_t* lo, int32_t* e, int Kp) {
+    if (!X || !hi || !lo || !e || M <= 0 || K <= 0 || Kp < K || Kp % 4 || ldx < K) return fail(VGEMM_ERR_ARG, "quant_rows: bad arguments");
+    return hip_status(vk::launch_quant_rows(static_cast<hipStream_t>(stream), X, M, K, ldx, hi, lo, e, Kp), "quant_rows launch");
+}
+
+int vgemm_epilogue(void* stream, const int32_t* Chi, const int32_t* Clo, int M, int N, int ldc, const int32_t* cst, const int32_t* e, int32_t* Y,
+                   int ldy, const int32_t* residual) {
+    if (N % 4 || ldc % 4 || ldy % 4) return fail(VGEMM_ERR_ARG, "epilogue: N/ld must be multiples of 4");
+    if (!Chi || !Clo || !cst || !e || !Y || M <= 0 || N <= 0) return fail(VGEMM_ERR_ARG, "epilogue: bad arguments");
+    if (!aligned16(Chi) || !aligned16(Clo) || !aligned16(Y) || (residual && !aligned16(residual))) return fail(VGEMM_ERR_ARG, "epilogue: pointers must be 16-byte aligned");
+    return hip_status(vk::launch_epilogue(static_cast<hipStream_t>(stream), Chi, Clo, M, N, ldc, reinterpret_cast<const int4*>(cst), e, Y, ldy, residual),
+                      "epilogue launch");
+}
+
+int vgemm_pixmax(void* stream, const int32_t* X, int rows, int C, uint32_t* pm) {
+    if (!X || !pm || rows <= 0 || C <= 0) return fail(VGEMM_ERR_ARG, "pixmax: bad arguments");
+    return hip_status(vk::launch_pixmax(static_cast<hipStream_t>(stream), X, rows, C, pm), "pixmax launch");
+}
+
+int vgemm_im2col3(void* stream, const int32_t* X, const uint32_t* pm, int B, int H, int W, int C, int stride, int8_t* hi, int8_t* lo, int32_t* e,
+                  int Kp) {
+    if (!X || !pm || !hi || !lo || !e || B <= 0 || H <= 0 || W <= 0 || stride <= 0) return fail(VGEMM_ERR_ARG, "im2col3: bad arguments");
+    if (C <= 0 || C % 4 || Kp < 9 * C || Kp % 4 || !aligned16(X)) return fail(VGEMM_ERR_ARG, "im2col3: C %% 4 == 0, Kp >= 9C, Kp %% 4 == 0, aligned X required");
+    return hip_status(vk::launch_im2col3(static_cast<hipStream_t>(stream), X, pm, B, H, W, C, stride, hi, lo, e, Kp), "im2col3 launch");
+}
+
+int vgemm_epilogue_split(void* stream, const int32_t* Chi, const int32_t* Clo, int M, int N, int ldc, const int32_t* cst, const int32_t* e, int Cs,
+                         int32_t* Y0, int32_t* Y1, int32_t* Y2) {
+    if (!Chi || !Clo || !cst || !e || !Y0 || M <= 0 || N <= 0 || Cs <= 0 || N > 3 * Cs || (N > Cs && !Y1) || (N > 2 * Cs && !Y2))
+        return fail(VGEMM_ERR_ARG, "epilogue_split: bad arguments");
+    return hip_status(vk::launch_epilogue_split(static_cast<hipStream_t>(stream), Chi, Clo, M, N, ldc, reinterpret_cast<const int4*>(cst), e, Cs, Y0, Y1, Y2),
+                      "epilogue_split launch");
+}
+
+int vgemm_epilogue_geglu_q(void* stream, const int32_t* Chi, const int32_t* Clo, int M, int F, int ldc, const int32_t* cst, const int32_t* e,
+                           const int32_t* Lphi, int8_t* hi, int8_t* lo, int32_t* eo, int Kp) {
+    if (!Chi || !Clo || !cst || !e || !Lphi || !hi || !lo || !eo || M <= 0 || F <= 0 || Kp < F) return fail(VGEMM_ERR_ARG, "epilogue_geglu_q: bad arguments");
+    if (F > 5120) return fail(VGEMM_ERR_ARG, "epilogue_geglu_q: F too large");
+    return hip_status(vk::launch_epilogue_geglu_q(static_cast<hipStream_t>(stream), Chi, Clo, M, F, ldc, reinterpret_cast<const int4*>(cst), e, Lphi, hi, lo,
+                                                  eo, Kp),
+                      "epilogue_geglu_q launch");
+}
+
+// ---- graphs
+int vgemm_graph_begin(void* stream) {
+    if (!stream) return fail(VGEMM_ERR_ARG, "graph_begin: the null stream cannot be captured");
+    return hip_status(hipStreamBeginCapture(static_cast<hipStream_t>(stream), hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+}
+
+int vgemm_graph_end(void* stream, void** exec) {
+    if (!stream || !exec) return fail(VGEMM_ERR_ARG, "graph_end: bad arguments");
+    hipGraph_t g = nullptr;
+    hipError_t e = hipStreamEndCapture(static_cast<hipStream_t>(stream), &g);
+    if (e != hipSuccess) return hip_status(e, "hipStreamEndCapture");
+    hipGraphExec_t x = nullptr;
+    e = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e != hipSuccess) return hip_status(e, "hipGraphInstantiate");
+    *exec = x;
+    return ok();
+}
+
+int vgemm_graph_launch(void* exec, void* stream) {
+    if (!exec) return fail(VGEMM_ERR_ARG, "graph_launch: null graph");
+    return hip_status(hipGraphLaunch(static_cast<hipGraphExec_t>(exec), static_cast<hipStream_t>(stream)), "hipGraphLaunch");
+}
+
+int vgemm_graph_destroy(void* exec) {
+    if (!exec) return ok();
+    return hip_status(hipGraphExecDestroy(static_cast<hipGraphExec_t>(exec)), "hipGraphExecDestroy");
+}
+
+int vgemm_fill_u32(void* stream, uint32_t* p, size_t count, uint32_t value) {
+    if (!p && count) return fail(VGEMM_ERR_ARG, "fill_u32: null pointer");
+    if (!count) return ok();
+    return hip_status(vk::launch_fill_u32(static_cast<hipStream_t>(stream), p, count, value), "fill_u32 launch");
+}
+
+const char* vgemm_last_error(void) { return g_err.c_str(); }
+const char* vgemm_version(void) { return "vgemm 0.1 gfx950"; }
+
+}  // extern "C"

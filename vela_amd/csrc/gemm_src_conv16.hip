@@ -1,0 +1,8 @@
+// Instantiations of the hi/lo GEMM kernel for the SRC_CONV16 source (all epilogues and tile variants).
+#include "gemm_kernel.h"
+
+namespace vk {
+hipError_t launch_gemm_conv16(int variant, int epi, const GemmParams& p, int batch, hipStream_t st) {
+    return launch_gemm_src<SRC_CONV16>(variant, epi, p, batch, st);
+}
+}  // namespace vk

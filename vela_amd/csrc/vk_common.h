@@ -1,0 +1,128 @@
+// Device-side helpers shared by the vgemm kernels: exact integer primitives (restating
+// src/intops.cuh:9-66 of the reference), buffer-resource loads and the parameter block.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace vk {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef short s2 __attribute__((ext_vector_type(2)));
+typedef long long i64;
+typedef unsigned long long u64;
+
+enum { SRC_I8 = 0, SRC_X32 = 1, SRC_CONV32 = 2, SRC_I16 = 3, SRC_CONV16 = 4 };
+enum { EPI_PLAIN = 0, EPI_SPLIT3 = 1, EPI_GEGLU = 2, EPI_GELU = 3, EPI_PARTIAL = 8, EPI_RAW = 9 };
+
+// A buffer offset that is outside every buffer this library builds (extents are checked < 2^31 on
+// the host): a load from it returns zeros (the hardware range check of raw buffer loads).
+constexpr unsigned OOB = 0x80000000u;
+// Third descriptor word of a raw (untyped) buffer resource on gfx9-family GPUs.
+constexpr int RSRC_WORD3 = 0x00020000;
+
+struct GemmParams {
+    // A operand
+    const void* a0;            // hi plane / q16 / x / img / img16
+    const void* a1;            // lo plane (SRC_I8)
+    unsigned a0_bytes, a1_bytes;
+    int lda;                   // row stride in elements (ld8 / ld16 / ldx)
+    const int32_t* e;          // per-row shift (SRC_I8, SRC_I16, SRC_CONV*); may be null
+    const uint32_t* xrowmax;   // SRC_X32
+    int K;                     // real K of the source (X32 / I16 / CONV)
+    int H, W, C, stride, Ho, Wo;
+    // weights
+    const int8_t* w; unsigned w_bytes; int ldw;
+    int Mreal, Nreal, Kp;
+    const int4* cst;
+    // epilogue
+    int32_t* Y; int ldy; const int32_t* R;
+    int Cs; int32_t* Y1; int32_t* Y2;
+    const int32_t* Lphi; uint32_t* rowmax;
+    int vec_store;             // output rows/pointers allow 16-byte stores
+    // split-K partials: ws[(split * 2 + plane) * ws_rows + row][col], row stride ws_ld
+    int ksplit, kper;
+    int32_t* ws; int ws_rows, ws_ld;
+    // tiling
+    int mtiles, ntiles;
+    // strided batch (EPI_RAW)
+    long long sA, sW, sC;
+};
+
+// ---------------------------------------------------------------- exact integer primitives
+
+__device__ __forceinline__ i64 sat32(i64 v) { return v < -2147483648LL ? -2147483648LL : (v > 2147483647LL ? 2147483647LL : v); }
+
+// rshr: rounding right shift for s >= 0, saturating left shift for s < 0, result saturated to int32
+// (src/intops.cuh:11-17). The rounding add wraps in 64 bits.
+__device__ __forceinline__ i64 rshr(i64 v, i64 s) {
+    if (s >= 0) {
+        const int p = s > 62 ? 62 : int(s);
+        const i64 t = i64(u64(v) + u64((1LL << p) >> 1));
+        return sat32(t >> p);
+    }
+    const int neg = -s > 31 ? 31 : int(-s);
+    const i64 lim = 1LL << (62 - neg);
+    const i64 r = v < -lim ? -lim : (v > lim ? lim : v);
+    return sat32(r * (1LL << neg));
+}
+
+// e = max(0, bitlen(m) - 15) (src/intops.cuh:37-38 for m < 2^32)
+__device__ __forceinline__ int rowexp_u32(uint32_t m) { return m ? max(0, 32 - __clz(m) - 15) : 0; }
+
+// quant16 of an int32 with e in [0,17] (src/intops.cuh:40-41)
+__device__ __forceinline__ int quant16_32(int v, int e) {
+    const int q = e ? ((v >> e) + ((v >> (e - 1)) & 1)) : v;
+    return min(max(q, -32767), 32767);
+}
+
+// Interpolated Q16 table over [-16,16) (src/intops.cuh:42-50); 32-bit arithmetic wraps.
+__device__ __forceinline__ int lut16i(i64 x, const int32_t* __restrict__ L) {
+    const i64 z = x + (16LL << 16);
+    if (z < 0) return 0;
+    if (z >= (32LL << 16)) return 65536;
+    const int i = int(z >> 10), f = int(z & 1023);
+    const int a = L[i], b = L[i + 1];
+    const int prod = int((unsigned(b) - unsigned(a)) * unsigned(f));
+    return int(unsigned(a) + unsigned(prod >> 10));
+}
+
+// The exact epilogue of one element (src/gemm_hl.cu:40-43); acc * m wraps in 64 bits.
+__device__ __forceinline__ int epi1_exact(int chi, int clo, int m, int s, int b, int wsum, int er) {
+    const i64 acc = 256LL * chi + clo + 128LL * wsum;
+    const i64 v = i64(u64(acc) * u64(i64(m)));
+    return int(sat32(rshr(v, i64(s) - er) + b));
+}
+
+__device__ __forceinline__ int geglu_exact(int a, int g, const int32_t* __restrict__ L) {
+    const i64 ge = sat32(rshr(i64(g) * lut16i(g, L), 16));
+    return int(sat32(rshr(i64(a) * ge, 16)));
+}
+
+__device__ __forceinline__ int gelu_exact(int y, const int32_t* __restrict__ L) { return int(sat32(rshr(i64(y) * lut16i(y, L), 16))); }
+
+__device__ __forceinline__ uint32_t uabs(int v) { return v < 0 ? uint32_t(-i64(v)) : uint32_t(v); }
+
+// ---------------------------------------------------------------- fast exact epilogue pieces
+
+// double -> int32 with saturation (v_cvt_i32_f64 clamps out-of-range values; the argument is
+// always an integer-valued double here)
+__device__ __forceinline__ int cvt_sat(double x) {
+    int r;
+    asm volatile("v_cvt_i32_f64 %0, %1" : "=v"(r) : "v"(x));
+    return r;
+}
+
+__device__ __forceinline__ int add_sat(int a, int b) { return __builtin_elementwise_add_sat(a, b); }
+
+// ---------------------------------------------------------------- buffer loads
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, unsigned bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, RSRC_WORD3);
+}
+
+__device__ __forceinline__ v4i bload16(__amdgpu_buffer_rsrc_t r, unsigned off) {
+    return __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+}
+
+}  // namespace vk

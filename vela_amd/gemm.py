@@ -1,0 +1,174 @@
+"""Python mirror of the reference's GEMM call surface over the C ABI of libvgemm.so.
+
+Names, argument order and meaning follow meow:: in src/gemm_hl.h:8-35, src/gemm.h:12-23 and
+src/kernels.h:11-21,68-70 of the reference; a failed shape check raises (VgemmError, a RuntimeError)
+where the reference throws std::runtime_error. Tensor arguments are torch CUDA tensors (or raw device
+addresses as ints, or None for a null pointer); `stream` defaults to torch's current stream.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from ._lib import AEpi, ASrc, VgemmError, check, load
+
+EPI_PLAIN, EPI_SPLIT3, EPI_GEGLU, EPI_GELU, EPI_QKV = 0, 1, 2, 3, 4
+SRC_I8, SRC_X32, SRC_CONV32, SRC_I16, SRC_CONV16 = 0, 1, 2, 3, 4
+
+__all__ = [
+    "ASrc", "AEpi", "VgemmError", "EPI_PLAIN", "EPI_SPLIT3", "EPI_GEGLU", "EPI_GELU", "EPI_QKV",
+    "SRC_I8", "SRC_X32", "SRC_CONV32", "SRC_I16", "SRC_CONV16", "k_gemm_hl2", "k_gemm_hl", "k_conv_e",
+    "gemm_hl_supported", "set_variant", "get_variant", "set_splitk", "workspace_bytes", "Gemm",
+    "k_quant_rows", "k_epilogue", "k_pixmax", "k_im2col3", "k_epilogue_split", "k_epilogue_geglu_q",
+    "fill_u32", "Graph", "ptr", "stream_ptr",
+]
+
+
+def ptr(t) -> int | None:
+    """Device address of a tensor (None/0 -> null)."""
+    if t is None:
+        return None
+    if isinstance(t, int):
+        return t or None
+    if isinstance(t, torch.Tensor):
+        if not t.is_cuda:
+            raise ValueError("vgemm takes device tensors")
+        return t.data_ptr()
+    raise TypeError(f"cannot take a device address of {type(t)}")
+
+
+def stream_ptr(stream=None) -> int | None:
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    if isinstance(stream, int):
+        return stream or None
+    return stream.cuda_stream or None
+
+
+def k_gemm_hl2(A: ASrc, Mp: int, Mreal: int, W, ldw: int, Np: int, Nreal: int, Kp: int, cst, E: AEpi, stream=None) -> None:
+    """meow::k_gemm_hl2 (src/gemm_hl.h:27)."""
+    check(load().vgemm_hl2(stream_ptr(stream), ctypes.byref(A), Mp, Mreal, ptr(W), ldw, Np, Nreal, Kp, ptr(cst), ctypes.byref(E)))
+
+
+def k_gemm_hl(Ahi, Alo, lda: int, Mp: int, Mreal: int, W, ldw: int, Np: int, Nreal: int, Kp: int, cst, e, Y, ldy: int,
+              residual=None, epi: int = EPI_PLAIN, Cs: int = 0, Y1=None, Y2=None, Lphi=None, stream=None) -> None:
+    """meow::k_gemm_hl (src/gemm_hl.h:30-33)."""
+    check(load().vgemm_hl(stream_ptr(stream), ptr(Ahi), ptr(Alo), lda, Mp, Mreal, ptr(W), ldw, Np, Nreal, Kp, ptr(cst), ptr(e),
+                          ptr(Y), ldy, ptr(residual), epi, Cs, ptr(Y1), ptr(Y2), ptr(Lphi)))
+
+
+def k_conv_e(pm, B: int, H: int, W: int, stride: int, e, stream=None) -> None:
+    """meow::k_conv_e (src/gemm_hl.h:29)."""
+    check(load().vgemm_conv_e(stream_ptr(stream), ptr(pm), B, H, W, stride, ptr(e)))
+
+
+def gemm_hl_supported(Mp: int, Np: int, Kp: int) -> bool:
+    """meow::gemm_hl_supported (src/gemm_hl.h:34)."""
+    return bool(load().vgemm_supported(Mp, Np, Kp))
+
+
+def set_variant(v: int) -> None:
+    """Write meow::g_gemm_hl_variant (src/gemm_hl.h:35): -1 auto, 0 128x128, 1 64x128, 2 128x64."""
+    load().vgemm_set_variant(v)
+
+
+def get_variant() -> int:
+    return load().vgemm_get_variant()
+
+
+def set_splitk(s: int) -> None:
+    """Force the split-K partition count for calls with a workspace (0 = automatic)."""
+    load().vgemm_set_splitk(s)
+
+
+def workspace_bytes(Mp: int, Mreal: int, Np: int, Nreal: int, Kp: int, epi: int = EPI_PLAIN) -> int:
+    return int(load().vgemm_workspace_bytes(Mp, Mreal, Np, Nreal, Kp, epi))
+
+
+class Gemm:
+    """meow::Gemm (src/gemm.h:12-23): C[M,N] = A[M,K] * W[N,K]^T, int8 -> int32, strided batch."""
+
+    def __init__(self):
+        self._h = ctypes.c_void_p()
+
+    def init(self, ws_bytes: int = 0) -> None:
+        check(load().vgemm_i8_create(ws_bytes, ctypes.byref(self._h)))
+
+    def run(self, A, lda: int, strideA: int, W, ldw: int, strideW: int, C, ldc: int, strideC: int, M: int, N: int, K: int,
+            batch: int = 1, stream=None) -> None:
+        if not self._h:
+            raise VgemmError(-1, "Gemm::run before init")
+        check(load().vgemm_i8_run(self._h, stream_ptr(stream), ptr(A), lda, strideA, ptr(W), ldw, strideW, ptr(C), ldc, strideC,
+                                  M, N, K, batch))
+
+    def __del__(self):
+        if getattr(self, "_h", None):
+            try:
+                load().vgemm_i8_destroy(self._h)
+            except Exception:
+                pass
+
+
+def k_quant_rows(X, M: int, K: int, ldx: int, hi, lo, e, Kp: int, stream=None) -> None:
+    """meow::k_quant_rows (src/kernels.h:12-13)."""
+    check(load().vgemm_quant_rows(stream_ptr(stream), ptr(X), M, K, ldx, ptr(hi), ptr(lo), ptr(e), Kp))
+
+
+def k_epilogue(Chi, Clo, M: int, N: int, ldc: int, cst, e, Y, ldy: int, residual=None, stream=None) -> None:
+    """meow::k_epilogue without GroupNorm statistics (src/kernels.h:14-17)."""
+    check(load().vgemm_epilogue(stream_ptr(stream), ptr(Chi), ptr(Clo), M, N, ldc, ptr(cst), ptr(e), ptr(Y), ldy, ptr(residual)))
+
+
+def k_pixmax(X, rows: int, C: int, pm, stream=None) -> None:
+    """meow::k_pixmax (src/kernels.h:18-19)."""
+    check(load().vgemm_pixmax(stream_ptr(stream), ptr(X), rows, C, ptr(pm)))
+
+
+def k_im2col3(X, pm, B: int, H: int, W: int, C: int, stride: int, hi, lo, e, Kp: int, stream=None) -> None:
+    """meow::k_im2col3 (src/kernels.h:20-21)."""
+    check(load().vgemm_im2col3(stream_ptr(stream), ptr(X), ptr(pm), B, H, W, C, stride, ptr(hi), ptr(lo), ptr(e), Kp))
+
+
+def k_epilogue_split(Chi, Clo, M: int, N: int, ldc: int, cst, e, Cs: int, Y0, Y1, Y2, stream=None) -> None:
+    """meow::k_epilogue_split (src/kernels.h:68-69)."""
+    check(load().vgemm_epilogue_split(stream_ptr(stream), ptr(Chi), ptr(Clo), M, N, ldc, ptr(cst), ptr(e), Cs, ptr(Y0), ptr(Y1), ptr(Y2)))
+
+
+def k_epilogue_geglu_q(Chi, Clo, M: int, F: int, ldc: int, cst, e, Lphi, hi, lo, eo, Kp: int, stream=None) -> None:
+    """meow::k_epilogue_geglu_q (src/kernels.h:70)."""
+    check(load().vgemm_epilogue_geglu_q(stream_ptr(stream), ptr(Chi), ptr(Clo), M, F, ldc, ptr(cst), ptr(e), ptr(Lphi), ptr(hi), ptr(lo),
+                                        ptr(eo), Kp))
+
+
+def fill_u32(t, value: int = 0, stream=None) -> None:
+    """Fill a uint32/int32 tensor by a kernel (capture-safe; no hipMemsetAsync)."""
+    check(load().vgemm_fill_u32(stream_ptr(stream), ptr(t), t.numel() * t.element_size() // 4, value & 0xFFFFFFFF))
+
+
+class Graph:
+    """A captured GEMM sequence (src/engine.cu:625-630): capture() on a non-default stream, then replay()."""
+
+    def __init__(self, stream: torch.cuda.Stream):
+        self.stream = stream
+        self._exec = ctypes.c_void_p()
+
+    def begin(self) -> None:
+        check(load().vgemm_graph_begin(stream_ptr(self.stream)))
+
+    def end(self) -> None:
+        check(load().vgemm_graph_end(stream_ptr(self.stream), ctypes.byref(self._exec)))
+
+    def replay(self) -> None:
+        check(load().vgemm_graph_launch(self._exec, stream_ptr(self.stream)))
+
+    def destroy(self) -> None:
+        if self._exec:
+            check(load().vgemm_graph_destroy(self._exec))
+            self._exec = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.destroy()
+        except Exception:
+            pass

@@ -1,0 +1,84 @@
+"""The UNet GEMM set: the 194 linear/conv GEMMs of an SD-turbo-sized UNet
+forward at batch 8, every input seeded and resident in HBM, captured once into one hipGraph and
+replayed (the reference captures its whole forward the same way, src/engine.cu:625-630, 661-667).
+
+All layers share one split-K workspace: they run in order on one stream, so the workspace is never
+used by two GEMMs at once.
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from . import configs as cf
+from . import gemm as vg
+
+
+class GemmSet:
+    def __init__(self, layers: list[cf.Layer] | None = None, device: str = "cuda", keep_host: bool = False):
+        self.layers = layers if layers is not None else cf.unet_layers()
+        ws_bytes = max(vg.workspace_bytes(L.Mp, L.M, L.Np, L.N, L.Kp, L.epi) for L in self.layers)
+        self.ws = torch.empty(max(ws_bytes // 4, 1) + 64, dtype=torch.int32, device=device) if ws_bytes else None
+        self.probs: list[cf.DeviceProblem] = []
+        for L in self.layers:
+            p = cf.DeviceProblem(L, device=device, with_ws=False)
+            if self.ws is not None and vg.workspace_bytes(L.Mp, L.M, L.Np, L.N, L.Kp, L.epi):
+                p.E.ws = vg.ptr(self.ws)
+                p.E.ws_bytes = self.ws.numel() * 4
+            if not keep_host:
+                p.h = None   # regenerated from the seed when checked
+            self.probs.append(p)
+        self.stream = torch.cuda.Stream(device=device)
+        self.graph: vg.Graph | None = None
+
+    @property
+    def ops(self) -> int:
+        return sum(L.ops for L in self.layers)
+
+    def _enqueue(self):
+        for p in self.probs:
+            p.reset()
+            p.run(stream=self.stream)
+
+    def run_eager(self):
+        with torch.cuda.stream(self.stream):
+            self._enqueue()
+
+    def capture(self):
+        """Capture the whole set (residual re-seeds and rowmax zeroing by kernels, then the GEMM of
+        each layer, in forward order) into one graph."""
+        self.run_eager()                      # first calls outside capture
+        self.stream.synchronize()
+        self.graph = vg.Graph(self.stream)
+        with torch.cuda.stream(self.stream):
+            self.graph.begin()
+            self._enqueue()
+            self.graph.end()
+
+    def replay(self):
+        self.graph.replay()
+
+    def check_layer(self, i: int, rows_per_block: int = 16, seed: int = 0) -> None:
+        """Bit-exact check of layer i on three row blocks (first, last and one seeded block; every
+        output row depends on its own A row only) against the CPU oracle."""
+        import oracle
+
+        p = self.probs[i]
+        L = p.L
+        h = cf.make_host(L)
+        if L.meta.get("conv_in"):
+            h = cf.unet_conv_in_operand(L, h)
+        r = np.random.default_rng(seed + i)
+        starts = sorted({0, max(0, L.M - rows_per_block), int(r.integers(0, max(1, L.M - rows_per_block)))})
+        y = p.y.cpu().numpy()
+        rm = p.rowmax.cpu().numpy().view(np.uint32) if p.rowmax is not None else None
+        for s0 in starts:
+            rows = (s0, min(L.M, s0 + rows_per_block))
+            want, wrm = oracle.layer_reference(L, h, rows=rows)
+            got = y[rows[0]:rows[1]]
+            exp = want[rows[0]:rows[1]]
+            if not np.array_equal(got, exp):
+                bad = np.argwhere(got != exp)[0]
+                raise AssertionError(f"layer {i} {L.name}: rows {rows} mismatch at {tuple(bad)}: {got[tuple(bad)]} != {exp[tuple(bad)]}")
+            if rm is not None and not np.array_equal(rm[rows[0]:rows[1]], wrm[rows[0]:rows[1]]):
+                raise AssertionError(f"layer {i} {L.name}: rowmax mismatch in rows {rows}")
