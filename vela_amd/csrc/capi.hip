@@ -189,7 +189,9 @@ int vgemm_hl2(void* stream, const VgemmASrc* A, int Mp, int Mreal, const int8_t*
     case VGEMM_SRC_CONV16: {
         const void* img = A->src == VGEMM_SRC_CONV32 ? static_cast<const void*>(A->img) : static_cast<const void*>(A->img16);
         if (!img || !aligned16(img)) return fail(VGEMM_ERR_ARG, "gemm_hl conv source: null or unaligned image");
-        if (A->C <= 0 || A->C % 16 || A->K != 9 * A->C) return fail(VGEMM_ERR_ARG, "gemm_hl conv source: C %% 16 or K");
+        if (A->src == VGEMM_SRC_CONV32 && (A->C <= 0 || A->C % 16 || A->K != 9 * A->C)) return fail(VGEMM_ERR_ARG, "gemm_hl conv source: C %% 16 or K");
+        if (A->src == VGEMM_SRC_CONV16 && (A->C <= 0 || A->C % 8 || A->C > 16384 || A->K != 9 * A->C))
+            return fail(VGEMM_ERR_ARG, "gemm_hl conv source: C %% 8, C <= 16384 and K == 9C required for SRC_CONV16");
         if (A->K > Kp || A->H <= 0 || A->W <= 0 || A->stride <= 0) return fail(VGEMM_ERR_ARG, "gemm_hl conv source: H/W/stride/Kp");
         const int Ho = (A->H - 1) / A->stride + 1, Wo = (A->W - 1) / A->stride + 1;
         if (A->Ho != Ho || A->Wo != Wo) return fail(VGEMM_ERR_ARG, "gemm_hl conv source: Ho/Wo must be (H-1)/stride+1, (W-1)/stride+1");

@@ -1,20 +1,27 @@
-// The W8A16 hi/lo-split GEMM kernel for gfx950 (CDNA4), templated on the A source, the epilogue
-// and the tile shape. Each source file gemm_src_*.hip instantiates it for one source.
+// The W8A16 hi/lo-split GEMM kernels for gfx950 (CDNA4), templated on the A source, the epilogue
+// and the tile shape. Each source file gemm_src_*.hip instantiates them for one source.
 //
-// Block = 256 threads = 4 wave64s, each wave owning a (BM/WM) x (BN/WN) output sub-tile. Per 64-wide
-// K step every thread loads its share of the W tile and of the A tile from HBM with buffer loads
-// (out-of-range offsets read as zero: pad rows/columns and the image border of the implicit im2col
-// cost no branches), splits int16 activations into a signed hi byte and an offset lo byte
-// (lo - 128 = (q & 255) ^ 0x80) with byte permutes, and stores the three int8 planes (W, hi, lo)
-// to an XOR-swizzled, double-buffered LDS stage. The MFMA v_mfma_i32_16x16x64_i8 takes W as its A
-// operand and the activations as its B operand, so each lane ends up holding four consecutive output
-// columns of one output row; one W fragment feeds both activation planes.
+// Arithmetic: the int16 activation q = 256*hi + lo + 128 is split into a signed hi byte and an
+// offset lo byte (lo - 128 = (q & 255) ^ 0x80) with byte permutes; both planes run through
+// v_mfma_i32_16x16x64_i8 against the same W fragment (W is the MFMA's A operand, the activations its
+// B operand, so each lane ends up holding four consecutive output columns of one output row).
+//
+// Two main loops:
+//  * gemm_dma_kernel (int8 planes, int16 rows, int16 NHWC image, plain int8 GEMM): every operand
+//    byte goes HBM -> LDS by buffer_load ... lds into a ring of LDS stages, two K steps ahead of the
+//    MFMAs, with no register staging; out-of-range offsets read as zero (pad rows/columns and the
+//    image border of the implicit im2col cost no branches). int16 data sits raw in LDS and is split
+//    (and for the image source clamped/quantised) as each MFMA fragment is read. Waves are stacked
+//    along M (4 x 1), so each activation row is split once per block and its row maximum is
+//    complete inside one wave.
+//  * gemm_hl_kernel (int32 rows, int32 NHWC image): register-staged loads, quantise + split at the
+//    LDS store, double-buffered.
 //
 // Epilogue: acc = 256*Chi + Clo + 128*wsum, y = sat32(rshr(acc*m, s-e) + b) (src/gemm_hl.cu:40-52).
 // When the block's columns satisfy Kp*|m| < 2^30 (so |acc*m| < 2^52) and every shift s-e lies in
-// [1, 52], the epilogue runs in FP64, where it is exact: acc*m*2^-(s-e) + 1/2 is a dyadic rational
-// with a numerator below 2^53, one FMA produces it without rounding, and floor() then gives the
-// rounding shift. Otherwise it runs the reference's int64 formula element by element.
+// [1, 52], it runs in FP64, where it is exact: acc*m*2^-(s-e) + 1/2 is a dyadic rational with a
+// numerator below 2^53, one FMA produces it without rounding, and floor() then gives the rounding
+// shift. Otherwise it runs the reference's int64 formula element by element.
 #pragma once
 #include <climits>
 
@@ -27,21 +34,27 @@ struct Tile {
     static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_;
     static constexpr int WTM = BM / WM, WTN = BN / WN;   // wave sub-tile (rows x columns)
     static constexpr int MS = WTM / 16, NS = WTN / 16;   // 16x16 MFMA tiles per wave
-    static constexpr int WT = BN * 4 / 256;              // 16-byte W chunks per thread per K step
-    static constexpr int AT = BM * 4 / 256;              // 16-value A chunks per thread per K step
+    static constexpr int WT = BN * 4 / 256;              // 16-byte W chunks per thread per K step (register path)
+    static constexpr int AT = BM * 4 / 256;              // 16-value A chunks per thread per K step (register path)
     static constexpr int STAGE = (BN + 2 * BM) * 64;     // LDS bytes per stage: W, hi, lo planes
     static_assert(WM * WN == 4, "four waves");
     static_assert(MS >= 1 && NS >= 2 && (NS % 2) == 0, "wave tile");
-    static_assert(WT >= 1 && AT >= 1 && (BN * 4) % 256 == 0 && (BM * 4) % 256 == 0, "loader mapping");
 };
 
-typedef Tile<128, 128, 2, 2> TileV0;   // 128 rows x 128 columns
-typedef Tile<64, 128, 1, 4> TileV1;    //  64 rows x 128 columns
-typedef Tile<128, 64, 2, 2> TileV2;    // 128 rows x  64 columns
+// register-path tiles (waves 2 x 2 / 1 x 4)
+typedef Tile<128, 128, 2, 2> TileV0;
+typedef Tile<64, 128, 1, 4> TileV1;
+typedef Tile<128, 64, 2, 2> TileV2;
+// DMA-path tiles (waves stacked along M)
+typedef Tile<128, 128, 4, 1> TileD0;
+typedef Tile<64, 128, 4, 1> TileD1;
+typedef Tile<128, 64, 4, 1> TileD2;
 
-// byte offset of 16-byte chunk `chunk` (0..3) of LDS row `row` (64 bytes per row); the XOR keeps
-// the 16 rows read by one MFMA fragment load on 16 distinct bank groups
+// byte offset of 16-byte chunk `chunk` (0..3) of a 64-byte LDS row; the XOR keeps the 16 rows read
+// by one MFMA fragment load on 16 distinct bank groups
 __device__ __forceinline__ int swz(int row, int chunk) { return row * 64 + ((chunk ^ ((row >> 2) & 3)) << 4); }
+// byte offset of 16-byte chunk `chunk` (0..7) of a 128-byte LDS row (raw int16 activations)
+__device__ __forceinline__ int swz16(int row, int chunk) { return row * 128 + ((chunk ^ ((row >> 1) & 7)) << 4); }
 
 // LDS row of W-tile row `row`. For GEGLU the a-columns (even) go to the first half and the
 // g-columns (odd) to the second half, so a wave's a- and g-subtiles hold matching columns.
@@ -49,6 +62,12 @@ template <int EPI, int BN>
 __device__ __forceinline__ int wrow_lds(int row) {
     if constexpr (EPI == EPI_GEGLU) return (row & 1) ? (BN / 2 + (row >> 1)) : (row >> 1);
     else return row;
+}
+// inverse: W-tile row stored at LDS row `lr`
+template <int EPI, int BN>
+__device__ __forceinline__ int wrow_of_lds(int lr) {
+    if constexpr (EPI == EPI_GEGLU) return lr < BN / 2 ? 2 * lr : 2 * (lr - BN / 2) + 1;
+    else return lr;
 }
 
 // first LDS row of MFMA column-subtile ns of wave column wn
@@ -81,15 +100,13 @@ __device__ __forceinline__ void quant_pack16(const v4i* x, int e, unsigned* d) {
     }
 }
 
-// 16 int16 values of an image quantised with shift e, packed back to int16 pairs
-__device__ __forceinline__ void quant16_pairs(const v4i* x, int e, unsigned* d) {
+// 16 int16 image values (two per dword, in place) quantised with shift e (quant16_32)
+__device__ __forceinline__ void quant16_pairs(unsigned* d, int e) {
     if (e == 0) {
         // quant16_32(v, 0) = max(v, -32767) for int16 v
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            // copy the vector element to a scalar first: this compiler folds __builtin_bit_cast of
-            // an ext-vector subscript to element 0 of the vector
-            const int w = x[j >> 2][j & 3];
+            const unsigned w = d[j];
             s2 v = __builtin_bit_cast(s2, w);
             v = __builtin_elementwise_max(v, s2{-32767, -32767});
             d[j] = __builtin_bit_cast(unsigned, v);
@@ -97,7 +114,7 @@ __device__ __forceinline__ void quant16_pairs(const v4i* x, int e, unsigned* d) 
     } else {
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            const int w = x[j >> 2][j & 3];
+            const int w = int(d[j]);
             const int q0 = quant16_32(int(short(w & 0xffff)), e);
             const int q1 = quant16_32(w >> 16, e);
             d[j] = __builtin_amdgcn_perm(unsigned(q1), unsigned(q0), 0x05040100u);
@@ -105,73 +122,67 @@ __device__ __forceinline__ void quant16_pairs(const v4i* x, int e, unsigned* d) 
     }
 }
 
-template <int SRC, int EPI, class T>
-__global__ void __launch_bounds__(256) gemm_hl_kernel(const GemmParams p) {
-    constexpr int BM = T::BM, BN = T::BN, MS = T::MS, NS = T::NS;
-    constexpr bool TWO = EPI != EPI_RAW;                            // two activation planes
-    constexpr bool FUSED = EPI != EPI_PARTIAL && EPI != EPI_RAW;     // requantising epilogue here
+// ---------------------------------------------------------------- epilogue shared state
+
+// Per-block epilogue constants, GELU table and exactness flags, in LDS.
+template <int BN, bool LUT>
+struct EpiShared {
+    double ms[BN];      // m * 2^-s
+    double wm[BN];      // 128 * wsum * m * 2^-s
+    double wmh[BN];     // wm + 1/2
+    int b[BN];
+    int2 lut[LUT ? 2050 : 1];   // lut[i + 1] = (L[i], L[i+1] - L[i]); lut[0] below the table, lut[2049] above
+    int flag[6];        // emin, emax, smin, smax, column bound failed, table range failed
+};
+
+struct EpiFlags {
+    bool fast, ezero;
+};
+
+// Fill the epilogue constants of columns [n0, n0 + BN) (in LDS-row order) and decide whether the
+// FP64 epilogue is exact for every element of this block.
+template <int EPI, int SRC, int BM, int BN, class S>
+__device__ __forceinline__ EpiFlags block_prologue(const GemmParams& p, int m0, int n0, S& sh) {
     constexpr bool NEEDLUT = EPI == EPI_GEGLU || EPI == EPI_GELU;
-    constexpr int AREG = (SRC == SRC_X32 || SRC == SRC_CONV32) ? 4 : 2;   // 16-byte loads per A chunk
-    constexpr bool CONV = SRC == SRC_CONV32 || SRC == SRC_CONV16;
-
-    __shared__ __attribute__((aligned(16))) unsigned char smem[2 * T::STAGE];
-    __shared__ __attribute__((aligned(16))) double s_ms[FUSED ? BN : 1];
-    __shared__ __attribute__((aligned(16))) double s_wm[FUSED ? BN : 1];
-    __shared__ __attribute__((aligned(16))) double s_wmh[FUSED ? BN : 1];
-    __shared__ __attribute__((aligned(16))) int s_b[FUSED ? BN : 1];
-    __shared__ int2 s_lut[NEEDLUT ? 2050 : 1];
-    __shared__ int s_flag[6];
-
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave % T::WM, wn = wave / T::WM;
-
-    // ---- tile of this block. Blocks are dispatched round-robin over the 8 XCDs; renumber them so
-    // that each XCD receives a contiguous range of tiles (neighbouring column tiles of one row
-    // stripe share the A stripe in that XCD's L2).
-    const int nblk = gridDim.x, bid = blockIdx.x;
-    const int q8 = nblk >> 3, r8 = nblk & 7, xcd = bid & 7, slot = bid >> 3;
-    const int lin = (xcd < r8 ? xcd * (q8 + 1) : r8 * (q8 + 1) + (xcd - r8) * q8) + slot;
-    const int ks = lin % p.ksplit, tl = lin / p.ksplit;
-    const int mt = tl / p.ntiles, nt = tl - mt * p.ntiles;
-    const int m0 = mt * BM, n0 = nt * BN;
-    const int nK = (p.Kp + 63) >> 6;
-    const int kb = ks * p.kper, ke = min(nK, kb + p.kper);
-
-    const int bt = blockIdx.y;   // batch index (EPI_RAW)
-    const char* a0p = static_cast<const char*>(p.a0) + (EPI == EPI_RAW ? bt * p.sA : 0);
-    const int8_t* wp = p.w + (EPI == EPI_RAW ? bt * p.sW : 0);
-    const __amdgpu_buffer_rsrc_t rW = make_rsrc(wp, p.w_bytes);
-    const __amdgpu_buffer_rsrc_t rA0 = make_rsrc(a0p, p.a0_bytes);
-    const __amdgpu_buffer_rsrc_t rA1 = make_rsrc(SRC == SRC_I8 && TWO ? p.a1 : a0p, SRC == SRC_I8 && TWO ? p.a1_bytes : p.a0_bytes);
-
-    // ---- block prologue: epilogue constants, GELU table, and the exactness conditions of the
-    // FP64 epilogue over this block's rows and columns
-    bool fast = true, ezero = true;
-    if constexpr (FUSED) {
-        if (tid == 0) {
-            s_flag[0] = INT_MAX; s_flag[1] = INT_MIN; s_flag[2] = INT_MAX; s_flag[3] = INT_MIN;
-            s_flag[4] = 0; s_flag[5] = 0;
-        }
-        __syncthreads();
-        if (tid < BM) {
-            const int r = m0 + tid;
+    const int tid = threadIdx.x, lane = tid & 63;
+    if (tid == 0) {
+        sh.flag[0] = INT_MAX; sh.flag[1] = INT_MIN; sh.flag[2] = INT_MAX; sh.flag[3] = INT_MIN;
+        sh.flag[4] = 0; sh.flag[5] = 0;
+    }
+    __syncthreads();
+    // per-row shift range (one LDS atomic per wave)
+    {
+        int emn = INT_MAX, emx = INT_MIN;
+        for (int i = tid; i < BM; i += 256) {
+            const int r = m0 + i;
             if (r < p.Mreal) {
                 const int er = SRC == SRC_X32 ? rowexp_u32(p.xrowmax[r]) : (p.e ? p.e[r] : 0);
-                atomicMin(&s_flag[0], er);
-                atomicMax(&s_flag[1], er);
+                emn = min(emn, er);
+                emx = max(emx, er);
             }
         }
-        if (tid < BN) {
-            const int j = tid;
-            const int n = EPI == EPI_GEGLU ? n0 + (j < BN / 2 ? 2 * j : 2 * (j - BN / 2) + 1) : n0 + j;
+#pragma unroll
+        for (int o = 32; o; o >>= 1) {
+            emn = min(emn, __shfl_xor(emn, o));
+            emx = max(emx, __shfl_xor(emx, o));
+        }
+        if (lane == 0 && emn <= emx) {
+            atomicMin(&sh.flag[0], emn);
+            atomicMax(&sh.flag[1], emx);
+        }
+    }
+    {
+        int smn = INT_MAX, smx = INT_MIN, bad = 0;
+        for (int j = tid; j < BN; j += 256) {
+            const int n = n0 + wrow_of_lds<EPI, BN>(j);
             double ms = 0.0, wmv = 0.0, wmh = 0.5;
             int bb = 0;
             if (n < p.Nreal) {
                 const int4 c = p.cst[n];
                 const i64 mag = (c.x < 0 ? -i64(c.x) : i64(c.x)) * i64(p.Kp);
-                if (mag >= (1LL << 30)) atomicOr(&s_flag[4], 1);
-                atomicMin(&s_flag[2], c.y);
-                atomicMax(&s_flag[3], c.y);
+                if (mag >= (1LL << 30) || c.y < -1000 || c.y > 1000) bad = 1;
+                smn = min(smn, c.y);
+                smx = max(smx, c.y);
                 if (c.y >= -1000 && c.y <= 1000) {
                     ms = ldexp(double(c.x), -c.y);
                     wmv = ldexp(128.0 * (double(c.w) * double(c.x)), -c.y);
@@ -179,28 +190,502 @@ __global__ void __launch_bounds__(256) gemm_hl_kernel(const GemmParams p) {
                 }
                 bb = c.z;
             }
-            s_ms[j] = ms; s_wm[j] = wmv; s_wmh[j] = wmh; s_b[j] = bb;
+            sh.ms[j] = ms; sh.wm[j] = wmv; sh.wmh[j] = wmh; sh.b[j] = bb;
         }
-        if constexpr (NEEDLUT) {
-            // s_lut[i + 1] = (L[i], L[i+1] - L[i]) for i in [0, 2048); s_lut[0] serves arguments
-            // below the table (value 0) and s_lut[2049] arguments at or above its end (65536)
-            for (int i = tid; i < 2050; i += 256) {
-                int2 v;
-                if (i == 0) v = make_int2(0, 0);
-                else if (i == 2049) v = make_int2(65536, 0);
-                else {
-                    const int a = p.Lphi[i - 1], nx = p.Lphi[i];
-                    v = make_int2(a, nx - a);
-                    if (a < 0 || a > 65536 || nx < 0 || nx > 65536) atomicOr(&s_flag[5], 1);
+#pragma unroll
+        for (int o = 32; o; o >>= 1) {
+            smn = min(smn, __shfl_xor(smn, o));
+            smx = max(smx, __shfl_xor(smx, o));
+            bad |= __shfl_xor(bad, o);
+        }
+        if (lane == 0) {
+            if (smn <= smx) {
+                atomicMin(&sh.flag[2], smn);
+                atomicMax(&sh.flag[3], smx);
+            }
+            if (bad) atomicOr(&sh.flag[4], 1);
+        }
+    }
+    if constexpr (NEEDLUT) {
+        int bad = 0;
+        for (int i = tid; i < 2050; i += 256) {
+            int2 v;
+            if (i == 0) v = make_int2(0, 0);
+            else if (i == 2049) v = make_int2(65536, 0);
+            else {
+                const int a = p.Lphi[i - 1], nx = p.Lphi[i];
+                v = make_int2(a, nx - a);
+                if (a < 0 || a > 65536 || nx < 0 || nx > 65536) bad = 1;
+            }
+            sh.lut[i] = v;
+        }
+#pragma unroll
+        for (int o = 32; o; o >>= 1) bad |= __shfl_xor(bad, o);
+        if (lane == 0 && bad) atomicOr(&sh.flag[5], 1);
+    }
+    __syncthreads();
+    const i64 emin = sh.flag[0], emax = sh.flag[1], smin = sh.flag[2], smax = sh.flag[3];
+    EpiFlags f;
+    f.fast = !sh.flag[4] && (smin - emax >= 1) && (smax - emin <= 52) && emin >= -1000 && emax <= 1000;
+    if (NEEDLUT && sh.flag[5]) f.fast = false;
+    f.ezero = emin > emax || (emin == 0 && emax == 0);
+    return f;
+}
+
+// The requantising epilogue of one wave. Subtile (ns, ms) of the wave holds rows
+// rbase + ms*16 + (lane & 15) and LDS-table rows wsub_row(wn, ns) + 4*(lane >> 4) + v, v = 0..3.
+template <int EPI, int SRC, class T, bool EZERO, bool SMALLK, class S>
+__device__ __forceinline__ void fused_epilogue_t(const GemmParams& p, const v4i (&acc_h)[T::NS][T::MS], const v4i (&acc_l)[T::NS][T::MS],
+                                                 int rbase, int n0, int wn, const S& sh, bool fast, const int (&er)[T::MS]) {
+    constexpr int MS = T::MS, NS = T::NS;
+    const int lane = threadIdx.x & 63, fr = lane & 15, fg = lane >> 4;
+    double pr[MS];
+#pragma unroll
+    for (int ms = 0; ms < MS; ++ms) pr[ms] = EZERO ? 1.0 : ldexp(1.0, min(max(er[ms], -1000), 1000));
+    uint32_t mx[MS];
+#pragma unroll
+    for (int ms = 0; ms < MS; ++ms) mx[ms] = 0;
+
+    // A = 256*Chi + Clo as an exact double
+    auto comb = [&](int h, int l) -> double {
+        if constexpr (SMALLK) return double((h << 8) + l);
+        else return __builtin_fma(double(h), 256.0, double(l));
+    };
+    // floor(acc*m*2^-(s-e) + 1/2) saturated, + b saturated: exact under the block conditions
+    auto epi_fast = [&](double A, double ms_, double wm_, double wmh_, int b_, double prr) -> int {
+        double X;
+        if constexpr (EZERO) X = __builtin_fma(A, ms_, wmh_);
+        else X = __builtin_fma(__builtin_fma(A, ms_, wm_), prr, 0.5);
+        return add_sat(cvt_sat(__builtin_floor(X)), b_);
+    };
+    // GELU factor (lut16i) for tables with 0 <= L <= 65536
+    auto phi = [&](int x) -> int {
+        const int z = min(max(x, -1048577), 1048576) + 1048576;   // [-1, 2^21]
+        const int2 t = sh.lut[(z >> 10) + 1];
+        return t.x + (__mul24(t.y, z & 1023) >> 10);
+    };
+    // floor((y * phi(y) + 2^15) / 2^16) for 0 <= phi <= 65536 (never saturates)
+    auto gelu_fast = [&](int y) -> double {
+        const double P = __builtin_fma(double(y), double(phi(y)), 32768.0);
+        return __builtin_floor(P * (1.0 / 65536.0));
+    };
+
+    constexpr int NOUT = EPI == EPI_GEGLU ? NS / 2 : NS;
+#pragma unroll
+    for (int ns = 0; ns < NOUT; ++ns) {
+        const int lr = wsub_row<EPI, T>(wn, ns) + 4 * fg;   // table row of this lane's 4 columns
+        const int lg = EPI == EPI_GEGLU ? wsub_row<EPI, T>(wn, ns + NS / 2) + 4 * fg : lr;
+        // output column of value v: n0 + lr + v (plain); (n0 >> 1) + lr + v (GEGLU, lr < BN/2)
+        const int ncol = EPI == EPI_GEGLU ? (n0 >> 1) + lr : n0 + lr;
+        const int nlim = EPI == EPI_GEGLU ? (p.Nreal >> 1) : p.Nreal;
+        if (ncol >= nlim) continue;
+        double c_ms[4], c_wm[4], c_wmh[4], g_ms[4], g_wm[4], g_wmh[4];
+        int c_b[4], g_b[4];
+        if (fast) {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                c_ms[v] = sh.ms[lr + v]; c_wmh[v] = sh.wmh[lr + v]; c_b[v] = sh.b[lr + v];
+                if constexpr (!EZERO) c_wm[v] = sh.wm[lr + v];
+                if constexpr (EPI == EPI_GEGLU) {
+                    g_ms[v] = sh.ms[lg + v]; g_wmh[v] = sh.wmh[lg + v]; g_b[v] = sh.b[lg + v];
+                    if constexpr (!EZERO) g_wm[v] = sh.wm[lg + v];
                 }
-                s_lut[i] = v;
             }
         }
-        __syncthreads();
-        const i64 emin = s_flag[0], emax = s_flag[1], smin = s_flag[2], smax = s_flag[3];
-        fast = !s_flag[4] && (smin - emax >= 1) && (smax - emin <= 52);
-        if (NEEDLUT && s_flag[5]) fast = false;
-        ezero = emin > emax || (emin == 0 && emax == 0);
+        const bool full = ncol + 3 < nlim;
+#pragma unroll
+        for (int ms = 0; ms < MS; ++ms) {
+            const int r = rbase + ms * 16 + fr;
+            if (r >= p.Mreal) continue;
+            int y[4];
+            if (fast) {
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const int ya = epi_fast(comb(acc_h[ns][ms][v], acc_l[ns][ms][v]), c_ms[v], c_wm[v], c_wmh[v], c_b[v], pr[ms]);
+                    if constexpr (EPI == EPI_GEGLU) {
+                        const int yg = epi_fast(comb(acc_h[ns + NS / 2][ms][v], acc_l[ns + NS / 2][ms][v]), g_ms[v], g_wm[v], g_wmh[v], g_b[v], pr[ms]);
+                        const double ge = gelu_fast(yg);
+                        const double Q = __builtin_fma(double(ya), ge, 32768.0);
+                        y[v] = cvt_sat(__builtin_floor(Q * (1.0 / 65536.0)));
+                    } else if constexpr (EPI == EPI_GELU) {
+                        y[v] = int(gelu_fast(ya));
+                    } else {
+                        y[v] = ya;
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    if (ncol + v >= nlim) { y[v] = 0; continue; }
+                    if constexpr (EPI == EPI_GEGLU) {
+                        const int na = 2 * (ncol + v);
+                        const int4 ca = p.cst[na], cg = p.cst[na + 1];
+                        const int ya = epi1_exact(acc_h[ns][ms][v], acc_l[ns][ms][v], ca.x, ca.y, ca.z, ca.w, er[ms]);
+                        const int yg = epi1_exact(acc_h[ns + NS / 2][ms][v], acc_l[ns + NS / 2][ms][v], cg.x, cg.y, cg.z, cg.w, er[ms]);
+                        y[v] = geglu_exact(ya, yg, p.Lphi);
+                    } else {
+                        const int4 c = p.cst[ncol + v];
+                        int yy = epi1_exact(acc_h[ns][ms][v], acc_l[ns][ms][v], c.x, c.y, c.z, c.w, er[ms]);
+                        if constexpr (EPI == EPI_GELU) yy = gelu_exact(yy, p.Lphi);
+                        y[v] = yy;
+                    }
+                }
+            }
+            if constexpr (EPI == EPI_SPLIT3) {
+                // Cs % 4 == 0: the four columns lie in one part (src/gemm_hl.cu:288-290)
+                const int part = ncol >= 2 * p.Cs ? 2 : (ncol >= p.Cs ? 1 : 0);
+                int32_t* d = (part == 0 ? p.Y : (part == 1 ? p.Y1 : p.Y2)) + size_t(r) * p.Cs + (ncol - part * p.Cs);
+                if (full && p.vec_store) *reinterpret_cast<v4i*>(d) = v4i{y[0], y[1], y[2], y[3]};
+                else {
+#pragma unroll
+                    for (int v = 0; v < 4; ++v)
+                        if (ncol + v < nlim) d[v] = y[v];
+                }
+            } else {
+                int32_t* d = p.Y + size_t(r) * p.ldy + ncol;
+                if constexpr (EPI != EPI_GEGLU) {
+                    if (p.R) {
+                        const int32_t* rp = p.R + size_t(r) * p.ldy + ncol;
+                        if (full && p.vec_store) {
+                            const v4i rv = *reinterpret_cast<const v4i*>(rp);
+#pragma unroll
+                            for (int v = 0; v < 4; ++v) y[v] = add_sat(y[v], rv[v]);
+                        } else {
+#pragma unroll
+                            for (int v = 0; v < 4; ++v)
+                                if (ncol + v < nlim) y[v] = add_sat(y[v], rp[v]);
+                        }
+                    }
+                }
+                if (full && p.vec_store) *reinterpret_cast<v4i*>(d) = v4i{y[0], y[1], y[2], y[3]};
+                else {
+#pragma unroll
+                    for (int v = 0; v < 4; ++v)
+                        if (ncol + v < nlim) d[v] = y[v];
+                }
+                if (p.rowmax) {
+                    // |y| as unsigned: max_i32(y, -y) is |y| except at INT_MIN, whose bits are 2^31
+#pragma unroll
+                    for (int v = 0; v < 4; ++v)
+                        if (ncol + v < nlim) mx[ms] = max(mx[ms], uint32_t(max(y[v], -y[v])));
+                }
+            }
+        }
+    }
+    if constexpr (EPI != EPI_SPLIT3) {
+        if (p.rowmax) {
+            // lanes fr, fr+16, fr+32, fr+48 hold the same row: one atomic per row and wave
+#pragma unroll
+            for (int ms = 0; ms < MS; ++ms) {
+                uint32_t m = mx[ms];
+                m = max(m, uint32_t(__shfl_xor(int(m), 16)));
+                m = max(m, uint32_t(__shfl_xor(int(m), 32)));
+                const int r = rbase + ms * 16 + fr;
+                if (fg == 0 && r < p.Mreal && m) atomicMax(p.rowmax + r, m);
+            }
+        }
+    }
+}
+
+template <int EPI, int SRC, class T, class S>
+__device__ __forceinline__ void fused_epilogue(const GemmParams& p, const v4i (&acc_h)[T::NS][T::MS], const v4i (&acc_l)[T::NS][T::MS],
+                                               int rbase, int n0, int wn, const S& sh, EpiFlags f, const int (&er)[T::MS]) {
+    const bool smallK = p.Kp <= 496;   // |256*Chi + Clo| < 2^31
+    if (f.ezero) {
+        if (smallK) fused_epilogue_t<EPI, SRC, T, true, true>(p, acc_h, acc_l, rbase, n0, wn, sh, f.fast, er);
+        else fused_epilogue_t<EPI, SRC, T, true, false>(p, acc_h, acc_l, rbase, n0, wn, sh, f.fast, er);
+    } else {
+        if (smallK) fused_epilogue_t<EPI, SRC, T, false, true>(p, acc_h, acc_l, rbase, n0, wn, sh, f.fast, er);
+        else fused_epilogue_t<EPI, SRC, T, false, false>(p, acc_h, acc_l, rbase, n0, wn, sh, f.fast, er);
+    }
+}
+
+// int32 partial sums of one K range: ws[(ks*2 + plane) * ws_rows + row][col]
+template <class T>
+__device__ __forceinline__ void store_partial(const GemmParams& p, const v4i (&acc_h)[T::NS][T::MS], const v4i (&acc_l)[T::NS][T::MS],
+                                              int rbase, int cbase, int ks) {
+    const int lane = threadIdx.x & 63, fr = lane & 15, fg = lane >> 4;
+#pragma unroll
+    for (int ns = 0; ns < T::NS; ++ns)
+#pragma unroll
+        for (int ms = 0; ms < T::MS; ++ms) {
+            const int r = rbase + ms * 16 + fr;
+            const int n = cbase + ns * 16 + 4 * fg;
+            int32_t* dh = p.ws + (size_t(ks * 2) * p.ws_rows + r) * p.ws_ld + n;
+            int32_t* dl = dh + size_t(p.ws_rows) * p.ws_ld;
+            *reinterpret_cast<v4i*>(dh) = acc_h[ns][ms];
+            *reinterpret_cast<v4i*>(dl) = acc_l[ns][ms];
+        }
+}
+
+// plain int32 output of the single-plane GEMM
+template <class T>
+__device__ __forceinline__ void store_raw(const GemmParams& p, const v4i (&acc)[T::NS][T::MS], int rbase, int cbase, int bt) {
+    const int lane = threadIdx.x & 63, fr = lane & 15, fg = lane >> 4;
+    int32_t* C = p.Y + bt * p.sC;
+#pragma unroll
+    for (int ns = 0; ns < T::NS; ++ns)
+#pragma unroll
+        for (int ms = 0; ms < T::MS; ++ms) {
+            const int r = rbase + ms * 16 + fr;
+            const int n = cbase + ns * 16 + 4 * fg;
+            if (r >= p.Mreal) continue;
+            int32_t* d = C + size_t(r) * p.ldy + n;
+            if (p.vec_store && n + 3 < p.Nreal) {
+                *reinterpret_cast<v4i*>(d) = acc[ns][ms];
+            } else {
+#pragma unroll
+                for (int v = 0; v < 4; ++v)
+                    if (n + v < p.Nreal) d[v] = acc[ns][ms][v];
+            }
+        }
+}
+
+// Tile of this block. Blocks are dispatched round-robin over the 8 XCDs; renumber them so that
+// each XCD receives a contiguous range of tiles (neighbouring column tiles of one row stripe share
+// the A stripe in that XCD's L2).
+struct TileIdx {
+    int ks, mt, nt;
+};
+__device__ __forceinline__ TileIdx tile_index(const GemmParams& p) {
+    const int nblk = gridDim.x, bid = blockIdx.x;
+    const int q8 = nblk >> 3, r8 = nblk & 7, xcd = bid & 7, slot = bid >> 3;
+    const int lin = (xcd < r8 ? xcd * (q8 + 1) : r8 * (q8 + 1) + (xcd - r8) * q8) + slot;
+    TileIdx t;
+    t.ks = lin % p.ksplit;
+    const int tl = lin / p.ksplit;
+    t.mt = tl / p.ntiles;
+    t.nt = tl - t.mt * p.ntiles;
+    return t;
+}
+
+// ================================================================ DMA main loop (I8, I16, CONV16, RAW)
+
+template <int SRC, int EPI, class T>
+struct DmaCfg {
+    static constexpr bool TWO = EPI != EPI_RAW;
+    static constexpr bool FUSED = EPI != EPI_PARTIAL && EPI != EPI_RAW;
+    static constexpr bool NEEDLUT = EPI == EPI_GEGLU || EPI == EPI_GELU;
+    static constexpr bool RAW16 = SRC == SRC_I16 || SRC == SRC_CONV16;   // raw int16 rows in LDS
+    static constexpr int W_BYTES = T::BN * 64;
+    static constexpr int A_BYTES = RAW16 ? T::BM * 128 : (TWO ? 2 : 1) * T::BM * 64;
+    static constexpr int STAGE = W_BYTES + A_BYTES;
+    static constexpr int NST = NEEDLUT ? 2 : 3;   // LDS stages (keeps two blocks per CU within 160 KB)
+    static constexpr int W_INS = T::BN / 64;      // DMA instructions per wave per stage: W
+    static constexpr int A_INS = A_BYTES / 4096;  //                                     A
+    static constexpr int PER_STAGE = W_INS + A_INS;
+    static_assert(W_INS >= 1 && A_INS >= 1 && (A_BYTES % 4096) == 0, "DMA mapping");
+};
+
+template <int SRC, int EPI, class T>
+__global__ void __launch_bounds__(256, 2) gemm_dma_kernel(const GemmParams p) {
+    using D = DmaCfg<SRC, EPI, T>;
+    constexpr int BM = T::BM, BN = T::BN, MS = T::MS, NS = T::NS, NST = D::NST;
+    constexpr bool TWO = D::TWO, FUSED = D::FUSED;
+
+    __shared__ __attribute__((aligned(16))) unsigned char smem[NST * D::STAGE];
+    __shared__ __attribute__((aligned(16))) EpiShared<FUSED ? BN : 1, D::NEEDLUT> sh;
+
+    // the wave index in a scalar register (the DMA's LDS addresses must be wave-uniform)
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const TileIdx ti = tile_index(p);
+    const int m0 = ti.mt * BM, n0 = ti.nt * BN;
+    const int nK = (p.Kp + 63) >> 6;
+    const int kb = ti.ks * p.kper, ke = min(nK, kb + p.kper);
+    const int bt = blockIdx.y;   // batch index (EPI_RAW)
+
+    const char* a0p = static_cast<const char*>(p.a0) + (EPI == EPI_RAW ? bt * p.sA : 0);
+    const int8_t* wp = p.w + (EPI == EPI_RAW ? bt * p.sW : 0);
+    const v4i rW = make_rsrc_words(wp, p.w_bytes);
+    const v4i rA0 = make_rsrc_words(a0p, p.a0_bytes);
+    const v4i rA1 = make_rsrc_words(SRC == SRC_I8 && TWO ? p.a1 : a0p, SRC == SRC_I8 && TWO ? p.a1_bytes : p.a0_bytes);
+
+    EpiFlags fl{true, true};
+    if constexpr (FUSED) fl = block_prologue<EPI, SRC, BM, BN>(p, m0, n0, sh);
+
+    // rows owned by this wave and their shifts (for the epilogue and the image quantisation)
+    const int rbase = m0 + wave * T::WTM;
+    int er[MS];
+#pragma unroll
+    for (int ms = 0; ms < MS; ++ms) {
+        const int r = rbase + ms * 16 + (lane & 15);
+        er[ms] = (r < p.Mreal && p.e && (FUSED || SRC == SRC_CONV16)) ? p.e[r] : 0;
+    }
+
+    // ---- DMA address state. W: wave instruction j covers LDS rows 16*(wave*W_INS + j) + lane/4,
+    // chunk position lane%4 (holding global chunk cp ^ swizzle). A (raw int16): rows
+    // 8*(wave*A_INS + j) + lane/8, chunk position lane%8. A (int8 planes): like W, hi then lo.
+    int w_row[D::W_INS], w_kc[D::W_INS];
+#pragma unroll
+    for (int j = 0; j < D::W_INS; ++j) {
+        const int lr = 16 * (wave * D::W_INS + j) + (lane >> 2);
+        w_row[j] = n0 + (FUSED ? wrow_of_lds<EPI, BN>(lr) : lr);
+        w_kc[j] = (lane & 3) ^ ((lr >> 2) & 3);
+    }
+    constexpr int A_ROWS_INS = D::RAW16 ? 8 : 16;                      // rows per DMA instruction
+    constexpr int A_INS_PLANE = D::RAW16 ? D::A_INS : D::A_INS / (TWO ? 2 : 1);
+    int a_r[A_INS_PLANE], a_c[A_INS_PLANE];
+    int a_b[A_INS_PLANE], a_iy0[A_INS_PLANE], a_ix0[A_INS_PLANE];
+#pragma unroll
+    for (int j = 0; j < A_INS_PLANE; ++j) {
+        const int row = A_ROWS_INS * (wave * A_INS_PLANE + j) + (D::RAW16 ? (lane >> 3) : (lane >> 2));
+        a_r[j] = m0 + row;
+        a_c[j] = D::RAW16 ? ((lane & 7) ^ ((row >> 1) & 7)) : ((lane & 3) ^ ((row >> 2) & 3));
+        if constexpr (SRC == SRC_CONV16) {
+            const int HoWo = p.Ho * p.Wo;
+            const int rr = a_r[j] < p.Mreal ? a_r[j] : 0;
+            const int b = rr / HoWo, pp = rr - b * HoWo, oy = pp / p.Wo, ox = pp - oy * p.Wo;
+            a_b[j] = b * p.H;
+            a_iy0[j] = a_r[j] < p.Mreal ? oy * p.stride - 1 : -(1 << 20);   // rows past Mreal read nothing
+            a_ix0[j] = ox * p.stride - 1;
+        }
+    }
+    const unsigned cmagic = SRC == SRC_CONV16 ? unsigned((0x100000000ull + unsigned(p.C) - 1) / unsigned(p.C)) : 0u;
+
+    auto issue = [&](int kt, int stage) {
+        const unsigned sbase = lds_addr(smem) + stage * D::STAGE;
+        const int kbase = kt * 64;
+#pragma unroll
+        for (int j = 0; j < D::W_INS; ++j) {
+            const int n = w_row[j], k = kbase + 16 * w_kc[j];
+            const unsigned off = (n < p.Nreal && k < p.Kp) ? unsigned(n) * unsigned(p.ldw) + unsigned(k) : OOB;
+            dma16(rW, off, sbase + (wave * D::W_INS + j) * 1024);
+        }
+        const unsigned sA = sbase + D::W_BYTES;
+#pragma unroll
+        for (int j = 0; j < A_INS_PLANE; ++j) {
+            const int r = a_r[j];
+            if constexpr (SRC == SRC_I16) {
+                const int k = kbase + 8 * a_c[j];
+                const unsigned off = (r < p.Mreal && k < p.K) ? (unsigned(r) * unsigned(p.lda) + unsigned(k)) * 2u : OOB;
+                dma16(rA0, off, sA + (wave * A_INS_PLANE + j) * 1024);
+            } else if constexpr (SRC == SRC_CONV16) {
+                // implicit 3x3 im2col, tap-major K: k = tap*C + c (src/gemm_hl.cu:104-114)
+                const int k = kbase + 8 * a_c[j];
+                const int tap = int(__umulhi(unsigned(k), cmagic));
+                const int ch = k - tap * p.C;
+                const int ky = (tap * 11) >> 5, kx = tap - 3 * ky;   // tap / 3, tap % 3 for tap < 9
+                const int iy = a_iy0[j] + ky, ix = a_ix0[j] + kx;
+                const bool ok = k < p.K && iy >= 0 && iy < p.H && ix >= 0 && ix < p.W;
+                const unsigned off = ok ? ((unsigned(a_b[j] + iy) * unsigned(p.W) + unsigned(ix)) * unsigned(p.C) + unsigned(ch)) * 2u : OOB;
+                dma16(rA0, off, sA + (wave * A_INS_PLANE + j) * 1024);
+            } else {
+                const int k = kbase + 16 * a_c[j];
+                const unsigned off = (r < p.Mreal && k < p.Kp) ? unsigned(r) * unsigned(p.lda) + unsigned(k) : OOB;
+                dma16(rA0, off, sA + (wave * A_INS_PLANE + j) * 1024);
+                if constexpr (TWO)
+                    dma16(rA1, off, sA + BM * 64 + (wave * A_INS_PLANE + j) * 1024);
+            }
+        }
+    };
+
+    v4i acc_h[NS][MS], acc_l[TWO ? NS : 1][TWO ? MS : 1];
+#pragma unroll
+    for (int ns = 0; ns < NS; ++ns)
+#pragma unroll
+        for (int ms = 0; ms < MS; ++ms) {
+            acc_h[ns][ms] = v4i{0, 0, 0, 0};
+            if constexpr (TWO) acc_l[ns][ms] = v4i{0, 0, 0, 0};
+        }
+
+    auto compute = [&](int stage) {
+        const unsigned char* sW = smem + stage * D::STAGE;
+        const unsigned char* sA = sW + D::W_BYTES;
+        const int fr = lane & 15, fg = lane >> 4;
+        v4i hf[MS], lf[TWO ? MS : 1];
+#pragma unroll
+        for (int ms = 0; ms < MS; ++ms) {
+            const int row = wave * T::WTM + ms * 16 + fr;
+            if constexpr (D::RAW16) {
+                const v4i x0 = *reinterpret_cast<const v4i*>(sA + swz16(row, 2 * fg));
+                const v4i x1 = *reinterpret_cast<const v4i*>(sA + swz16(row, 2 * fg + 1));
+                unsigned d[8] = {unsigned(x0[0]), unsigned(x0[1]), unsigned(x0[2]), unsigned(x0[3]),
+                                 unsigned(x1[0]), unsigned(x1[1]), unsigned(x1[2]), unsigned(x1[3])};
+                if constexpr (SRC == SRC_CONV16) quant16_pairs(d, er[ms]);
+                split16x16(d, hf[ms], lf[ms]);
+            } else {
+                hf[ms] = *reinterpret_cast<const v4i*>(sA + swz(row, fg));
+                if constexpr (TWO) lf[ms] = *reinterpret_cast<const v4i*>(sA + BM * 64 + swz(row, fg));
+            }
+        }
+#pragma unroll
+        for (int ns = 0; ns < NS; ++ns) {
+            const int row = (FUSED ? wsub_row<EPI, T>(0, ns) : ns * 16) + fr;
+            const v4i wf = *reinterpret_cast<const v4i*>(sW + swz(row, fg));
+#pragma unroll
+            for (int ms = 0; ms < MS; ++ms) {
+                acc_h[ns][ms] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf, hf[ms], acc_h[ns][ms], 0, 0, 0);
+                if constexpr (TWO) acc_l[ns][ms] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf, lf[ms], acc_l[ns][ms], 0, 0, 0);
+            }
+        }
+    };
+
+    // ---- main loop: NST-stage LDS ring, loads NST-1 steps ahead of the MFMAs.
+    // Every ordinary load above completes here, with a wait the compiler sees; otherwise it places
+    // that wait at the first use, inside the loop, where it would also drain the stage prefetch.
+    __builtin_amdgcn_s_waitcnt(0);
+    const int n = ke - kb;
+    if (n > 0) {
+#pragma unroll
+        for (int s = 0; s < NST - 1; ++s)
+            if (s < n) issue(kb + s, s);
+        for (int s = 0; s < n; ++s) {
+            // this stage's DMA done (the next stage's may still be in flight), then publish it
+            if constexpr (NST == 3) {
+                if (s + 1 < n) vm_wait<D::PER_STAGE>();
+                else vm_wait<0>();
+            } else {
+                vm_wait<0>();
+            }
+            block_barrier();
+            if (s + NST - 1 < n) issue(kb + s + NST - 1, (s + NST - 1) % NST);
+            compute(s % NST);
+        }
+    }
+
+    if constexpr (EPI == EPI_PARTIAL) {
+        store_partial<T>(p, acc_h, acc_l, rbase, n0, ti.ks);
+    } else if constexpr (EPI == EPI_RAW) {
+        store_raw<T>(p, acc_h, rbase, n0, bt);
+    } else {
+        fused_epilogue<EPI, SRC, T>(p, acc_h, acc_l, rbase, n0, 0, sh, fl, er);
+    }
+}
+
+// ================================================================ register-staged main loop (X32, CONV32)
+
+template <int SRC, int EPI, class T>
+__global__ void __launch_bounds__(256) gemm_hl_kernel(const GemmParams p) {
+    constexpr int BM = T::BM, BN = T::BN, MS = T::MS, NS = T::NS;
+    constexpr bool FUSED = EPI != EPI_PARTIAL;
+    constexpr bool NEEDLUT = EPI == EPI_GEGLU || EPI == EPI_GELU;
+    constexpr int AREG = 4;   // 16-byte loads per 16-value int32 chunk
+    constexpr bool CONV = SRC == SRC_CONV32;
+    static_assert(SRC == SRC_X32 || SRC == SRC_CONV32, "register path serves the int32 sources");
+
+    __shared__ __attribute__((aligned(16))) unsigned char smem[2 * T::STAGE];
+    __shared__ __attribute__((aligned(16))) EpiShared<FUSED ? BN : 1, NEEDLUT> sh;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave % T::WM, wn = wave / T::WM;
+    const TileIdx ti = tile_index(p);
+    const int m0 = ti.mt * BM, n0 = ti.nt * BN;
+    const int nK = (p.Kp + 63) >> 6;
+    const int kb = ti.ks * p.kper, ke = min(nK, kb + p.kper);
+
+    const __amdgpu_buffer_rsrc_t rW = make_rsrc(p.w, p.w_bytes);
+    const __amdgpu_buffer_rsrc_t rA0 = make_rsrc(p.a0, p.a0_bytes);
+
+    EpiFlags fl{true, true};
+    if constexpr (FUSED) fl = block_prologue<EPI, SRC, BM, BN>(p, m0, n0, sh);
+
+    const int rbase = m0 + wm * T::WTM;
+    int er[MS];
+#pragma unroll
+    for (int ms = 0; ms < MS; ++ms) {
+        const int r = rbase + ms * 16 + (lane & 15);
+        er[ms] = 0;
+        if (r < p.Mreal) er[ms] = SRC == SRC_X32 ? rowexp_u32(p.xrowmax[r]) : (p.e ? p.e[r] : 0);
     }
 
     // ---- per-thread load tasks (fixed over the K loop)
@@ -238,33 +723,24 @@ __global__ void __launch_bounds__(256) gemm_hl_kernel(const GemmParams p) {
 #pragma unroll
         for (int i = 0; i < T::WT; ++i) {
             const int c = tid + i * 256, row = c >> 2, kc = c & 3;
-            const int n = n0 + row, k = kbase + kc * 16;
+            const int n = n0 + (FUSED ? wrow_of_lds<EPI, BN>(row) : row), k = kbase + kc * 16;
             const unsigned off = (n < p.Nreal && k < p.Kp) ? unsigned(n) * unsigned(p.ldw) + unsigned(k) : OOB;
             wreg[i] = bload16(rW, off);
         }
 #pragma unroll
         for (int i = 0; i < T::AT; ++i) {
             const int r = m0 + a_row[i], k = kbase + a_kc[i] * 16;
-            if constexpr (SRC == SRC_I8) {
-                const unsigned off = (a_ok[i] && k < p.Kp) ? unsigned(r) * unsigned(p.lda) + unsigned(k) : OOB;
-                areg[i][0] = bload16(rA0, off);
-                if constexpr (TWO) areg[i][1] = bload16(rA1, off);
-            } else if constexpr (SRC == SRC_I16) {
-                const unsigned base = (unsigned(r) * unsigned(p.lda) + unsigned(k)) * 2u;
-                areg[i][0] = bload16(rA0, (a_ok[i] && k < p.K) ? base : OOB);
-                areg[i][1] = bload16(rA0, (a_ok[i] && k + 8 < p.K) ? base + 16u : OOB);
-            } else if constexpr (SRC == SRC_X32) {
+            if constexpr (SRC == SRC_X32) {
                 const unsigned base = (unsigned(r) * unsigned(p.lda) + unsigned(k)) * 4u;
 #pragma unroll
                 for (int j = 0; j < 4; ++j) areg[i][j] = bload16(rA0, (a_ok[i] && k + 4 * j < p.K) ? base + 16u * j : OOB);
             } else {
                 // implicit 3x3 im2col, tap-major K: k = tap*C + c (src/gemm_hl.cu:104-114)
                 const int tap = a_tap[i], c0 = a_c0[i];
-                const int ky = (tap * 11) >> 5, kx = tap - 3 * ky;   // tap / 3, tap % 3 for tap < 9
+                const int ky = (tap * 11) >> 5, kx = tap - 3 * ky;
                 const int iy = a_iy0[i] + ky, ix = a_ix0[i] + kx;
                 const bool ok = a_ok[i] && tap < 9 && iy >= 0 && iy < p.H && ix >= 0 && ix < p.W;
-                constexpr unsigned ES = SRC == SRC_CONV32 ? 4u : 2u;
-                const unsigned base = ((unsigned(a_base[i] + iy) * unsigned(p.W) + unsigned(ix)) * unsigned(p.C) + unsigned(c0)) * ES;
+                const unsigned base = ((unsigned(a_base[i] + iy) * unsigned(p.W) + unsigned(ix)) * unsigned(p.C) + unsigned(c0)) * 4u;
 #pragma unroll
                 for (int j = 0; j < AREG; ++j) areg[i][j] = bload16(rA0, ok ? base + 16u * j : OOB);
                 int nc = c0 + 64, ntap = tap;
@@ -275,6 +751,7 @@ __global__ void __launch_bounds__(256) gemm_hl_kernel(const GemmParams p) {
         }
     };
 
+    // the W tile is stored row-for-row here (gload already picked the permuted global rows)
     auto lstore = [&](int buf) {
         unsigned char* sW = smem + buf * T::STAGE;
         unsigned char* sAh = sW + BN * 64;
@@ -282,40 +759,27 @@ __global__ void __launch_bounds__(256) gemm_hl_kernel(const GemmParams p) {
 #pragma unroll
         for (int i = 0; i < T::WT; ++i) {
             const int c = tid + i * 256, row = c >> 2, kc = c & 3;
-            const int lr = FUSED ? wrow_lds<EPI, BN>(row) : row;
-            *reinterpret_cast<v4i*>(sW + swz(lr, kc)) = wreg[i];
+            *reinterpret_cast<v4i*>(sW + swz(row, kc)) = wreg[i];
         }
 #pragma unroll
         for (int i = 0; i < T::AT; ++i) {
             v4i h, l;
-            if constexpr (SRC == SRC_I8) {
-                h = areg[i][0];
-                if constexpr (TWO) l = areg[i][1];
-            } else {
-                unsigned d[8];
-                if constexpr (SRC == SRC_I16) {
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) d[j] = unsigned(areg[i][j >> 2][j & 3]);
-                } else if constexpr (SRC == SRC_CONV16) {
-                    quant16_pairs(areg[i], a_e[i], d);
-                } else {
-                    quant_pack16(areg[i], a_e[i], d);
-                }
-                split16x16(d, h, l);
-            }
+            unsigned d[8];
+            quant_pack16(areg[i], a_e[i], d);
+            split16x16(d, h, l);
             const int off = swz(a_row[i], a_kc[i]);
             *reinterpret_cast<v4i*>(sAh + off) = h;
-            if constexpr (TWO) *reinterpret_cast<v4i*>(sAl + off) = l;
+            *reinterpret_cast<v4i*>(sAl + off) = l;
         }
     };
 
-    v4i acc_h[NS][MS], acc_l[TWO ? NS : 1][TWO ? MS : 1];
+    v4i acc_h[NS][MS], acc_l[NS][MS];
 #pragma unroll
     for (int ns = 0; ns < NS; ++ns)
 #pragma unroll
         for (int ms = 0; ms < MS; ++ms) {
             acc_h[ns][ms] = v4i{0, 0, 0, 0};
-            if constexpr (TWO) acc_l[ns][ms] = v4i{0, 0, 0, 0};
+            acc_l[ns][ms] = v4i{0, 0, 0, 0};
         }
 
     auto compute = [&](int buf) {
@@ -323,7 +787,7 @@ __global__ void __launch_bounds__(256) gemm_hl_kernel(const GemmParams p) {
         const unsigned char* sAh = sW + BN * 64;
         const unsigned char* sAl = sAh + BM * 64;
         const int fr = lane & 15, fc = lane >> 4;
-        v4i wf[NS], hf[MS], lf[TWO ? MS : 1];
+        v4i wf[NS], hf[MS], lf[MS];
 #pragma unroll
         for (int ns = 0; ns < NS; ++ns) {
             const int row = (FUSED ? wsub_row<EPI, T>(wn, ns) : (wn * NS + ns) * 16) + fr;
@@ -333,14 +797,14 @@ __global__ void __launch_bounds__(256) gemm_hl_kernel(const GemmParams p) {
         for (int ms = 0; ms < MS; ++ms) {
             const int row = wm * T::WTM + ms * 16 + fr;
             hf[ms] = *reinterpret_cast<const v4i*>(sAh + swz(row, fc));
-            if constexpr (TWO) lf[ms] = *reinterpret_cast<const v4i*>(sAl + swz(row, fc));
+            lf[ms] = *reinterpret_cast<const v4i*>(sAl + swz(row, fc));
         }
 #pragma unroll
         for (int ns = 0; ns < NS; ++ns)
 #pragma unroll
             for (int ms = 0; ms < MS; ++ms) {
                 acc_h[ns][ms] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf[ns], hf[ms], acc_h[ns][ms], 0, 0, 0);
-                if constexpr (TWO) acc_l[ns][ms] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf[ns], lf[ms], acc_l[ns][ms], 0, 0, 0);
+                acc_l[ns][ms] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf[ns], lf[ms], acc_l[ns][ms], 0, 0, 0);
             }
     };
 
@@ -359,188 +823,11 @@ __global__ void __launch_bounds__(256) gemm_hl_kernel(const GemmParams p) {
         }
     }
 
-    // ---- epilogues
-    const int fr = lane & 15, fg = lane >> 4;
     if constexpr (EPI == EPI_PARTIAL) {
-        // int32 partial sums of this K range: ws[(ks*2 + plane) * ws_rows + row][col]
-#pragma unroll
-        for (int ns = 0; ns < NS; ++ns)
-#pragma unroll
-            for (int ms = 0; ms < MS; ++ms) {
-                const int r = m0 + wm * T::WTM + ms * 16 + fr;
-                const int n = n0 + (wn * NS + ns) * 16 + 4 * fg;
-                int32_t* dh = p.ws + (size_t(ks * 2) * p.ws_rows + r) * p.ws_ld + n;
-                int32_t* dl = dh + size_t(p.ws_rows) * p.ws_ld;
-                *reinterpret_cast<v4i*>(dh) = acc_h[ns][ms];
-                *reinterpret_cast<v4i*>(dl) = acc_l[ns][ms];
-            }
-        return;
-    } else if constexpr (EPI == EPI_RAW) {
-        int32_t* C = p.Y + bt * p.sC;
-#pragma unroll
-        for (int ns = 0; ns < NS; ++ns)
-#pragma unroll
-            for (int ms = 0; ms < MS; ++ms) {
-                const int r = m0 + wm * T::WTM + ms * 16 + fr;
-                const int n = n0 + (wn * NS + ns) * 16 + 4 * fg;
-                if (r >= p.Mreal) continue;
-                int32_t* d = C + size_t(r) * p.ldy + n;
-                if (p.vec_store && n + 3 < p.Nreal) {
-                    *reinterpret_cast<v4i*>(d) = acc_h[ns][ms];
-                } else {
-#pragma unroll
-                    for (int v = 0; v < 4; ++v)
-                        if (n + v < p.Nreal) d[v] = acc_h[ns][ms][v];
-                }
-            }
-        return;
+        // columns in natural order: W rows were not permuted for partials
+        store_partial<T>(p, acc_h, acc_l, rbase, n0 + wn * T::WTN, ti.ks);
     } else {
-        // per-lane row shifts
-        int er[MS];
-        double pr[MS];
-#pragma unroll
-        for (int ms = 0; ms < MS; ++ms) {
-            const int r = m0 + wm * T::WTM + ms * 16 + fr;
-            er[ms] = 0;
-            if (r < p.Mreal) er[ms] = SRC == SRC_X32 ? rowexp_u32(p.xrowmax[r]) : (p.e ? p.e[r] : 0);
-            pr[ms] = ldexp(1.0, er[ms] > 1000 ? 1000 : (er[ms] < -1000 ? -1000 : er[ms]));
-        }
-        const bool smallK = p.Kp <= 496;   // |256*Chi + Clo| < 2^31
-        uint32_t mx[MS];
-#pragma unroll
-        for (int ms = 0; ms < MS; ++ms) mx[ms] = 0;
-
-        // A = 256*Chi + Clo as an exact double
-        auto comb = [&](int h, int l) -> double {
-            if (smallK) return double((h << 8) + l);
-            return __builtin_fma(double(h), 256.0, double(l));
-        };
-        // floor(acc*m*2^-(s-e) + 1/2) saturated, + b saturated: exact under the block conditions
-        auto epi_fast = [&](double A, double ms_, double wm_, double wmh_, int b_, double prr) -> int {
-            const double X = ezero ? __builtin_fma(A, ms_, wmh_) : __builtin_fma(__builtin_fma(A, ms_, wm_), prr, 0.5);
-            return add_sat(cvt_sat(__builtin_floor(X)), b_);
-        };
-        // GELU factor table lookup (lut16i) for 0 <= L <= 65536
-        auto phi = [&](int x) -> int {
-            const int z = min(max(x, -1048577), 1048576) + 1048576;   // [-1, 2^21]
-            const int2 t = s_lut[(z >> 10) + 1];
-            return t.x + (__mul24(t.y, z & 1023) >> 10);
-        };
-        // sat32(rshr(y * phi(y), 16)) for 0 <= phi <= 65536: never saturates
-        auto gelu_fast = [&](int y) -> double {
-            const double P = __builtin_fma(double(y), double(phi(y)), 32768.0);
-            return __builtin_floor(P * (1.0 / 65536.0));
-        };
-
-        constexpr int NOUT = EPI == EPI_GEGLU ? NS / 2 : NS;
-#pragma unroll
-        for (int ns = 0; ns < NOUT; ++ns) {
-            const int lr = wsub_row<EPI, T>(wn, ns) + 4 * fg;   // table row of this lane's 4 columns
-            const int lg = EPI == EPI_GEGLU ? wsub_row<EPI, T>(wn, ns + NS / 2) + 4 * fg : lr;
-            double c_ms[4], c_wm[4], c_wmh[4], g_ms[4], g_wm[4], g_wmh[4];
-            int c_b[4], g_b[4];
-            if (fast) {
-#pragma unroll
-                for (int v = 0; v < 4; ++v) {
-                    c_ms[v] = s_ms[lr + v]; c_wm[v] = s_wm[lr + v]; c_wmh[v] = s_wmh[lr + v]; c_b[v] = s_b[lr + v];
-                    if constexpr (EPI == EPI_GEGLU) { g_ms[v] = s_ms[lg + v]; g_wm[v] = s_wm[lg + v]; g_wmh[v] = s_wmh[lg + v]; g_b[v] = s_b[lg + v]; }
-                }
-            }
-            // output column of value v: n0 + lr + v (plain); (n0 >> 1) + lr + v (GEGLU, lr < BN/2)
-            const int ncol = EPI == EPI_GEGLU ? (n0 >> 1) + lr : n0 + lr;
-            const int nlim = EPI == EPI_GEGLU ? (p.Nreal >> 1) : p.Nreal;
-#pragma unroll
-            for (int ms = 0; ms < MS; ++ms) {
-                const int r = m0 + wm * T::WTM + ms * 16 + fr;
-                if (r >= p.Mreal || ncol >= nlim) continue;
-                int y[4];
-                if (fast) {
-#pragma unroll
-                    for (int v = 0; v < 4; ++v) {
-                        const int ya = epi_fast(comb(acc_h[ns][ms][v], acc_l[ns][ms][v]), c_ms[v], c_wm[v], c_wmh[v], c_b[v], pr[ms]);
-                        if constexpr (EPI == EPI_GEGLU) {
-                            const int yg = epi_fast(comb(acc_h[ns + NS / 2][ms][v], acc_l[ns + NS / 2][ms][v]), g_ms[v], g_wm[v], g_wmh[v], g_b[v], pr[ms]);
-                            const double ge = gelu_fast(yg);
-                            const double Q = __builtin_fma(double(ya), ge, 32768.0);
-                            y[v] = cvt_sat(__builtin_floor(Q * (1.0 / 65536.0)));
-                        } else if constexpr (EPI == EPI_GELU) {
-                            y[v] = int(gelu_fast(ya));
-                        } else {
-                            y[v] = ya;
-                        }
-                    }
-                } else {
-#pragma unroll
-                    for (int v = 0; v < 4; ++v) {
-                        if (ncol + v >= nlim) { y[v] = 0; continue; }
-                        if constexpr (EPI == EPI_GEGLU) {
-                            const int na = 2 * (ncol + v);
-                            const int4 ca = p.cst[na], cg = p.cst[na + 1];
-                            const int ya = epi1_exact(acc_h[ns][ms][v], acc_l[ns][ms][v], ca.x, ca.y, ca.z, ca.w, er[ms]);
-                            const int yg = epi1_exact(acc_h[ns + NS / 2][ms][v], acc_l[ns + NS / 2][ms][v], cg.x, cg.y, cg.z, cg.w, er[ms]);
-                            y[v] = geglu_exact(ya, yg, p.Lphi);
-                        } else {
-                            const int4 c = p.cst[ncol + v];
-                            int yy = epi1_exact(acc_h[ns][ms][v], acc_l[ns][ms][v], c.x, c.y, c.z, c.w, er[ms]);
-                            if constexpr (EPI == EPI_GELU) yy = gelu_exact(yy, p.Lphi);
-                            y[v] = yy;
-                        }
-                    }
-                }
-                const bool full = ncol + 3 < nlim;
-                if constexpr (EPI == EPI_SPLIT3) {
-                    // Cs % 4 == 0: the four columns lie in one part (src/gemm_hl.cu:288-290)
-                    const int part = ncol >= 2 * p.Cs ? 2 : (ncol >= p.Cs ? 1 : 0);
-                    int32_t* d = (part == 0 ? p.Y : (part == 1 ? p.Y1 : p.Y2)) + size_t(r) * p.Cs + (ncol - part * p.Cs);
-                    if (full && p.vec_store) *reinterpret_cast<v4i*>(d) = v4i{y[0], y[1], y[2], y[3]};
-                    else {
-#pragma unroll
-                        for (int v = 0; v < 4; ++v)
-                            if (ncol + v < nlim) d[v] = y[v];
-                    }
-                } else {
-                    int32_t* d = p.Y + size_t(r) * p.ldy + ncol;
-                    if constexpr (EPI != EPI_GEGLU) {
-                        if (p.R) {
-                            const int32_t* rp = p.R + size_t(r) * p.ldy + ncol;
-                            if (full && p.vec_store) {
-                                const v4i rv = *reinterpret_cast<const v4i*>(rp);
-#pragma unroll
-                                for (int v = 0; v < 4; ++v) y[v] = add_sat(y[v], rv[v]);
-                            } else {
-#pragma unroll
-                                for (int v = 0; v < 4; ++v)
-                                    if (ncol + v < nlim) y[v] = add_sat(y[v], rp[v]);
-                            }
-                        }
-                    }
-                    if (full && p.vec_store) *reinterpret_cast<v4i*>(d) = v4i{y[0], y[1], y[2], y[3]};
-                    else {
-#pragma unroll
-                        for (int v = 0; v < 4; ++v)
-                            if (ncol + v < nlim) d[v] = y[v];
-                    }
-                    if (p.rowmax) {
-#pragma unroll
-                        for (int v = 0; v < 4; ++v)
-                            if (ncol + v < nlim) mx[ms] = max(mx[ms], uabs(y[v]));
-                    }
-                }
-            }
-        }
-        if constexpr (EPI != EPI_SPLIT3) {
-            if (p.rowmax) {
-                // lanes fr, fr+16, fr+32, fr+48 hold the same row: one atomic per row and wave
-#pragma unroll
-                for (int ms = 0; ms < MS; ++ms) {
-                    uint32_t m = mx[ms];
-                    m = max(m, uint32_t(__shfl_xor(int(m), 16)));
-                    m = max(m, uint32_t(__shfl_xor(int(m), 32)));
-                    const int r = m0 + wm * T::WTM + ms * 16 + fr;
-                    if (fg == 0 && r < p.Mreal && m) atomicMax(p.rowmax + r, m);
-                }
-            }
-        }
+        fused_epilogue<EPI, SRC, T>(p, acc_h, acc_l, rbase, n0, wn, sh, fl, er);
     }
 }
 
@@ -597,36 +884,59 @@ __global__ void __launch_bounds__(256) splitk_epilogue_kernel(const GemmParams p
     if (EPI != EPI_SPLIT3 && p.rowmax && mx) atomicMax(p.rowmax + r, mx);
 }
 
-// host-side launch of one instantiation
+// ---------------------------------------------------------------- host-side launches
+
 template <int SRC, int EPI, class T>
-hipError_t launch_gemm_t(const GemmParams& p, int batch, hipStream_t st) {
+hipError_t launch_dma_t(const GemmParams& p, int batch, hipStream_t st) {
+    dim3 grid(unsigned(p.mtiles * p.ntiles * p.ksplit), unsigned(batch));
+    hipLaunchKernelGGL((gemm_dma_kernel<SRC, EPI, T>), grid, dim3(256), 0, st, p);
+    return hipGetLastError();
+}
+
+template <int SRC, int EPI, class T>
+hipError_t launch_reg_t(const GemmParams& p, int batch, hipStream_t st) {
     dim3 grid(unsigned(p.mtiles * p.ntiles * p.ksplit), unsigned(batch));
     hipLaunchKernelGGL((gemm_hl_kernel<SRC, EPI, T>), grid, dim3(256), 0, st, p);
     return hipGetLastError();
 }
 
-template <int SRC, class T>
+template <int SRC, class T, bool DMA>
 hipError_t launch_gemm_epi(int epi, const GemmParams& p, int batch, hipStream_t st) {
+#define VK_LAUNCH(E)                                       \
+    [&]() {                                                \
+        if constexpr (DMA) return launch_dma_t<SRC, E, T>(p, batch, st); \
+        else return launch_reg_t<SRC, E, T>(p, batch, st); \
+    }()
     switch (epi) {
-    case EPI_PLAIN: return launch_gemm_t<SRC, EPI_PLAIN, T>(p, batch, st);
-    case EPI_SPLIT3: return launch_gemm_t<SRC, EPI_SPLIT3, T>(p, batch, st);
-    case EPI_GEGLU: return launch_gemm_t<SRC, EPI_GEGLU, T>(p, batch, st);
-    case EPI_GELU: return launch_gemm_t<SRC, EPI_GELU, T>(p, batch, st);
-    case EPI_PARTIAL: return launch_gemm_t<SRC, EPI_PARTIAL, T>(p, batch, st);
+    case EPI_PLAIN: return VK_LAUNCH(EPI_PLAIN);
+    case EPI_SPLIT3: return VK_LAUNCH(EPI_SPLIT3);
+    case EPI_GEGLU: return VK_LAUNCH(EPI_GEGLU);
+    case EPI_GELU: return VK_LAUNCH(EPI_GELU);
+    case EPI_PARTIAL: return VK_LAUNCH(EPI_PARTIAL);
     default: return hipErrorInvalidValue;
     }
+#undef VK_LAUNCH
 }
 
+// variant -> tile: 0 = 128x128, 1 = 64x128, 2 = 128x64 (rows x columns)
 template <int SRC>
 hipError_t launch_gemm_src(int variant, int epi, const GemmParams& p, int batch, hipStream_t st) {
-    switch (variant) {
-    case 1: return launch_gemm_epi<SRC, TileV1>(epi, p, batch, st);
-    case 2: return launch_gemm_epi<SRC, TileV2>(epi, p, batch, st);
-    default: return launch_gemm_epi<SRC, TileV0>(epi, p, batch, st);
+    constexpr bool DMA = SRC == SRC_I8 || SRC == SRC_I16 || SRC == SRC_CONV16;
+    if constexpr (DMA) {
+        switch (variant) {
+        case 1: return launch_gemm_epi<SRC, TileD1, true>(epi, p, batch, st);
+        case 2: return launch_gemm_epi<SRC, TileD2, true>(epi, p, batch, st);
+        default: return launch_gemm_epi<SRC, TileD0, true>(epi, p, batch, st);
+        }
+    } else {
+        switch (variant) {
+        case 1: return launch_gemm_epi<SRC, TileV1, false>(epi, p, batch, st);
+        case 2: return launch_gemm_epi<SRC, TileV2, false>(epi, p, batch, st);
+        default: return launch_gemm_epi<SRC, TileV0, false>(epi, p, batch, st);
+        }
     }
 }
 
-// declared here, defined in the per-source translation units
 hipError_t launch_gemm_i8(int variant, int epi, const GemmParams& p, int batch, hipStream_t st);
 hipError_t launch_gemm_x32(int variant, int epi, const GemmParams& p, int batch, hipStream_t st);
 hipError_t launch_gemm_conv32(int variant, int epi, const GemmParams& p, int batch, hipStream_t st);

@@ -4,9 +4,9 @@
 namespace vk {
 hipError_t launch_gemm_raw(int variant, const GemmParams& p, int batch, hipStream_t st) {
     switch (variant) {
-    case 1: return launch_gemm_t<SRC_I8, EPI_RAW, TileV1>(p, batch, st);
-    case 2: return launch_gemm_t<SRC_I8, EPI_RAW, TileV2>(p, batch, st);
-    default: return launch_gemm_t<SRC_I8, EPI_RAW, TileV0>(p, batch, st);
+    case 1: return launch_dma_t<SRC_I8, EPI_RAW, TileD1>(p, batch, st);
+    case 2: return launch_dma_t<SRC_I8, EPI_RAW, TileD2>(p, batch, st);
+    default: return launch_dma_t<SRC_I8, EPI_RAW, TileD0>(p, batch, st);
     }
 }
 

@@ -125,4 +125,33 @@ __device__ __forceinline__ v4i bload16(__amdgpu_buffer_rsrc_t r, unsigned off) {
     return __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
 }
 
+// The same raw buffer resource as four words, for the asm DMA loads below.
+__device__ __forceinline__ v4i make_rsrc_words(const void* base, unsigned bytes) {
+    const unsigned long long a = reinterpret_cast<unsigned long long>(base);
+    return v4i{int(unsigned(a)), int(unsigned(a >> 32) & 0xffffu), int(bytes), RSRC_WORD3};
+}
+
+// HBM -> LDS without registers: each lane's 16 bytes at buffer offset `off` land at LDS byte
+// address lds + 16 * lane (buffer_load_dwordx4 ... lds, M0 = LDS base). Issued from asm so that
+// the compiler does not wait for it before every barrier and LDS read: completion is awaited
+// explicitly with vm_wait<N>() before the barrier that publishes the stage.
+__device__ __forceinline__ void dma16(v4i rsrc, unsigned off, unsigned lds) {
+    asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" : : "v"(off), "s"(rsrc), "s"(lds) : "memory");
+}
+
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+    static_assert(N >= 0 && N < 64, "vmcnt");
+    asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
+}
+
+// workgroup barrier that orders memory accesses in the compiler (no implicit waits)
+__device__ __forceinline__ void block_barrier() { asm volatile("s_barrier" : : : "memory"); }
+
+// LDS byte address of a pointer into __shared__ memory (generic -> local address-space cast)
+__device__ __forceinline__ unsigned lds_addr(const void* p) {
+    typedef const __attribute__((address_space(3))) char* lds_ptr;
+    return unsigned(uintptr_t((lds_ptr)(p)));
+}
+
 }  // namespace vk
