@@ -30,6 +30,16 @@ PEAK_HBM_GBS = 8000.0        # MI355X HBM3E, 8 TB/s
 METRIC = "effective W8A16 TOPS & % int8 MFMA peak; UNet GEMM-set ms at batch 8"
 
 
+ONLY_NAMES = ("c1", "c2", "c2plain", "c3", "c4a", "c4b", "c4c")
+
+
+def only_layer(name):
+    from vela_amd import configs as cf
+
+    return {"c1": cf.c1, "c2": lambda: cf.c2(cf.EPI_GEGLU), "c2plain": lambda: cf.c2(cf.EPI_PLAIN), "c3": cf.c3,
+            "c4a": lambda: cf.c4()[0], "c4b": lambda: cf.c4()[1], "c4c": lambda: cf.c4()[2]}[name]()
+
+
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
@@ -111,6 +121,7 @@ def main():
     ap.add_argument("--no-unet", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-configs", action="store_true")
+    ap.add_argument("--only", choices=ONLY_NAMES, help="time one configuration only (for profiler runs)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (the GEMM shards by rows with no "
@@ -127,6 +138,16 @@ def main():
         sys.exit(2)
     dev = torch.device("cuda:0")
     stream = torch.cuda.Stream(device=dev)
+
+    if args.only:
+        L = only_layer(args.only)
+        p = cf.DeviceProblem(L)
+        p.reset()
+        torch.cuda.synchronize()
+        t = time_launches(lambda: p.run(stream=stream), stream, args.steps, args.warmup)
+        log(f"[bench] {L.name}: {t * 1e3:.2f} us/launch, {L.ops / (t * 1e-3) / 1e12:.1f} TOPS")
+        print(json.dumps({"workload": L.name, "us": round(t * 1e3, 3), "tops": round(L.ops / (t * 1e-3) / 1e12, 2)}), flush=True)
+        return
 
     # ---- headline: C2 GEGLU
     L = cf.c2(cf.EPI_GEGLU)

@@ -21,14 +21,14 @@ def rng(seed):
     return np.random.default_rng(seed)
 
 
-def make_w_cst(r, N, K, Np, Kp, s_range=(20, 29), m_range=(1 << 14, 1 << 15), wlo=-128):
+def make_w_cst(r, N, K, Np, Kp, s_range=(20, 29), m_range=(1 << 14, 1 << 15), wlo=-128, b_range=(-50000, 50000)):
     w = np.zeros((Np, Kp), np.int8)
     w[:N, :K] = r.integers(wlo, 128, (N, K))
     cst = np.zeros((Np, 4), np.int32)
     cst[:, 0] = 1
     cst[:N, 0] = r.integers(m_range[0], m_range[1], N, dtype=np.int64)
     cst[:N, 1] = r.integers(s_range[0], s_range[1] + 1, N)
-    cst[:N, 2] = r.integers(-50000, 50000, N)
+    cst[:N, 2] = r.integers(b_range[0], b_range[1], N, dtype=np.int64)
     cst[:N, 3] = w[:N].astype(np.int64).sum(1)
     return w, cst
 
@@ -47,14 +47,14 @@ class Case:
     """Host inputs + oracle + device run of one vgemm_hl2 call."""
 
     def __init__(self, src, M, N, K, epi=vg.EPI_PLAIN, seed=0, residual=False, rowmax=False, e_max=0, s_range=(20, 29),
-                 m_range=(1 << 14, 1 << 15), conv=None, lut=None, Cs=0):
+                 m_range=(1 << 14, 1 << 15), conv=None, lut=None, Cs=0, b_range=(-50000, 50000)):
         r = rng(seed)
         self.src, self.M, self.N, self.K, self.epi = src, M, N, K, epi
         self.Kp = cf.align(K, 16)
         self.Np = cf.align(N, 64)
         self.Mp = cf.align(M, 64)
         self.conv = conv
-        self.w, self.cst = make_w_cst(r, N, K, self.Np, self.Kp, s_range, m_range)
+        self.w, self.cst = make_w_cst(r, N, K, self.Np, self.Kp, s_range, m_range, b_range=b_range)
         self.e = r.integers(0, e_max + 1, M).astype(np.int32) if e_max else None
         self.kw = {}
         if src == vg.SRC_I8:
@@ -223,6 +223,20 @@ def test_exact_slow_path(src):
     K = 512
     for seed, s_range, m_range in [(1, (-6, 3), (1, 1 << 10)), (2, (50, 70), (1 << 14, 1 << 15)), (3, (20, 40), ((1 << 30), (1 << 31) - 1))]:
         Case(src, 200, 128, K, seed=seed, s_range=s_range, m_range=m_range, e_max=5, residual=True).check(what=f"slow {seed}")
+
+
+@pytest.mark.parametrize("epi", [vg.EPI_PLAIN, vg.EPI_GEGLU, vg.EPI_GELU])
+def test_fast_epilogue_branches(epi):
+    """The three FP64 epilogue branches with e == 0: b folded into the FMA constant (no element can
+    reach 2^31), b near +-2^31 (saturating add, not foldable), and a GEGLU product a*ge far beyond
+    2^31 with y itself in range (folded, saturating only at the last step)."""
+    cases = [
+        ("fold", dict(s_range=(16, 20), m_range=(1 << 10, 1 << 12))),
+        ("b near 2^31", dict(s_range=(16, 20), m_range=(1 << 10, 1 << 12), b_range=(-(2**31), 2**31))),
+        ("large y", dict(s_range=(16, 16), m_range=(1 << 16, 1 << 18))),
+    ]
+    for i, (name, kw) in enumerate(cases):
+        Case(vg.SRC_I16, 192, 128, 64, epi=epi, seed=40 + i, rowmax=True, residual=epi == vg.EPI_PLAIN, **kw).check(what=f"{name} epi {epi}")
 
 
 def test_lut_outside_range_takes_exact_path():

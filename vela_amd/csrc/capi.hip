@@ -69,16 +69,15 @@ constexpr int NCU = 256;   // MI355X compute units
 
 int cdiv(long long a, long long b) { return int((a + b - 1) / b); }
 
-// Tile variant: fewest rounds of the 256 CUs weighted by tile area (one 128x128 block per CU,
-// two of the half-size tiles).
+// Tile variant: the CU that receives the most tiles sets the time; a tile costs its area, and the
+// half-size tiles carry a fixed-overhead penalty (prologue, epilogue, fewer MFMAs per fragment load).
 int pick_variant(int M, int N) {
     int best = 0;
     double bestCost = 1e300;
     for (int v = 0; v < 3; ++v) {
         const long long tiles = (long long)cdiv(M, TILES[v].BM) * cdiv(N, TILES[v].BN);
-        const int slots = v == 0 ? NCU : 2 * NCU;
-        const double rounds = double((tiles + slots - 1) / slots);
-        const double cost = rounds * TILES[v].BM * TILES[v].BN / (v == 0 ? 1.0 : 2.0);
+        const double rounds = double((tiles + NCU - 1) / NCU);
+        const double cost = rounds * TILES[v].BM * TILES[v].BN * (v == 0 ? 1.0 : 1.15);
         if (cost < bestCost - 1e-9) { bestCost = cost; best = v; }
     }
     return best;

@@ -50,11 +50,14 @@ typedef Tile<128, 128, 4, 1> TileD0;
 typedef Tile<64, 128, 4, 1> TileD1;
 typedef Tile<128, 64, 4, 1> TileD2;
 
-// byte offset of 16-byte chunk `chunk` (0..3) of a 64-byte LDS row; the XOR keeps the 16 rows read
-// by one MFMA fragment load on 16 distinct bank groups
-__device__ __forceinline__ int swz(int row, int chunk) { return row * 64 + ((chunk ^ ((row >> 2) & 3)) << 4); }
-// byte offset of 16-byte chunk `chunk` (0..7) of a 128-byte LDS row (raw int16 activations)
-__device__ __forceinline__ int swz16(int row, int chunk) { return row * 128 + ((chunk ^ ((row >> 1) & 7)) << 4); }
+// Byte offset of 16-byte chunk `chunk` (0..3) of a 64-byte LDS row. The XOR makes the rows read
+// by one MFMA fragment load hit distinct bank groups whether the LDS serves 8 or 16 lanes of a
+// 16-byte read per cycle.
+__device__ __forceinline__ int swz(int row, int chunk) { return row * 64 + ((chunk ^ (((row >> 1) + (row >> 3)) & 3)) << 4); }
+// byte offset of 16-byte chunk `chunk` (0..7) of a 128-byte LDS row (raw int16 activations), same property
+__device__ __forceinline__ int swz16(int row, int chunk) { return row * 128 + ((chunk ^ ((row & 7) ^ ((row >> 3) & 1))) << 4); }
+__device__ __forceinline__ int swz_key(int row) { return ((row >> 1) + (row >> 3)) & 3; }
+__device__ __forceinline__ int swz16_key(int row) { return (row & 7) ^ ((row >> 3) & 1); }
 
 // LDS row of W-tile row `row`. For GEGLU the a-columns (even) go to the first half and the
 // g-columns (odd) to the second half, so a wave's a- and g-subtiles hold matching columns.
@@ -100,25 +103,26 @@ __device__ __forceinline__ void quant_pack16(const v4i* x, int e, unsigned* d) {
     }
 }
 
-// 16 int16 image values (two per dword, in place) quantised with shift e (quant16_32)
+// 16 int16 image values (two per dword, in place) quantised with shift 0: quant16_32(v, 0) =
+// max(v, -32767) for int16 v
+__device__ __forceinline__ void clamp16_pairs(unsigned* d) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const unsigned w = d[j];
+        s2 v = __builtin_bit_cast(s2, w);
+        v = __builtin_elementwise_max(v, s2{-32767, -32767});
+        d[j] = __builtin_bit_cast(unsigned, v);
+    }
+}
+
+// the same with any shift e in [0, 17] (quant16_32)
 __device__ __forceinline__ void quant16_pairs(unsigned* d, int e) {
-    if (e == 0) {
-        // quant16_32(v, 0) = max(v, -32767) for int16 v
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const unsigned w = d[j];
-            s2 v = __builtin_bit_cast(s2, w);
-            v = __builtin_elementwise_max(v, s2{-32767, -32767});
-            d[j] = __builtin_bit_cast(unsigned, v);
-        }
-    } else {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int w = int(d[j]);
-            const int q0 = quant16_32(int(short(w & 0xffff)), e);
-            const int q1 = quant16_32(w >> 16, e);
-            d[j] = __builtin_amdgcn_perm(unsigned(q1), unsigned(q0), 0x05040100u);
-        }
+    for (int j = 0; j < 8; ++j) {
+        const int w = int(d[j]);
+        const int q0 = quant16_32(int(short(w & 0xffff)), e);
+        const int q1 = quant16_32(w >> 16, e);
+        d[j] = __builtin_amdgcn_perm(unsigned(q1), unsigned(q0), 0x05040100u);
     }
 }
 
@@ -128,15 +132,15 @@ __device__ __forceinline__ void quant16_pairs(unsigned* d, int e) {
 template <int BN, bool LUT>
 struct EpiShared {
     double ms[BN];      // m * 2^-s
-    double wm[BN];      // 128 * wsum * m * 2^-s
-    double wmh[BN];     // wm + 1/2
+    double wm[BN];      // 128 * wsum * m * 2^-s; + 1/2 when e == 0, and + b as well when the block folds b
     int b[BN];
     int2 lut[LUT ? 2050 : 1];   // lut[i + 1] = (L[i], L[i+1] - L[i]); lut[0] below the table, lut[2049] above
-    int flag[6];        // emin, emax, smin, smax, column bound failed, table range failed
+    unsigned long long umax;    // bits of max over columns of 2^22*Kp*|m|*2^-s (a positive double)
+    int flag[8];        // emin, emax, smin, smax, column bound failed, table range failed, max |b|, b not foldable
 };
 
 struct EpiFlags {
-    bool fast, ezero;
+    bool fast, ezero, fold;
 };
 
 // Fill the epilogue constants of columns [n0, n0 + BN) (in LDS-row order) and decide whether the
@@ -147,7 +151,8 @@ __device__ __forceinline__ EpiFlags block_prologue(const GemmParams& p, int m0, 
     const int tid = threadIdx.x, lane = tid & 63;
     if (tid == 0) {
         sh.flag[0] = INT_MAX; sh.flag[1] = INT_MIN; sh.flag[2] = INT_MAX; sh.flag[3] = INT_MIN;
-        sh.flag[4] = 0; sh.flag[5] = 0;
+        sh.flag[4] = 0; sh.flag[5] = 0; sh.flag[6] = 0; sh.flag[7] = 0;
+        sh.umax = 0;
     }
     __syncthreads();
     // per-row shift range (one LDS atomic per wave)
@@ -172,10 +177,11 @@ __device__ __forceinline__ EpiFlags block_prologue(const GemmParams& p, int m0, 
         }
     }
     {
-        int smn = INT_MAX, smx = INT_MIN, bad = 0;
+        int smn = INT_MAX, smx = INT_MIN, bad = 0, bmx = 0, nofold = 0;
+        double um = 0.0;
         for (int j = tid; j < BN; j += 256) {
             const int n = n0 + wrow_of_lds<EPI, BN>(j);
-            double ms = 0.0, wmv = 0.0, wmh = 0.5;
+            double ms = 0.0, wmv = 0.0;
             int bb = 0;
             if (n < p.Nreal) {
                 const int4 c = p.cst[n];
@@ -186,17 +192,24 @@ __device__ __forceinline__ EpiFlags block_prologue(const GemmParams& p, int m0, 
                 if (c.y >= -1000 && c.y <= 1000) {
                     ms = ldexp(double(c.x), -c.y);
                     wmv = ldexp(128.0 * (double(c.w) * double(c.x)), -c.y);
-                    wmh = wmv + 0.5;
+                    // |acc*m*2^-s| <= 2^22*Kp*|m|*2^-s, since |acc| <= 32768*128*Kp
+                    um = max(um, ldexp(4194304.0 * double(p.Kp) * fabs(double(c.x)), -c.y));
+                    // wm + 1/2 + b is exact when |b|*2^s < 2^51 (numerator below 2^53)
+                    if (ldexp(fabs(double(c.z)), c.y) >= 2251799813685248.0) nofold = 1;
                 }
                 bb = c.z;
+                bmx = max(bmx, int(min(uabs(c.z), 0x7fffffffu)));
             }
-            sh.ms[j] = ms; sh.wm[j] = wmv; sh.wmh[j] = wmh; sh.b[j] = bb;
+            sh.ms[j] = ms; sh.wm[j] = wmv; sh.b[j] = bb;
         }
 #pragma unroll
         for (int o = 32; o; o >>= 1) {
             smn = min(smn, __shfl_xor(smn, o));
             smx = max(smx, __shfl_xor(smx, o));
             bad |= __shfl_xor(bad, o);
+            bmx = max(bmx, __shfl_xor(bmx, o));
+            nofold |= __shfl_xor(nofold, o);
+            um = max(um, __shfl_xor(um, o));
         }
         if (lane == 0) {
             if (smn <= smx) {
@@ -204,6 +217,9 @@ __device__ __forceinline__ EpiFlags block_prologue(const GemmParams& p, int m0, 
                 atomicMax(&sh.flag[3], smx);
             }
             if (bad) atomicOr(&sh.flag[4], 1);
+            atomicMax(&sh.flag[6], bmx);
+            if (nofold) atomicOr(&sh.flag[7], 1);
+            atomicMax(&sh.umax, __double_as_longlong(um));
         }
     }
     if constexpr (NEEDLUT) {
@@ -229,22 +245,32 @@ __device__ __forceinline__ EpiFlags block_prologue(const GemmParams& p, int m0, 
     f.fast = !sh.flag[4] && (smin - emax >= 1) && (smax - emin <= 52) && emin >= -1000 && emax <= 1000;
     if (NEEDLUT && sh.flag[5]) f.fast = false;
     f.ezero = emin > emax || (emin == 0 && emax == 0);
+    // fold: e == 0 and no element can saturate (|floor(X)| + |b| < 2^31), so y = floor(X + b) with b
+    // folded into the FMA constant and no saturating int steps
+    f.fold = f.fast && f.ezero && !sh.flag[7] && __longlong_as_double(sh.umax) + double(sh.flag[6]) + 2.0 < 2147483647.0;
+    if (f.ezero) {
+        // the FMA constant of the e == 0 forms: wm + 1/2, and + b when folded (exact, see above)
+        for (int j = tid; j < BN; j += 256) sh.wm[j] = (sh.wm[j] + 0.5) + (f.fold ? double(sh.b[j]) : 0.0);
+        __syncthreads();
+    }
     return f;
 }
 
 // The requantising epilogue of one wave. Subtile (ns, ms) of the wave holds rows
 // rbase + ms*16 + (lane & 15) and LDS-table rows wsub_row(wn, ns) + 4*(lane >> 4) + v, v = 0..3.
-template <int EPI, int SRC, class T, bool EZERO, bool SMALLK, class S>
+template <int EPI, int SRC, class T, bool EZERO, bool SMALLK, bool FOLD, class S>
 __device__ __forceinline__ void fused_epilogue_t(const GemmParams& p, const v4i (&acc_h)[T::NS][T::MS], const v4i (&acc_l)[T::NS][T::MS],
                                                  int rbase, int n0, int wn, const S& sh, bool fast, const int (&er)[T::MS]) {
+    static_assert(!FOLD || EZERO, "folding b assumes e == 0");
     constexpr int MS = T::MS, NS = T::NS;
     const int lane = threadIdx.x & 63, fr = lane & 15, fg = lane >> 4;
     double pr[MS];
 #pragma unroll
     for (int ms = 0; ms < MS; ++ms) pr[ms] = EZERO ? 1.0 : ldexp(1.0, min(max(er[ms], -1000), 1000));
-    uint32_t mx[MS];
+    // running max and min of y per row: max |y| = max(ymax, -ymin), two instructions per value
+    int ymax[MS], ymin[MS];
 #pragma unroll
-    for (int ms = 0; ms < MS; ++ms) mx[ms] = 0;
+    for (int ms = 0; ms < MS; ++ms) { ymax[ms] = 0; ymin[ms] = 0; }
 
     // A = 256*Chi + Clo as an exact double
     auto comb = [&](int h, int l) -> double {
@@ -269,6 +295,11 @@ __device__ __forceinline__ void fused_epilogue_t(const GemmParams& p, const v4i 
         const double P = __builtin_fma(double(y), double(phi(y)), 32768.0);
         return __builtin_floor(P * (1.0 / 65536.0));
     };
+    // the same from y held both as an int and as a double
+    auto gelu_fast2 = [&](int yi, double yd) -> double {
+        const double P = __builtin_fma(yd, double(phi(yi)), 32768.0);
+        return __builtin_floor(P * (1.0 / 65536.0));
+    };
 
     constexpr int NOUT = EPI == EPI_GEGLU ? NS / 2 : NS;
 #pragma unroll
@@ -284,11 +315,15 @@ __device__ __forceinline__ void fused_epilogue_t(const GemmParams& p, const v4i 
         if (fast) {
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
-                c_ms[v] = sh.ms[lr + v]; c_wmh[v] = sh.wmh[lr + v]; c_b[v] = sh.b[lr + v];
-                if constexpr (!EZERO) c_wm[v] = sh.wm[lr + v];
+                c_ms[v] = sh.ms[lr + v];
+                if constexpr (EZERO) c_wmh[v] = sh.wm[lr + v];
+                else c_wm[v] = sh.wm[lr + v];
+                if constexpr (!FOLD) c_b[v] = sh.b[lr + v];
                 if constexpr (EPI == EPI_GEGLU) {
-                    g_ms[v] = sh.ms[lg + v]; g_wmh[v] = sh.wmh[lg + v]; g_b[v] = sh.b[lg + v];
-                    if constexpr (!EZERO) g_wm[v] = sh.wm[lg + v];
+                    g_ms[v] = sh.ms[lg + v];
+                    if constexpr (EZERO) g_wmh[v] = sh.wm[lg + v];
+                    else g_wm[v] = sh.wm[lg + v];
+                    if constexpr (!FOLD) g_b[v] = sh.b[lg + v];
                 }
             }
         }
@@ -298,7 +333,23 @@ __device__ __forceinline__ void fused_epilogue_t(const GemmParams& p, const v4i 
             const int r = rbase + ms * 16 + fr;
             if (r >= p.Mreal) continue;
             int y[4];
-            if (fast) {
+            if (FOLD) {
+                // y = floor(A*m*2^-s + 1/2 + b): b folded into the constant, nothing saturates
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const double ya = __builtin_floor(__builtin_fma(comb(acc_h[ns][ms][v], acc_l[ns][ms][v]), c_ms[v], c_wmh[v]));
+                    if constexpr (EPI == EPI_GEGLU) {
+                        const double yg = __builtin_floor(__builtin_fma(comb(acc_h[ns + NS / 2][ms][v], acc_l[ns + NS / 2][ms][v]), g_ms[v], g_wmh[v]));
+                        const double ge = gelu_fast2(int(yg), yg);
+                        // (a*ge + 2^15) * 2^-16 with a pre-scaled by 2^-16 (exact: a power of two)
+                        y[v] = cvt_sat(__builtin_floor(__builtin_fma(ya * (1.0 / 65536.0), ge, 0.5)));
+                    } else if constexpr (EPI == EPI_GELU) {
+                        y[v] = int(gelu_fast2(int(ya), ya));
+                    } else {
+                        y[v] = int(ya);
+                    }
+                }
+            } else if (fast) {
 #pragma unroll
                 for (int v = 0; v < 4; ++v) {
                     const int ya = epi_fast(comb(acc_h[ns][ms][v], acc_l[ns][ms][v]), c_ms[v], c_wm[v], c_wmh[v], c_b[v], pr[ms]);
@@ -364,10 +415,9 @@ __device__ __forceinline__ void fused_epilogue_t(const GemmParams& p, const v4i 
                         if (ncol + v < nlim) d[v] = y[v];
                 }
                 if (p.rowmax) {
-                    // |y| as unsigned: max_i32(y, -y) is |y| except at INT_MIN, whose bits are 2^31
 #pragma unroll
                     for (int v = 0; v < 4; ++v)
-                        if (ncol + v < nlim) mx[ms] = max(mx[ms], uint32_t(max(y[v], -y[v])));
+                        if (ncol + v < nlim) { ymax[ms] = max(ymax[ms], y[v]); ymin[ms] = min(ymin[ms], y[v]); }
                 }
             }
         }
@@ -377,7 +427,7 @@ __device__ __forceinline__ void fused_epilogue_t(const GemmParams& p, const v4i 
             // lanes fr, fr+16, fr+32, fr+48 hold the same row: one atomic per row and wave
 #pragma unroll
             for (int ms = 0; ms < MS; ++ms) {
-                uint32_t m = mx[ms];
+                uint32_t m = max(uint32_t(ymax[ms]), uabs(ymin[ms]));
                 m = max(m, uint32_t(__shfl_xor(int(m), 16)));
                 m = max(m, uint32_t(__shfl_xor(int(m), 32)));
                 const int r = rbase + ms * 16 + fr;
@@ -391,12 +441,15 @@ template <int EPI, int SRC, class T, class S>
 __device__ __forceinline__ void fused_epilogue(const GemmParams& p, const v4i (&acc_h)[T::NS][T::MS], const v4i (&acc_l)[T::NS][T::MS],
                                                int rbase, int n0, int wn, const S& sh, EpiFlags f, const int (&er)[T::MS]) {
     const bool smallK = p.Kp <= 496;   // |256*Chi + Clo| < 2^31
-    if (f.ezero) {
-        if (smallK) fused_epilogue_t<EPI, SRC, T, true, true>(p, acc_h, acc_l, rbase, n0, wn, sh, f.fast, er);
-        else fused_epilogue_t<EPI, SRC, T, true, false>(p, acc_h, acc_l, rbase, n0, wn, sh, f.fast, er);
+    if (f.fold) {
+        if (smallK) fused_epilogue_t<EPI, SRC, T, true, true, true>(p, acc_h, acc_l, rbase, n0, wn, sh, f.fast, er);
+        else fused_epilogue_t<EPI, SRC, T, true, false, true>(p, acc_h, acc_l, rbase, n0, wn, sh, f.fast, er);
+    } else if (f.ezero) {
+        if (smallK) fused_epilogue_t<EPI, SRC, T, true, true, false>(p, acc_h, acc_l, rbase, n0, wn, sh, f.fast, er);
+        else fused_epilogue_t<EPI, SRC, T, true, false, false>(p, acc_h, acc_l, rbase, n0, wn, sh, f.fast, er);
     } else {
-        if (smallK) fused_epilogue_t<EPI, SRC, T, false, true>(p, acc_h, acc_l, rbase, n0, wn, sh, f.fast, er);
-        else fused_epilogue_t<EPI, SRC, T, false, false>(p, acc_h, acc_l, rbase, n0, wn, sh, f.fast, er);
+        if (smallK) fused_epilogue_t<EPI, SRC, T, false, true, false>(p, acc_h, acc_l, rbase, n0, wn, sh, f.fast, er);
+        else fused_epilogue_t<EPI, SRC, T, false, false, false>(p, acc_h, acc_l, rbase, n0, wn, sh, f.fast, er);
     }
 }
 
@@ -496,12 +549,9 @@ __global__ void __launch_bounds__(256, 2) gemm_dma_kernel(const GemmParams p) {
 
     const char* a0p = static_cast<const char*>(p.a0) + (EPI == EPI_RAW ? bt * p.sA : 0);
     const int8_t* wp = p.w + (EPI == EPI_RAW ? bt * p.sW : 0);
-    const v4i rW = make_rsrc_words(wp, p.w_bytes);
+    const v4i rW = make_rsrc_words(wp, p.w_bytes);   // scalar registers
     const v4i rA0 = make_rsrc_words(a0p, p.a0_bytes);
     const v4i rA1 = make_rsrc_words(SRC == SRC_I8 && TWO ? p.a1 : a0p, SRC == SRC_I8 && TWO ? p.a1_bytes : p.a0_bytes);
-
-    EpiFlags fl{true, true};
-    if constexpr (FUSED) fl = block_prologue<EPI, SRC, BM, BN>(p, m0, n0, sh);
 
     // rows owned by this wave and their shifts (for the epilogue and the image quantisation)
     const int rbase = m0 + wave * T::WTM;
@@ -513,71 +563,124 @@ __global__ void __launch_bounds__(256, 2) gemm_dma_kernel(const GemmParams p) {
     }
 
     // ---- DMA address state. W: wave instruction j covers LDS rows 16*(wave*W_INS + j) + lane/4,
-    // chunk position lane%4 (holding global chunk cp ^ swizzle). A (raw int16): rows
-    // 8*(wave*A_INS + j) + lane/8, chunk position lane%8. A (int8 planes): like W, hi then lo.
-    int w_row[D::W_INS], w_kc[D::W_INS];
+    // chunk position lane%4 (holding the global chunk that the swizzle puts there). A (raw int16):
+    // rows 8*(wave*A_INS + j) + lane/8, chunk position lane%8. A (int8 planes): like W, hi then lo.
+    // Per-lane byte offsets are fixed over the K loop; each K step adds a scalar offset, and only
+    // the last, partial K step checks columns lane by lane.
+    unsigned w_off[D::W_INS];
+    int w_k[D::W_INS];
 #pragma unroll
     for (int j = 0; j < D::W_INS; ++j) {
         const int lr = 16 * (wave * D::W_INS + j) + (lane >> 2);
-        w_row[j] = n0 + (FUSED ? wrow_of_lds<EPI, BN>(lr) : lr);
-        w_kc[j] = (lane & 3) ^ ((lr >> 2) & 3);
+        const int nrow = n0 + (FUSED ? wrow_of_lds<EPI, BN>(lr) : lr);
+        w_k[j] = 16 * ((lane & 3) ^ swz_key(lr));
+        w_off[j] = nrow < p.Nreal ? unsigned(nrow) * unsigned(p.ldw) + unsigned(w_k[j]) : OOB;
     }
     constexpr int A_ROWS_INS = D::RAW16 ? 8 : 16;                      // rows per DMA instruction
     constexpr int A_INS_PLANE = D::RAW16 ? D::A_INS : D::A_INS / (TWO ? 2 : 1);
-    int a_r[A_INS_PLANE], a_c[A_INS_PLANE];
-    int a_b[A_INS_PLANE], a_iy0[A_INS_PLANE], a_ix0[A_INS_PLANE];
+    unsigned a_off[A_INS_PLANE];
+    int a_k[A_INS_PLANE], a_pix[A_INS_PLANE];
+    unsigned a_mask[A_INS_PLANE];
+    // SRC_CONV16 with C % 64 == 0: a 64-wide K step never straddles a 3x3 tap, so the tap and the
+    // channel offset of a step are block-wide scalars and each lane only checks its tap mask
+    const bool conv_fast = SRC == SRC_CONV16 && (p.C & 63) == 0;
+    const unsigned cmagic = SRC == SRC_CONV16 ? unsigned((0x100000000ull + unsigned(p.C) - 1) / unsigned(p.C)) : 0u;
 #pragma unroll
     for (int j = 0; j < A_INS_PLANE; ++j) {
         const int row = A_ROWS_INS * (wave * A_INS_PLANE + j) + (D::RAW16 ? (lane >> 3) : (lane >> 2));
-        a_r[j] = m0 + row;
-        a_c[j] = D::RAW16 ? ((lane & 7) ^ ((row >> 1) & 7)) : ((lane & 3) ^ ((row >> 2) & 3));
-        if constexpr (SRC == SRC_CONV16) {
+        const int r = m0 + row;
+        const bool rok = r < p.Mreal;
+        if constexpr (D::RAW16) a_k[j] = 8 * ((lane & 7) ^ swz16_key(row));
+        else a_k[j] = 16 * ((lane & 3) ^ swz_key(row));
+        if constexpr (SRC == SRC_I16) {
+            a_off[j] = rok ? (unsigned(r) * unsigned(p.lda) + unsigned(a_k[j])) * 2u : OOB;
+        } else if constexpr (SRC == SRC_CONV16) {
             const int HoWo = p.Ho * p.Wo;
-            const int rr = a_r[j] < p.Mreal ? a_r[j] : 0;
+            const int rr = rok ? r : 0;
             const int b = rr / HoWo, pp = rr - b * HoWo, oy = pp / p.Wo, ox = pp - oy * p.Wo;
-            a_b[j] = b * p.H;
-            a_iy0[j] = a_r[j] < p.Mreal ? oy * p.stride - 1 : -(1 << 20);   // rows past Mreal read nothing
-            a_ix0[j] = ox * p.stride - 1;
+            const int iy0 = oy * p.stride - 1, ix0 = ox * p.stride - 1;
+            unsigned mask = 0;
+#pragma unroll
+            for (int t = 0; t < 9; ++t) {
+                const int iy = iy0 + t / 3, ix = ix0 + t % 3;
+                mask |= unsigned(rok && iy >= 0 && iy < p.H && ix >= 0 && ix < p.W) << t;
+            }
+            a_mask[j] = mask;
+            // byte offset of channel a_k of pixel (iy0, ix0); negative at the border, but only taps
+            // inside the image are ever added to it
+            a_pix[j] = (((b * p.H + iy0) * p.W + ix0) * p.C + a_k[j]) * 2;
+            a_off[j] = unsigned(a_pix[j]);
+        } else {
+            a_off[j] = rok ? unsigned(r) * unsigned(p.lda) + unsigned(a_k[j]) : OOB;
         }
     }
-    const unsigned cmagic = SRC == SRC_CONV16 ? unsigned((0x100000000ull + unsigned(p.C) - 1) / unsigned(p.C)) : 0u;
 
     auto issue = [&](int kt, int stage) {
         const unsigned sbase = lds_addr(smem) + stage * D::STAGE;
         const int kbase = kt * 64;
+        const bool wtail = kbase + 64 > p.Kp;
 #pragma unroll
         for (int j = 0; j < D::W_INS; ++j) {
-            const int n = w_row[j], k = kbase + 16 * w_kc[j];
-            const unsigned off = (n < p.Nreal && k < p.Kp) ? unsigned(n) * unsigned(p.ldw) + unsigned(k) : OOB;
-            dma16(rW, off, sbase + (wave * D::W_INS + j) * 1024);
+            const unsigned off = (wtail && kbase + w_k[j] >= p.Kp) ? OOB : w_off[j];
+            dma16(rW, off, unsigned(kbase), sbase + (wave * D::W_INS + j) * 1024);
         }
         const unsigned sA = sbase + D::W_BYTES;
+        if constexpr (SRC == SRC_I16) {
+            const bool atail = kbase + 64 > p.K;
 #pragma unroll
-        for (int j = 0; j < A_INS_PLANE; ++j) {
-            const int r = a_r[j];
-            if constexpr (SRC == SRC_I16) {
-                const int k = kbase + 8 * a_c[j];
-                const unsigned off = (r < p.Mreal && k < p.K) ? (unsigned(r) * unsigned(p.lda) + unsigned(k)) * 2u : OOB;
-                dma16(rA0, off, sA + (wave * A_INS_PLANE + j) * 1024);
-            } else if constexpr (SRC == SRC_CONV16) {
+            for (int j = 0; j < A_INS_PLANE; ++j) {
+                const unsigned off = (atail && kbase + a_k[j] >= p.K) ? OOB : a_off[j];
+                dma16(rA0, off, unsigned(kbase) * 2u, sA + (wave * A_INS_PLANE + j) * 1024);
+            }
+        } else if constexpr (SRC == SRC_CONV16) {
+            if (conv_fast) {
                 // implicit 3x3 im2col, tap-major K: k = tap*C + c (src/gemm_hl.cu:104-114)
-                const int k = kbase + 8 * a_c[j];
-                const int tap = int(__umulhi(unsigned(k), cmagic));
-                const int ch = k - tap * p.C;
+                const int tap = kbase / p.C, c0 = kbase - tap * p.C;
                 const int ky = (tap * 11) >> 5, kx = tap - 3 * ky;   // tap / 3, tap % 3 for tap < 9
-                const int iy = a_iy0[j] + ky, ix = a_ix0[j] + kx;
-                const bool ok = k < p.K && iy >= 0 && iy < p.H && ix >= 0 && ix < p.W;
-                const unsigned off = ok ? ((unsigned(a_b[j] + iy) * unsigned(p.W) + unsigned(ix)) * unsigned(p.C) + unsigned(ch)) * 2u : OOB;
-                dma16(rA0, off, sA + (wave * A_INS_PLANE + j) * 1024);
+                const int soff = ((ky * p.W + kx) * p.C + c0) * 2;
+#pragma unroll
+                for (int j = 0; j < A_INS_PLANE; ++j) {
+                    const bool ok = tap < 9 && ((a_mask[j] >> tap) & 1u);
+                    dma16(rA0, ok ? unsigned(a_pix[j] + soff) : OOB, 0u, sA + (wave * A_INS_PLANE + j) * 1024);
+                }
             } else {
-                const int k = kbase + 16 * a_c[j];
-                const unsigned off = (r < p.Mreal && k < p.Kp) ? unsigned(r) * unsigned(p.lda) + unsigned(k) : OOB;
-                dma16(rA0, off, sA + (wave * A_INS_PLANE + j) * 1024);
-                if constexpr (TWO)
-                    dma16(rA1, off, sA + BM * 64 + (wave * A_INS_PLANE + j) * 1024);
+#pragma unroll
+                for (int j = 0; j < A_INS_PLANE; ++j) {
+                    const int k = kbase + a_k[j];
+                    const int tap = int(__umulhi(unsigned(k), cmagic));
+                    const int ch = k - tap * p.C;
+                    const int ky = (tap * 11) >> 5, kx = tap - 3 * ky;
+                    const bool ok = k < p.K && ((a_mask[j] >> tap) & 1u);
+                    const int off = a_pix[j] - a_k[j] * 2 + ((ky * p.W + kx) * p.C + ch) * 2;
+                    dma16(rA0, ok ? unsigned(off) : OOB, 0u, sA + (wave * A_INS_PLANE + j) * 1024);
+                }
+            }
+        } else {
+            const bool atail = kbase + 64 > p.Kp;
+#pragma unroll
+            for (int j = 0; j < A_INS_PLANE; ++j) {
+                const unsigned off = (atail && kbase + a_k[j] >= p.Kp) ? OOB : a_off[j];
+                dma16(rA0, off, unsigned(kbase), sA + (wave * A_INS_PLANE + j) * 1024);
+                if constexpr (TWO) dma16(rA1, off, unsigned(kbase), sA + BM * 64 + (wave * A_INS_PLANE + j) * 1024);
             }
         }
     };
+
+    // the first stages load while the block prologue runs
+    const int n = ke - kb;
+#pragma unroll
+    for (int s = 0; s < NST - 1; ++s)
+        if (s < n) issue(kb + s, s);
+
+    EpiFlags fl{true, true, false};
+    if constexpr (FUSED) fl = block_prologue<EPI, SRC, BM, BN>(p, m0, n0, sh);
+
+    // image rows of this wave all have e == 0 (the usual case): a clamp is the whole quantisation.
+    // Decided per wave, so that the compiler branches instead of evaluating both forms.
+    bool e_any = false;
+#pragma unroll
+    for (int ms = 0; ms < MS; ++ms) e_any |= er[ms] != 0;
+    const bool wave_e0 = SRC == SRC_CONV16 ? __builtin_amdgcn_ballot_w64(e_any) == 0 : true;
 
     v4i acc_h[NS][MS], acc_l[TWO ? NS : 1][TWO ? MS : 1];
 #pragma unroll
@@ -601,7 +704,10 @@ __global__ void __launch_bounds__(256, 2) gemm_dma_kernel(const GemmParams p) {
                 const v4i x1 = *reinterpret_cast<const v4i*>(sA + swz16(row, 2 * fg + 1));
                 unsigned d[8] = {unsigned(x0[0]), unsigned(x0[1]), unsigned(x0[2]), unsigned(x0[3]),
                                  unsigned(x1[0]), unsigned(x1[1]), unsigned(x1[2]), unsigned(x1[3])};
-                if constexpr (SRC == SRC_CONV16) quant16_pairs(d, er[ms]);
+                if constexpr (SRC == SRC_CONV16) {
+                    if (wave_e0) clamp16_pairs(d);
+                    else quant16_pairs(d, er[ms]);
+                }
                 split16x16(d, hf[ms], lf[ms]);
             } else {
                 hf[ms] = *reinterpret_cast<const v4i*>(sA + swz(row, fg));
@@ -620,26 +726,23 @@ __global__ void __launch_bounds__(256, 2) gemm_dma_kernel(const GemmParams p) {
         }
     };
 
-    // ---- main loop: NST-stage LDS ring, loads NST-1 steps ahead of the MFMAs.
+    // ---- main loop: NST-stage LDS ring, loads NST-1 steps ahead of the MFMAs, unrolled by NST so
+    // that every LDS address is an immediate offset.
     // Every ordinary load above completes here, with a wait the compiler sees; otherwise it places
     // that wait at the first use, inside the loop, where it would also drain the stage prefetch.
     __builtin_amdgcn_s_waitcnt(0);
-    const int n = ke - kb;
-    if (n > 0) {
+    for (int s0 = 0; s0 < n; s0 += NST) {
 #pragma unroll
-        for (int s = 0; s < NST - 1; ++s)
-            if (s < n) issue(kb + s, s);
-        for (int s = 0; s < n; ++s) {
-            // this stage's DMA done (the next stage's may still be in flight), then publish it
-            if constexpr (NST == 3) {
-                if (s + 1 < n) vm_wait<D::PER_STAGE>();
+        for (int u = 0; u < NST; ++u) {
+            const int s = s0 + u;
+            if (s < n) {
+                // this stage's DMA done (the next stage's may still be in flight), then publish it
+                if (NST == 3 && s + 1 < n) vm_wait<D::PER_STAGE>();
                 else vm_wait<0>();
-            } else {
-                vm_wait<0>();
+                block_barrier();
+                if (s + NST - 1 < n) issue(kb + s + NST - 1, (u + NST - 1) % NST);
+                compute(u);
             }
-            block_barrier();
-            if (s + NST - 1 < n) issue(kb + s + NST - 1, (s + NST - 1) % NST);
-            compute(s % NST);
         }
     }
 
@@ -676,7 +779,7 @@ __global__ void __launch_bounds__(256) gemm_hl_kernel(const GemmParams p) {
     const __amdgpu_buffer_rsrc_t rW = make_rsrc(p.w, p.w_bytes);
     const __amdgpu_buffer_rsrc_t rA0 = make_rsrc(p.a0, p.a0_bytes);
 
-    EpiFlags fl{true, true};
+    EpiFlags fl{true, true, false};
     if constexpr (FUSED) fl = block_prologue<EPI, SRC, BM, BN>(p, m0, n0, sh);
 
     const int rbase = m0 + wm * T::WTM;

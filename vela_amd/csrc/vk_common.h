@@ -131,12 +131,16 @@ __device__ __forceinline__ v4i make_rsrc_words(const void* base, unsigned bytes)
     return v4i{int(unsigned(a)), int(unsigned(a >> 32) & 0xffffu), int(bytes), RSRC_WORD3};
 }
 
-// HBM -> LDS without registers: each lane's 16 bytes at buffer offset `off` land at LDS byte
-// address lds + 16 * lane (buffer_load_dwordx4 ... lds, M0 = LDS base). Issued from asm so that
-// the compiler does not wait for it before every barrier and LDS read: completion is awaited
-// explicitly with vm_wait<N>() before the barrier that publishes the stage.
-__device__ __forceinline__ void dma16(v4i rsrc, unsigned off, unsigned lds) {
-    asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" : : "v"(off), "s"(rsrc), "s"(lds) : "memory");
+// HBM -> LDS without registers: each lane's 16 bytes at buffer offset `off` + `soff` land at LDS
+// byte address lds + 16 * lane (buffer_load_dwordx4 ... lds, M0 = LDS base). Lanes whose `off` is
+// at or above 2^31 read zeros. Issued from asm so that the compiler does not wait for it before
+// every barrier and LDS read: completion is awaited explicitly with vm_wait<N>() before the barrier
+// that publishes the stage.
+__device__ __forceinline__ void dma16(v4i rsrc, unsigned off, unsigned soff, unsigned lds) {
+    // both are wave-uniform by construction; readfirstlane states it where the compiler cannot prove it
+    soff = __builtin_amdgcn_readfirstlane(soff);
+    lds = __builtin_amdgcn_readfirstlane(lds);
+    asm volatile("s_mov_b32 m0, %3\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds" : : "v"(off), "s"(rsrc), "s"(soff), "s"(lds) : "memory");
 }
 
 template <int N>
