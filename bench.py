@@ -5,13 +5,16 @@ One "step" is one launch of the headline GEMM: config C2, the GEGLU FF up-projec
 latent at batch 8 (A int16 [32768 x 320], W int8 [2560 x 320] with interleaved a/g rows, per-column
 requantisation, GEGLU epilogue to int32 [32768 x 1280] + per-row max). Inputs are seeded synthetic
 data resident in HBM before the timed region. `value` is effective int8 TOPS = 4*M*N*K / time (two
-int8 passes, 2 ops per MAC, real M, N, K).
+int8 passes, 2 ops per MAC, real M, N, K), timed with HIP events on the launch stream.
 
-Also reported on the same JSON line: the roofline of that kernel (MFMA peak 5.0 POPS dense int8),
-the 194-GEMM UNet set (config C5) as one hipGraph in ms per replay, every other config's time, and
-the CPU baseline (the oracle restatement of the reference's integer semantics, timed on this host).
+Also reported on the same JSON line: the roofline of that kernel (the larger of its MFMA time at
+5.0 POPS dense int8 and its HBM time at 8 TB/s bounds it), the HBM traffic per launch from the
+committed rocprofv3 counter summary, the 194-GEMM UNet set (config C5) as one hipGraph in ms per
+replay, every other config's time, and the CPU baseline: the oracle restatement of the reference's
+integer semantics (the reference has no CPU GEMM of its own), timed on this host's cores.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-unet] [--no-cpu] [--no-configs]
+       python bench.py --only {c1,c2,c2plain,c3,c4a,c4b,c4c,copy}   (one kernel, for profiler runs)
 """
 from __future__ import annotations
 
@@ -30,7 +33,8 @@ PEAK_HBM_GBS = 8000.0        # MI355X HBM3E, 8 TB/s
 METRIC = "effective W8A16 TOPS & % int8 MFMA peak; UNet GEMM-set ms at batch 8"
 
 
-ONLY_NAMES = ("c1", "c2", "c2plain", "c3", "c4a", "c4b", "c4c")
+ONLY_NAMES = ("c1", "c2", "c2plain", "c3", "c4a", "c4b", "c4c", "copy")
+COPY_BYTES = 256 << 20       # the calibration copy of --only copy: 256 MiB read + 256 MiB written
 
 
 def only_layer(name):
@@ -63,44 +67,78 @@ def time_launches(fn, stream, steps, warmup):
 
 
 def pmc_traffic():
-    """HBM bytes per launch of the C2 kernel from the committed rocprofv3 PMC summary, if present."""
+    """HBM bytes per launch of the C2 kernel from the committed rocprofv3 counter summary, if present."""
     p = ROOT / "profiles" / "c2_geglu_pmc.json"
     if p.exists():
         try:
             d = json.loads(p.read_text())
             return d.get("hbm_bytes_per_launch"), d.get("source")
-        except Exception:
+        except (OSError, ValueError):
             return None, None
     return None, None
 
 
-def cpu_baseline(L, h, reps=3):
+def roofline(ops, nbytes, seconds):
+    """The roof that bounds a kernel is the larger of its MFMA time and its HBM time."""
+    t_mfma = ops / (PEAK_INT8_TOPS * 1e12)
+    t_hbm = nbytes / (PEAK_HBM_GBS * 1e9)
+    if t_hbm > t_mfma:
+        achieved = nbytes / seconds / 1e9
+        return {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": round(achieved / PEAK_HBM_GBS, 4)}
+    achieved = ops / seconds / 1e12
+    return {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_INT8_TOPS, "unit": "TOP/s",
+            "frac": round(achieved / PEAK_INT8_TOPS, 4)}
+
+
+def cpu_time(L, h, reps, rows=None):
     import numpy as np
 
     import oracle
 
-    threads = oracle.lib().orc_get_threads()
     times = []
     for _ in range(reps):
         t = time.perf_counter()
-        oracle.layer_reference(L, h)
+        oracle.layer_reference(L, h, rows=rows)
         times.append(time.perf_counter() - t)
-    tmed = float(np.median(times))
-    # one thread on a 2048-row sample
+    return float(np.median(times))
+
+
+def cpu_baseline(L, h, unet_fraction=4):
+    """The oracle on this host: the full C2 GEMM (median of 5) at all cores and a 2048-row sample on
+    one core, and the C5 set with every layer run on its first 1/unet_fraction rows (time scaled by
+    M / rows: each output row costs the same)."""
+    import oracle
+    from vela_amd import configs as cf
+
+    threads = oracle.lib().orc_get_threads()
+    tmed = cpu_time(L, h, 5)
     oracle.set_threads(1)
     rows = 2048
-    t = time.perf_counter()
-    oracle.layer_reference(L, h, rows=(0, rows))
-    t1 = time.perf_counter() - t
+    t1 = cpu_time(L, h, 1, rows=(0, rows))
     oracle.set_threads(0)
-    return {
+    out = {
         "value": round(L.ops / tmed / 1e12, 4), "unit": "TOPS", "cores": threads, "kind": "port",
-        "sample": f"full C2 GEMM ({L.M}x{L.K}x{L.N}, GEGLU + rowmax) by the C oracle (oracle/oracle.c, OpenMP), median of {reps}",
+        "sample": f"the full C2 GEMM ({L.M}x{L.K}x{L.N}, GEGLU + rowmax) by the C oracle (oracle/oracle.c, OpenMP "
+                  f"over rows, {threads} threads), median of 5",
         "ms": round(tmed * 1e3, 2),
         "one_thread": {"value": round(L.ops * rows / L.M / t1 / 1e12, 5), "unit": "TOPS", "cores": 1,
                         "sample": f"first {rows} rows of C2"},
         "cpu": _cpu_model(),
     }
+    if unet_fraction:
+        total = 0.0
+        t_all = time.perf_counter()
+        for Lu in cf.unet_layers():
+            hu = cf.make_host(Lu)
+            if Lu.meta.get("conv_in"):
+                hu = cf.unet_conv_in_operand(Lu, hu)
+            r1 = max(1, -(-Lu.M // unet_fraction))
+            total += cpu_time(Lu, hu, 1, rows=(0, r1)) * Lu.M / r1
+        out["unet_gemm_set_ms"] = round(total * 1e3, 1)
+        out["unet_sample"] = (f"all 194 C5 layers, each on its first ceil(M/{unet_fraction}) rows, time scaled by "
+                              f"M/rows ({time.perf_counter() - t_all:.1f} s wall including input generation)")
+    return out
 
 
 def _cpu_model():
@@ -139,6 +177,15 @@ def main():
     dev = torch.device("cuda:0")
     stream = torch.cuda.Stream(device=dev)
 
+    if args.only == "copy":
+        # calibration kernel for the HBM byte counters: a plain device copy of known size
+        src = torch.empty(COPY_BYTES // 4, dtype=torch.int32, device=dev).fill_(7)
+        dst = torch.empty_like(src)
+        with torch.cuda.stream(stream):
+            t = time_launches(lambda: dst.copy_(src), stream, args.steps, args.warmup)
+        log(f"[bench] copy {COPY_BYTES >> 20} MiB: {t * 1e3:.2f} us/launch, {2 * COPY_BYTES / (t * 1e-3) / 1e9:.0f} GB/s")
+        print(json.dumps({"workload": "copy", "bytes_read": COPY_BYTES, "bytes_written": COPY_BYTES, "us": round(t * 1e3, 3)}), flush=True)
+        return
     if args.only:
         L = only_layer(args.only)
         p = cf.DeviceProblem(L)
@@ -160,6 +207,12 @@ def main():
     log(f"[bench] {L.name}: {ms * 1e3:.1f} us/launch, {tops:.1f} TOPS ({100 * tops / PEAK_INT8_TOPS:.1f}% of int8 peak)")
     traffic, traffic_src = pmc_traffic()
 
+    roof = roofline(L.ops, L.hbm_bytes, ms * 1e-3)
+    roof["traffic"] = traffic
+    roof.update({"traffic_source": traffic_src, "kernel": "vk::gemm_dma_kernel<SRC_I16, EPI_GEGLU, Tile<128,128,4,1>>",
+                 "algorithmic_ops_per_launch": L.ops, "algorithmic_bytes_per_launch": L.hbm_bytes,
+                 "mfma_frac": round(tops / PEAK_INT8_TOPS, 4),
+                 "hbm_frac": round(L.hbm_bytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)})
     out = {
         "metric": METRIC,
         "value": round(tops, 2),
@@ -176,11 +229,7 @@ def main():
         "config": {"workload": "C2: W8A16 GEGLU up-proj, A int16 [32768x320] x W int8 [320x2560] -> int32 [32768x1280] + rowmax",
                    "M": L.M, "K": L.K, "N": L.N, "epilogue": "GEGLU + rowmax", "source": "SRC_I16"},
         "pct_int8_peak": round(100 * tops / PEAK_INT8_TOPS, 2),
-        "roofline": {"bound": "mfma", "achieved": round(tops, 2), "peak": PEAK_INT8_TOPS, "unit": "TOP/s",
-                     "frac": round(tops / PEAK_INT8_TOPS, 4),
-                     "traffic": traffic, "traffic_source": traffic_src,
-                     "algorithmic_ops_per_launch": L.ops, "algorithmic_bytes_per_launch": L.hbm_bytes,
-                     "hbm_gbs_algorithmic": round(L.hbm_bytes / (ms * 1e-3) / 1e9, 1), "hbm_peak_gbs": PEAK_HBM_GBS},
+        "roofline": roof,
     }
 
     # ---- the other configurations (one line each in "configs")
@@ -193,7 +242,10 @@ def main():
             t = time_launches(lambda: p.run(stream=stream), stream, max(5, args.steps), 3)
             table[Lc.name] = {"us": round(t * 1e3, 2), "tops": round(Lc.ops / (t * 1e-3) / 1e12, 2),
                               "pct_int8_peak": round(100 * Lc.ops / (t * 1e-3) / 1e12 / PEAK_INT8_TOPS, 2),
-                              "gbs_algorithmic": round(Lc.hbm_bytes / (t * 1e-3) / 1e9, 1)}
+                              "gbs_algorithmic": round(Lc.hbm_bytes / (t * 1e-3) / 1e9, 1),
+                              "roofline": roofline(Lc.ops, Lc.hbm_bytes, t * 1e-3)}
+            if not args.no_cpu:
+                table[Lc.name]["cpu_ms"] = round(cpu_time(Lc, p.h, 3) * 1e3, 2)
             log(f"[bench] {Lc.name}: {table[Lc.name]}")
             del p
         out["configs"] = table
@@ -216,8 +268,10 @@ def main():
     # ---- CPU baseline (rank 0, N = 1)
     if not args.no_cpu:
         log("[bench] CPU baseline (oracle)")
-        out["cpu_baseline"] = cpu_baseline(L, prob.h)
+        out["cpu_baseline"] = cpu_baseline(L, prob.h, unet_fraction=0 if args.no_unet else 4)
         out["gpu_over_cpu"] = round(tops / out["cpu_baseline"]["value"], 1)
+        if "unet_gemm_set_ms" in out and "unet_gemm_set_ms" in out["cpu_baseline"]:
+            out["unet_gpu_over_cpu"] = round(out["cpu_baseline"]["unet_gemm_set_ms"] / out["unet_gemm_set_ms"], 1)
     print(json.dumps(out), flush=True)
 
 

@@ -1,0 +1,58 @@
+// The producers and epilogues of the reference's src/kernels.h (emanwrxsti/vela) that feed and
+// finish the GEMM path, as drop-in meow:: functions over libvgemm.so (include/vgemm.h). Only the
+// GEMM-path kernels are here; norms, attention and the rest of src/kernels.h are not part of this
+// library. Errors throw std::runtime_error.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+
+#include "../vgemm.h"
+
+namespace meow {
+
+namespace detail {
+inline void kcheck(int rc) {
+    if (rc != VGEMM_OK) throw std::runtime_error(std::string(vgemm_last_error()));
+}
+}  // namespace detail
+
+struct GnStat;   // src/kernels.h:9 (GroupNorm statistics are not implemented here)
+
+// src/kernels.h:11-12
+inline void k_quant_rows(hipStream_t st, const int32_t* X, int M, int K, int ldx, int8_t* hi, int8_t* lo, int32_t* e, int Kp) {
+    detail::kcheck(vgemm_quant_rows(st, X, M, K, ldx, hi, lo, e, Kp));
+}
+
+// src/kernels.h:13-16 (gs must be null: GroupNorm statistics are not implemented)
+inline void k_epilogue(hipStream_t st, const int32_t* Chi, const int32_t* Clo, int M, int N, int ldc, const int4* cst, const int32_t* e,
+                       int32_t* Y, int ldy, const int32_t* residual = nullptr, GnStat* gs = nullptr, int T = 0) {
+    (void)T;
+    if (gs) throw std::runtime_error("k_epilogue: GroupNorm statistics are not implemented");
+    detail::kcheck(vgemm_epilogue(st, Chi, Clo, M, N, ldc, reinterpret_cast<const int32_t*>(cst), e, Y, ldy, residual));
+}
+
+// src/kernels.h:17-18
+inline void k_pixmax(hipStream_t st, const int32_t* X, int rows, int C, uint32_t* pm) { detail::kcheck(vgemm_pixmax(st, X, rows, C, pm)); }
+
+// src/kernels.h:19-21 (K index tap-major: tap*C + c, tap = 3*ky + kx, as src/test_im2col.cu:41 checks)
+inline void k_im2col3(hipStream_t st, const int32_t* X, const uint32_t* pm, int B, int H, int W, int C, int stride, int8_t* hi, int8_t* lo,
+                      int32_t* e, int Kp) {
+    detail::kcheck(vgemm_im2col3(st, X, pm, B, H, W, C, stride, hi, lo, e, Kp));
+}
+
+// src/kernels.h:67-68
+inline void k_epilogue_split(hipStream_t st, const int32_t* Chi, const int32_t* Clo, int M, int N, int ldc, const int4* cst, const int32_t* e,
+                             int Cs, int32_t* Y0, int32_t* Y1, int32_t* Y2) {
+    detail::kcheck(vgemm_epilogue_split(st, Chi, Clo, M, N, ldc, reinterpret_cast<const int32_t*>(cst), e, Cs, Y0, Y1, Y2));
+}
+
+// src/kernels.h:69-70
+inline void k_epilogue_geglu_q(hipStream_t st, const int32_t* Chi, const int32_t* Clo, int M, int F, int ldc, const int4* cst,
+                               const int32_t* e, const int32_t* Lphi, int8_t* hi, int8_t* lo, int32_t* eo, int Kp) {
+    detail::kcheck(vgemm_epilogue_geglu_q(st, Chi, Clo, M, F, ldc, reinterpret_cast<const int32_t*>(cst), e, Lphi, hi, lo, eo, Kp));
+}
+
+}  // namespace meow

@@ -46,7 +46,7 @@ typedef struct VgemmASrc {
     const int32_t* x; int ldx; const uint32_t* rowmax; int K;              /* SRC_X32 (K = real columns) */
     const int32_t* img; int H, W, C, stride, Ho, Wo;                       /* SRC_CONV32 (K = 9C, C % 16 == 0) */
     const int16_t* q16; int ld16;                                          /* SRC_I16 (K % 8, ld16 % 8) */
-    const int16_t* img16;                                                  /* SRC_CONV16 (C % 16 == 0) */
+    const int16_t* img16;                                                  /* SRC_CONV16 (C % 8 == 0, C <= 16384) */
 } VgemmASrc;
 
 /* Epilogue description: meow::AEpi (src/gemm_hl.h:18-26) in the same order, plus an optional

@@ -47,6 +47,7 @@ _SIGS = {
     "orc_quant16": (I64, [I64, I]),
     "orc_quant16_32": (ctypes.c_int32, [ctypes.c_int32, I]),
     "orc_lut16i": (ctypes.c_int32, [I64, P]),
+    "orc_split16": (None, [I64, P, P]),
     "orc_epi1": (ctypes.c_int32, [ctypes.c_int32, ctypes.c_int32, P, ctypes.c_int32]),
     "orc_geglu": (ctypes.c_int32, [ctypes.c_int32, ctypes.c_int32, P]),
     "orc_gelu": (ctypes.c_int32, [ctypes.c_int32, P]),
@@ -118,6 +119,13 @@ def quant16_32(v, e):
 def lut16i(x, L):
     x = np.ascontiguousarray(x, np.int64); L = np.ascontiguousarray(L, np.int32)
     out = np.empty(x.shape, np.int32); lib().orc_lut16i_n(a(x), a(L), a(out), x.size); return out
+
+
+def split16(v):
+    """(hi, lo) of one 16-bit value through orc_split16."""
+    h, l = ctypes.c_int8(), ctypes.c_int8()
+    lib().orc_split16(int(v), ctypes.addressof(h), ctypes.addressof(l))
+    return h.value, l.value
 
 
 def epi1(chi, clo, cst4, er):

@@ -1,0 +1,168 @@
+"""The C ABI of libvgemm.so without a GPU: the library loads, exports every entry point that
+include/vgemm.h declares, the ctypes mirror of VgemmASrc / VgemmAEpi has the C layout (checked
+against a gcc-compiled probe of the header), and argument checks fail the way the reference throws
+(src/gemm_hl.cu:351,357; src/gemm.cu:41) before any device work."""
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+from vela_amd import _lib
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "vgemm.h"
+
+
+def declared():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    out = {}
+    for m in re.finditer(r"^[A-Za-z_][\w \*]*?\b(vgemm_\w+)\s*\(([^)]*)\)\s*;", text, flags=re.M):
+        args = m.group(2).strip()
+        out[m.group(1)] = 0 if args in ("", "void") else args.count(",") + 1
+    return out
+
+
+def test_every_declared_symbol_is_exported_and_bound():
+    lib = _lib.load()
+    decl = declared()
+    assert len(decl) >= 26
+    sigs = {name: args for name, _, args in _lib.SIGNATURES}
+    for name, nargs in decl.items():
+        assert hasattr(lib, name), f"{name} not exported"
+        assert name in sigs, f"{name} has no ctypes prototype"
+        assert len(sigs[name]) == nargs, f"{name}: {len(sigs[name])} ctypes args, header has {nargs}"
+    assert set(sigs) == set(decl)
+
+
+PROBE = r"""
+#include <stdio.h>
+#include <stddef.h>
+#include "vgemm.h"
+#define F(T, f) printf(#T " " #f " %zu\n", offsetof(T, f));
+int main(void) {
+    printf("VgemmASrc sizeof %zu\nVgemmAEpi sizeof %zu\n", sizeof(VgemmASrc), sizeof(VgemmAEpi));
+    %FIELDS%
+    return 0;
+}
+"""
+
+
+def test_struct_layout_matches_c(tmp_path):
+    lines = []
+    for T, cls in (("VgemmASrc", _lib.ASrc), ("VgemmAEpi", _lib.AEpi)):
+        for f, _ in cls._fields_:
+            lines.append(f"F({T}, {f})")
+    src = tmp_path / "probe.c"
+    src.write_text(PROBE.replace("%FIELDS%", "\n    ".join(lines)))
+    exe = tmp_path / "probe"
+    subprocess.run(["gcc", "-std=c11", "-I", str(ROOT / "include"), str(src), "-o", str(exe)], check=True)
+    got = {}
+    for line in subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.splitlines():
+        T, f, v = line.split()
+        got[(T, f)] = int(v)
+    for T, cls in (("VgemmASrc", _lib.ASrc), ("VgemmAEpi", _lib.AEpi)):
+        assert got[(T, "sizeof")] == ctypes.sizeof(cls), T
+        for f, _ in cls._fields_:
+            assert got[(T, f)] == getattr(cls, f).offset, f"{T}.{f}"
+
+
+def test_init_defaults():
+    lib = _lib.load()
+    a = _lib.ASrc(src=3, K=99)
+    lib.vgemm_asrc_init(ctypes.byref(a))
+    assert (a.src, a.stride, a.K, a.hi) == (0, 1, 0, None)
+    e = _lib.AEpi(epi=2, ldy=5)
+    lib.vgemm_aepi_init(ctypes.byref(e))
+    assert (e.epi, e.ldy, e.ws_bytes) == (0, 0, 0)
+
+
+def test_supported_shapes():
+    lib = _lib.load()
+    assert lib.vgemm_supported(64, 64, 16) == 1
+    assert lib.vgemm_supported(32768, 2560, 320) == 1
+    for shape in [(63, 64, 16), (64, 65, 16), (64, 64, 8), (0, 64, 16), (64, 64, 0)]:
+        assert lib.vgemm_supported(*shape) == 0, shape
+
+
+FAKE = 1 << 40   # a 16-byte aligned address that is never dereferenced: every case fails validation first
+
+
+def call_hl2(A, E, Mp=64, Mreal=64, ldw=64, Np=64, Nreal=64, Kp=64):
+    lib = _lib.load()
+    rc = lib.vgemm_hl2(None, ctypes.byref(A), Mp, Mreal, FAKE, ldw, Np, Nreal, Kp, FAKE, ctypes.byref(E))
+    return rc, lib.vgemm_last_error().decode()
+
+
+@pytest.mark.parametrize("kw,code,msg", [
+    (dict(Mp=65), -1, "unsupported shape"),
+    (dict(Kp=8), -1, "unsupported shape"),
+    (dict(Mreal=65), -1, "Mreal/Nreal"),
+    (dict(ldw=48), -1, "ldw"),
+])
+def test_hl2_shape_errors(kw, code, msg):
+    A = _lib.ASrc(src=0, hi=FAKE, lo=FAKE, ld8=64)
+    E = _lib.AEpi(Y=FAKE, ldy=64)
+    rc, err = call_hl2(A, E, **kw)
+    assert rc == code and msg in err, err
+
+
+@pytest.mark.parametrize("asrc,aepi,code,msg", [
+    (dict(src=2, img=FAKE, C=12, K=108, H=4, W=4, Ho=4, Wo=4), {}, -1, "conv source"),
+    (dict(src=4, img16=FAKE, C=4, K=36, H=4, W=4, Ho=4, Wo=4), {}, -1, "C % 8"),
+    (dict(src=4, img16=FAKE, C=8, K=72, H=4, W=4, Ho=3, Wo=4), {}, -1, "Ho/Wo"),
+    (dict(src=4, img16=FAKE, C=16, K=144, H=4, W=4, Ho=4, Wo=4), {}, -1, "H/W/stride/Kp"),
+    (dict(src=3, q16=FAKE, K=60, ld16=64), {}, -1, "SRC_I16"),
+    (dict(src=1, x=FAKE, K=64, ldx=64), {}, -1, "SRC_X32"),
+    (dict(src=9), {}, -1, "unknown A source"),
+    (dict(src=0, hi=FAKE, lo=FAKE, ld8=64), dict(epi=4), -3, "EPI_QKV"),
+    (dict(src=0, hi=FAKE, lo=FAKE, ld8=64), dict(gnstat=FAKE), -3, "GroupNorm"),
+    (dict(src=0, hi=FAKE, lo=FAKE, ld8=64), dict(epi=2), -1, "Lphi"),
+    (dict(src=0, hi=FAKE, lo=FAKE, ld8=64), dict(epi=2, Lphi=FAKE, residual=FAKE), -1, "no residual"),
+    (dict(src=0, hi=FAKE, lo=FAKE, ld8=64), dict(epi=1, Cs=30), -1, "SPLIT3"),
+    (dict(src=0, hi=FAKE, lo=FAKE, ld8=64), dict(Y=None), -1, "null Y"),
+])
+def test_hl2_argument_errors(asrc, aepi, code, msg):
+    A = _lib.ASrc(**asrc)
+    E = _lib.AEpi(**{"Y": FAKE, "ldy": 64, **aepi})
+    Kp = 80 if asrc.get("K") == 72 else 64
+    rc, err = call_hl2(A, E, Kp=Kp, ldw=Kp)
+    assert rc == code and msg in err, err
+
+
+def test_empty_problem_is_a_no_op():
+    """Mreal = 0 or Nreal = 0 returns before any launch (no device needed)."""
+    A = _lib.ASrc(src=0, hi=FAKE, lo=FAKE, ld8=64)
+    E = _lib.AEpi(Y=FAKE, ldy=64)
+    assert call_hl2(A, E, Mreal=0)[0] == 0
+    assert call_hl2(A, E, Nreal=0)[0] == 0
+
+
+def test_i8gemm_errors():
+    lib = _lib.load()
+    h = ctypes.c_void_p()
+    assert lib.vgemm_i8_create(0, ctypes.byref(h)) == 0
+    try:
+        rc = lib.vgemm_i8_run(h, None, FAKE, 64, 0, FAKE, 64, 0, FAKE, 64, 0, 0, 64, 64, 1)
+        assert rc == -1 and "no int8 GEMM" in lib.vgemm_last_error().decode()
+        rc = lib.vgemm_i8_run(h, None, FAKE, 64, 0, FAKE, 64, 0, FAKE, 64, 0, 64, 64, 40, 1)
+        assert rc == -1 and "K % 16" in lib.vgemm_last_error().decode()
+    finally:
+        lib.vgemm_i8_destroy(h)
+
+
+def test_workspace_heuristic():
+    """Split-K only for deep K whose tiles leave CUs idle (C4 conv at M = 512), none for C2."""
+    lib = _lib.load()
+    lib.vgemm_set_variant(-1)
+    lib.vgemm_set_splitk(0)
+    assert lib.vgemm_workspace_bytes(32768, 32768, 2560, 2560, 320, 2) == 0
+    assert lib.vgemm_workspace_bytes(512, 512, 1280, 1280, 11520, 0) > 0
+    lib.vgemm_set_variant(1)
+    assert lib.vgemm_get_variant() == 1
+    lib.vgemm_set_variant(-1)
+
+
+def test_version():
+    assert b"gfx950" in _lib.load().vgemm_version()
