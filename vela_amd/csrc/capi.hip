@@ -69,28 +69,31 @@ constexpr int NCU = 256;   // MI355X compute units
 
 int cdiv(long long a, long long b) { return int((a + b - 1) / b); }
 
-// Tile variant: the CU that receives the most tiles sets the time; a tile costs its area, and the
-// half-size tiles carry a fixed-overhead penalty (prologue, epilogue, fewer MFMAs per fragment load).
-int pick_variant(int M, int N) {
-    int best = 0;
-    double bestCost = 1e300;
-    for (int v = 0; v < 3; ++v) {
-        const long long tiles = (long long)cdiv(M, TILES[v].BM) * cdiv(N, TILES[v].BN);
-        const double rounds = double((tiles + NCU - 1) / NCU);
-        const double cost = rounds * TILES[v].BM * TILES[v].BN * (v == 0 ? 1.0 : 1.15);
-        if (cost < bestCost - 1e-9) { bestCost = cost; best = v; }
-    }
-    return best;
+// Tile variant and split-K, from measurements over the BASELINE and UNet shapes on MI355X:
+//  * 64x128 tiles (three blocks per CU) are fastest for most shapes;
+//  * 128x128 tiles win for wide, shallow GEMMs (N >= 960, K <= 1280) with plenty of tiles, where the
+//    epilogue dominates and the larger tile halves its fixed per-tile cost;
+//  * deep K (>= 8192) with fewer 128x128 tiles than CUs splits K over ceil(NCU / tiles) blocks per
+//    tile (at least 16 K steps each) and reduces the int32 partials in a second pass.
+bool deep_split_shape(int M, int N, int Kp) {
+    const long long tiles0 = (long long)cdiv(M, TILES[0].BM) * cdiv(N, TILES[0].BN);
+    return Kp >= 8192 && tiles0 < NCU;
 }
 
-// Split-K partitions: only for deep K whose tile count leaves CUs idle.
+int pick_variant(int M, int N, int Kp) {
+    if (deep_split_shape(M, N, Kp)) return 0;
+    const long long tiles1 = (long long)cdiv(M, TILES[1].BM) * cdiv(N, TILES[1].BN);
+    if (N >= 960 && Kp <= 1280 && tiles1 > 3LL * NCU) return 0;
+    return 1;
+}
+
 int pick_splitk(int variant, int M, int N, int Kp) {
     const int nK = (Kp + 63) / 64;
-    const long long tiles = (long long)cdiv(M, TILES[variant].BM) * cdiv(N, TILES[variant].BN);
     if (g_splitk > 0) return g_splitk < nK ? g_splitk : nK;
-    if (nK < 16 || tiles >= NCU) return 1;
+    if (!deep_split_shape(M, N, Kp)) return 1;
+    const long long tiles = (long long)cdiv(M, TILES[variant].BM) * cdiv(N, TILES[variant].BN);
     int s = int((NCU + tiles - 1) / tiles);
-    if (s > nK / 8) s = nK / 8;
+    if (s > nK / 16) s = nK / 16;
     return s < 1 ? 1 : s;
 }
 
@@ -137,7 +140,7 @@ void vgemm_set_splitk(int s) { g_splitk = s < 0 ? 0 : s; }
 
 size_t vgemm_workspace_bytes(int Mp, int Mreal, int Np, int Nreal, int Kp, int epi) {
     (void)Mp; (void)Np; (void)epi;
-    int v = g_variant >= 0 && g_variant < 3 ? g_variant : pick_variant(Mreal, Nreal);
+    int v = g_variant >= 0 && g_variant < 3 ? g_variant : pick_variant(Mreal, Nreal, Kp);
     return ws_bytes_for(v, Mreal, Nreal, pick_splitk(v, Mreal, Nreal, Kp));
 }
 
@@ -232,7 +235,7 @@ int vgemm_hl2(void* stream, const VgemmASrc* A, int Mp, int Mreal, const int8_t*
     }
     p.vec_store = vec ? 1 : 0;
 
-    int variant = g_variant >= 0 && g_variant < 3 ? g_variant : pick_variant(Mreal, Nreal);
+    int variant = g_variant >= 0 && g_variant < 3 ? g_variant : pick_variant(Mreal, Nreal, Kp);
     const int BM = TILES[variant].BM, BN = TILES[variant].BN;
     p.mtiles = cdiv(Mreal, BM);
     p.ntiles = cdiv(Nreal, BN);
@@ -306,7 +309,7 @@ int vgemm_i8_run(void* handle, void* stream, const int8_t* A, int lda, long long
     p.Y = C; p.ldy = ldc; p.vec_store = ldc % 4 == 0 ? 1 : 0;
     p.Mreal = M; p.Nreal = N; p.Kp = K; p.K = K;
     p.sA = strideA; p.sW = strideW; p.sC = strideC;
-    const int variant = g_variant >= 0 && g_variant < 3 ? g_variant : pick_variant(M, N);
+    const int variant = g_variant >= 0 && g_variant < 3 ? g_variant : pick_variant(M, N, K);
     p.mtiles = cdiv(M, TILES[variant].BM);
     p.ntiles = cdiv(N, TILES[variant].BN);
     p.ksplit = 1; p.kper = (K + 63) / 64;

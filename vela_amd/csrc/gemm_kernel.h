@@ -938,53 +938,89 @@ __global__ void __launch_bounds__(256) gemm_hl_kernel(const GemmParams p) {
 // int32 partials of all K ranges and applies the exact int64 epilogue.
 template <int EPI>
 __global__ void __launch_bounds__(256) splitk_epilogue_kernel(const GemmParams p) {
+    // grid: x = groups of 1024 output columns (4 per thread), y = rows (strided when M > gridDim.y)
     const int nout = EPI == EPI_GEGLU ? (p.Nreal >> 1) : p.Nreal;
-    const int groups = (nout + 3) >> 2;
-    const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
-    const int r = int(idx / groups), g = int(idx - (long long)r * groups);
-    if (r >= p.Mreal) return;
-    const int er = p.xrowmax ? rowexp_u32(p.xrowmax[r]) : (p.e ? p.e[r] : 0);
+    const int c0 = (blockIdx.x * 256 + threadIdx.x) * 4;
     const size_t plane = size_t(p.ws_rows) * p.ws_ld;
-    auto sum = [&](int col, int& h, int& l) {
-        int sh = 0, sl = 0;
-        for (int s = 0; s < p.ksplit; ++s) {
-            const int32_t* b = p.ws + (size_t(s * 2) * p.ws_rows + r) * p.ws_ld + col;
-            sh += b[0];
-            sl += b[plane];
-        }
-        h = sh; l = sl;
-    };
-    uint32_t mx = 0;
-    for (int v = 0; v < 4; ++v) {
-        const int c = g * 4 + v;
-        if (c >= nout) break;
-        int y;
-        if constexpr (EPI == EPI_GEGLU) {
-            int ah, al, gh, gl;
-            sum(2 * c, ah, al);
-            sum(2 * c + 1, gh, gl);
-            const int4 ca = p.cst[2 * c], cg = p.cst[2 * c + 1];
-            y = geglu_exact(epi1_exact(ah, al, ca.x, ca.y, ca.z, ca.w, er), epi1_exact(gh, gl, cg.x, cg.y, cg.z, cg.w, er), p.Lphi);
-            p.Y[size_t(r) * p.ldy + c] = y;
-        } else {
-            int h, l;
-            sum(c, h, l);
-            const int4 cc = p.cst[c];
-            y = epi1_exact(h, l, cc.x, cc.y, cc.z, cc.w, er);
-            if constexpr (EPI == EPI_GELU) y = gelu_exact(y, p.Lphi);
-            if constexpr (EPI == EPI_SPLIT3) {
-                const int part = c >= 2 * p.Cs ? 2 : (c >= p.Cs ? 1 : 0);
-                int32_t* d = part == 0 ? p.Y : (part == 1 ? p.Y1 : p.Y2);
-                d[size_t(r) * p.Cs + (c - part * p.Cs)] = y;
-                continue;
+    const bool in = c0 < nout;
+    const bool full = c0 + 3 < nout;
+    for (int r = blockIdx.y; r < p.Mreal; r += gridDim.y) {
+        const int er = p.xrowmax ? rowexp_u32(p.xrowmax[r]) : (p.e ? p.e[r] : 0);
+        // plane sums of ws columns [wc, wc + 4) over the K splits (16-byte loads: ws_ld % 4 == 0)
+        auto sum4 = [&](int wc, v4i& h, v4i& l) {
+            h = v4i{0, 0, 0, 0};
+            l = v4i{0, 0, 0, 0};
+            for (int s = 0; s < p.ksplit; ++s) {
+                const int32_t* b = p.ws + (size_t(s * 2) * p.ws_rows + r) * p.ws_ld + wc;
+                h += *reinterpret_cast<const v4i*>(b);
+                l += *reinterpret_cast<const v4i*>(b + plane);
+            }
+        };
+        int y[4] = {0, 0, 0, 0};
+        uint32_t mx = 0;
+        if (in) {
+            if constexpr (EPI == EPI_GEGLU) {
+                v4i h0, l0, h1, l1;
+                sum4(2 * c0, h0, l0);       // columns a0 g0 a1 g1
+                sum4(2 * c0 + 4, h1, l1);   // columns a2 g2 a3 g3
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const int c = c0 + v;
+                    if (c >= nout) break;
+                    const int ah = v < 2 ? h0[2 * v] : h1[2 * v - 4], al = v < 2 ? l0[2 * v] : l1[2 * v - 4];
+                    const int gh = v < 2 ? h0[2 * v + 1] : h1[2 * v - 3], gl = v < 2 ? l0[2 * v + 1] : l1[2 * v - 3];
+                    const int4 ca = p.cst[2 * c], cg = p.cst[2 * c + 1];
+                    y[v] = geglu_exact(epi1_exact(ah, al, ca.x, ca.y, ca.z, ca.w, er), epi1_exact(gh, gl, cg.x, cg.y, cg.z, cg.w, er), p.Lphi);
+                }
             } else {
-                if (p.R) y = add_sat(y, p.R[size_t(r) * p.ldy + c]);
-                p.Y[size_t(r) * p.ldy + c] = y;
+                v4i h, l;
+                sum4(c0, h, l);
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const int c = c0 + v;
+                    if (c >= nout) break;
+                    const int4 cc = p.cst[c];
+                    int yy = epi1_exact(h[v], l[v], cc.x, cc.y, cc.z, cc.w, er);
+                    if constexpr (EPI == EPI_GELU) yy = gelu_exact(yy, p.Lphi);
+                    y[v] = yy;
+                }
+            }
+            if constexpr (EPI == EPI_SPLIT3) {
+                // Cs % 4 == 0: the four columns lie in one part
+                const int part = c0 >= 2 * p.Cs ? 2 : (c0 >= p.Cs ? 1 : 0);
+                int32_t* d = (part == 0 ? p.Y : (part == 1 ? p.Y1 : p.Y2)) + size_t(r) * p.Cs + (c0 - part * p.Cs);
+                if (full && p.vec_store) *reinterpret_cast<v4i*>(d) = v4i{y[0], y[1], y[2], y[3]};
+                else
+                    for (int v = 0; v < 4 && c0 + v < nout; ++v) d[v] = y[v];
+            } else {
+                int32_t* d = p.Y + size_t(r) * p.ldy + c0;
+                if constexpr (EPI != EPI_GEGLU) {
+                    if (p.R) {
+                        const int32_t* rp = p.R + size_t(r) * p.ldy + c0;
+                        if (full && p.vec_store) {
+                            const v4i rv = *reinterpret_cast<const v4i*>(rp);
+#pragma unroll
+                            for (int v = 0; v < 4; ++v) y[v] = add_sat(y[v], rv[v]);
+                        } else {
+                            for (int v = 0; v < 4 && c0 + v < nout; ++v) y[v] = add_sat(y[v], rp[v]);
+                        }
+                    }
+                }
+                if (full && p.vec_store) *reinterpret_cast<v4i*>(d) = v4i{y[0], y[1], y[2], y[3]};
+                else
+                    for (int v = 0; v < 4 && c0 + v < nout; ++v) d[v] = y[v];
+#pragma unroll
+                for (int v = 0; v < 4; ++v)
+                    if (c0 + v < nout) mx = max(mx, uabs(y[v]));
             }
         }
-        mx = max(mx, uabs(y));
+        if (EPI != EPI_SPLIT3 && p.rowmax) {
+            // every lane of the wave is on row r: one atomic per wave
+#pragma unroll
+            for (int o = 32; o; o >>= 1) mx = max(mx, uint32_t(__shfl_xor(int(mx), o)));
+            if ((threadIdx.x & 63) == 0 && mx) atomicMax(p.rowmax + r, mx);
+        }
     }
-    if (EPI != EPI_SPLIT3 && p.rowmax && mx) atomicMax(p.rowmax + r, mx);
 }
 
 // ---------------------------------------------------------------- host-side launches

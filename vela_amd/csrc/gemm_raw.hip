@@ -12,8 +12,7 @@ hipError_t launch_gemm_raw(int variant, const GemmParams& p, int batch, hipStrea
 
 hipError_t launch_splitk_epilogue(int epi, const GemmParams& p, hipStream_t st) {
     const int nout = epi == EPI_GEGLU ? (p.Nreal >> 1) : p.Nreal;
-    const long long threads = (long long)p.Mreal * ((nout + 3) / 4);
-    const dim3 grid(unsigned((threads + 255) / 256));
+    const dim3 grid(unsigned((nout + 1023) / 1024), unsigned(p.Mreal < 65535 ? p.Mreal : 65535));
     switch (epi) {
     case EPI_PLAIN: hipLaunchKernelGGL(splitk_epilogue_kernel<EPI_PLAIN>, grid, dim3(256), 0, st, p); break;
     case EPI_SPLIT3: hipLaunchKernelGGL(splitk_epilogue_kernel<EPI_SPLIT3>, grid, dim3(256), 0, st, p); break;
