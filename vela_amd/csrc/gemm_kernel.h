@@ -256,6 +256,128 @@ __device__ __forceinline__ EpiFlags block_prologue(const GemmParams& p, int m0, 
     return f;
 }
 
+// ---- the same set-up for a kernel that loads its inputs before the K loop and builds the
+// tables after it, so that no load latency sits between the loads of the first K steps and the
+// first MFMA: the cst entry of table column tid and the shift of tile row tid are held in
+// registers (TilePre), and the GELU table arrives in LDS by DMA, raw, in the upper half of
+// sh.lut, and is expanded to (L[i], L[i+1] - L[i]) pairs here.
+struct TilePre {
+    int4 c;
+    int e;
+    bool cok, eok;
+};
+
+template <int EPI, int SRC, int BM, int BN>
+__device__ __forceinline__ TilePre load_tile_pre(const GemmParams& p, int m0, int n0) {
+    static_assert(BM <= 256 && BN <= 256, "one table row and column per thread");
+    const int tid = threadIdx.x;
+    TilePre t;
+    const int n = n0 + wrow_of_lds<EPI, BN>(tid < BN ? tid : 0);
+    t.cok = tid < BN && n < p.Nreal;
+    t.c = t.cok ? p.cst[n] : make_int4(0, 0, 0, 0);
+    const int r = m0 + tid;
+    t.eok = tid < BM && r < p.Mreal;
+    t.e = t.eok ? (SRC == SRC_X32 ? rowexp_u32(p.xrowmax[r]) : (p.e ? p.e[r] : 0)) : 0;
+    return t;
+}
+
+// byte offset inside sh.lut of the raw table copy (entries 0..2047; entry 2048 comes in a register)
+constexpr unsigned LUT_RAW_OFF = 8192;
+
+template <int EPI, int SRC, int BM, int BN, class S>
+__device__ __forceinline__ EpiFlags epi_setup(const GemmParams& p, const TilePre& t, int L2048, S& sh) {
+    constexpr bool NEEDLUT = EPI == EPI_GEGLU || EPI == EPI_GELU;
+    const int tid = threadIdx.x, lane = tid & 63;
+    // ---- phase 1: everything that reads LDS or needs no LDS (the raw table is still in place)
+    constexpr int LPT = NEEDLUT ? (2050 + 255) / 256 : 1;   // table entries per thread
+    int2 lv[LPT];
+    int lbad = 0;
+    if constexpr (NEEDLUT) {
+        const int* raw = reinterpret_cast<const int*>(reinterpret_cast<const char*>(sh.lut) + LUT_RAW_OFF);
+#pragma unroll
+        for (int q = 0; q < LPT; ++q) {
+            const int i = tid + 256 * q;
+            int2 v = make_int2(0, 0);
+            if (i == 2049) v = make_int2(65536, 0);
+            else if (i >= 1 && i <= 2049) {
+                const int a = raw[i - 1], nx = i - 1 == 2047 ? L2048 : raw[i];
+                v = make_int2(a, nx - a);
+                if (a < 0 || a > 65536 || nx < 0 || nx > 65536) lbad = 1;
+            }
+            lv[q] = v;
+        }
+    }
+    double ms = 0.0, wmv = 0.0, um = 0.0;
+    int bb = 0, smn = INT_MAX, smx = INT_MIN, bad = 0, bmx = 0, nofold = 0;
+    if (t.cok) {
+        const int4 c = t.c;
+        const i64 mag = (c.x < 0 ? -i64(c.x) : i64(c.x)) * i64(p.Kp);
+        if (mag >= (1LL << 30) || c.y < -1000 || c.y > 1000) bad = 1;
+        smn = c.y;
+        smx = c.y;
+        if (c.y >= -1000 && c.y <= 1000) {
+            ms = ldexp(double(c.x), -c.y);
+            wmv = ldexp(128.0 * (double(c.w) * double(c.x)), -c.y);
+            // |acc*m*2^-s| <= 2^22*Kp*|m|*2^-s, since |acc| <= 32768*128*Kp
+            um = ldexp(4194304.0 * double(p.Kp) * fabs(double(c.x)), -c.y);
+            // wm + 1/2 + b is exact when |b|*2^s < 2^51 (numerator below 2^53)
+            if (ldexp(fabs(double(c.z)), c.y) >= 2251799813685248.0) nofold = 1;
+        }
+        bb = c.z;
+        bmx = int(min(uabs(c.z), 0x7fffffffu));
+    }
+    int emn = t.eok ? t.e : INT_MAX, emx = t.eok ? t.e : INT_MIN;
+#pragma unroll
+    for (int o = 32; o; o >>= 1) {
+        emn = min(emn, __shfl_xor(emn, o));
+        emx = max(emx, __shfl_xor(emx, o));
+        smn = min(smn, __shfl_xor(smn, o));
+        smx = max(smx, __shfl_xor(smx, o));
+        bad |= __shfl_xor(bad, o);
+        bmx = max(bmx, __shfl_xor(bmx, o));
+        nofold |= __shfl_xor(nofold, o);
+        um = max(um, __shfl_xor(um, o));
+        if constexpr (NEEDLUT) lbad |= __shfl_xor(lbad, o);
+    }
+    if (tid == 0) {
+        sh.flag[0] = INT_MAX; sh.flag[1] = INT_MIN; sh.flag[2] = INT_MAX; sh.flag[3] = INT_MIN;
+        sh.flag[4] = 0; sh.flag[5] = 0; sh.flag[6] = 0; sh.flag[7] = 0;
+        sh.umax = 0;
+    }
+    __syncthreads();   // raw table read by everyone, flags reset
+    // ---- phase 2: tables, expanded GELU table, flags
+    if (tid < BN) { sh.ms[tid] = ms; sh.wm[tid] = wmv; sh.b[tid] = bb; }
+    if constexpr (NEEDLUT) {
+#pragma unroll
+        for (int q = 0; q < LPT; ++q) {
+            const int i = tid + 256 * q;
+            if (i < 2050) sh.lut[i] = lv[q];
+        }
+    }
+    if (lane == 0) {
+        if (emn <= emx) { atomicMin(&sh.flag[0], emn); atomicMax(&sh.flag[1], emx); }
+        if (smn <= smx) { atomicMin(&sh.flag[2], smn); atomicMax(&sh.flag[3], smx); }
+        if (bad) atomicOr(&sh.flag[4], 1);
+        if (lbad) atomicOr(&sh.flag[5], 1);
+        atomicMax(&sh.flag[6], bmx);
+        if (nofold) atomicOr(&sh.flag[7], 1);
+        atomicMax(&sh.umax, __double_as_longlong(um));
+    }
+    __syncthreads();
+    const i64 emin = sh.flag[0], emax = sh.flag[1], smin = sh.flag[2], smax = sh.flag[3];
+    EpiFlags f;
+    f.fast = !sh.flag[4] && (smin - emax >= 1) && (smax - emin <= 52) && emin >= -1000 && emax <= 1000;
+    if (NEEDLUT && sh.flag[5]) f.fast = false;
+    f.ezero = emin > emax || (emin == 0 && emax == 0);
+    f.fold = f.fast && f.ezero && !sh.flag[7] && __longlong_as_double(sh.umax) + double(sh.flag[6]) + 2.0 < 2147483647.0;
+    if (f.ezero) {
+        // the FMA constant of the e == 0 forms: wm + 1/2, and + b when folded (exact, see above)
+        if (tid < BN) sh.wm[tid] = (sh.wm[tid] + 0.5) + (f.fold ? double(sh.b[tid]) : 0.0);
+        __syncthreads();
+    }
+    return f;
+}
+
 // The requantising epilogue of one wave. Subtile (ns, ms) of the wave holds rows
 // rbase + ms*16 + (lane & 15) and LDS-table rows wsub_row(wn, ns) + 4*(lane >> 4) + v, v = 0..3.
 template <int EPI, int SRC, class T, bool EZERO, bool SMALLK, bool FOLD, class S>
@@ -553,13 +675,28 @@ __global__ void __launch_bounds__(256, 2) gemm_dma_kernel(const GemmParams p) {
     const v4i rA0 = make_rsrc_words(a0p, p.a0_bytes);
     const v4i rA1 = make_rsrc_words(SRC == SRC_I8 && TWO ? p.a1 : a0p, SRC == SRC_I8 && TWO ? p.a1_bytes : p.a0_bytes);
 
-    // rows owned by this wave and their shifts (for the epilogue and the image quantisation)
+    // rows owned by this wave and their shifts (for the epilogue and the image quantisation), and
+    // the epilogue's table inputs: all loaded first, so that they are older than every DMA below
+    // (loads complete in order: waiting for a K step's DMA then implies these are in too)
     const int rbase = m0 + wave * T::WTM;
     int er[MS];
 #pragma unroll
     for (int ms = 0; ms < MS; ++ms) {
         const int r = rbase + ms * 16 + (lane & 15);
         er[ms] = (r < p.Mreal && p.e && (FUSED || SRC == SRC_CONV16)) ? p.e[r] : 0;
+    }
+    TilePre pre{};
+    if constexpr (FUSED) pre = load_tile_pre<EPI, SRC, BM, BN>(p, m0, n0);
+    const int L2048 = D::NEEDLUT ? p.Lphi[2048] : 0;
+    if constexpr (D::NEEDLUT) {
+        // GELU table entries 0..2047 -> LDS (raw), 8 KB: two 1 KB DMA instructions per wave
+        const v4i rL = make_rsrc_words(p.Lphi, 2049u * 4u);
+        const unsigned lbase = lds_addr(sh.lut) + LUT_RAW_OFF;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const unsigned c = unsigned(wave * 2 + j) * 1024u;
+            dma16(rL, unsigned(lane) * 16u, c, lbase + c);
+        }
     }
 
     // ---- DMA address state. W: wave instruction j covers LDS rows 16*(wave*W_INS + j) + lane/4,
@@ -672,9 +809,6 @@ __global__ void __launch_bounds__(256, 2) gemm_dma_kernel(const GemmParams p) {
     for (int s = 0; s < NST - 1; ++s)
         if (s < n) issue(kb + s, s);
 
-    EpiFlags fl{true, true, false};
-    if constexpr (FUSED) fl = block_prologue<EPI, SRC, BM, BN>(p, m0, n0, sh);
-
     // image rows of this wave all have e == 0 (the usual case): a clamp is the whole quantisation.
     // Decided per wave, so that the compiler branches instead of evaluating both forms.
     bool e_any = false;
@@ -727,10 +861,8 @@ __global__ void __launch_bounds__(256, 2) gemm_dma_kernel(const GemmParams p) {
     };
 
     // ---- main loop: NST-stage LDS ring, loads NST-1 steps ahead of the MFMAs, unrolled by NST so
-    // that every LDS address is an immediate offset.
-    // Every ordinary load above completes here, with a wait the compiler sees; otherwise it places
-    // that wait at the first use, inside the loop, where it would also drain the stage prefetch.
-    __builtin_amdgcn_s_waitcnt(0);
+    // that every LDS address is an immediate offset. The ordinary loads above are first used after
+    // the loop (or, for image rows, by the ballot above), so no compiler wait lands inside it.
     for (int s0 = 0; s0 < n; s0 += NST) {
 #pragma unroll
         for (int u = 0; u < NST; ++u) {
@@ -751,6 +883,7 @@ __global__ void __launch_bounds__(256, 2) gemm_dma_kernel(const GemmParams p) {
     } else if constexpr (EPI == EPI_RAW) {
         store_raw<T>(p, acc_h, rbase, n0, bt);
     } else {
+        const EpiFlags fl = epi_setup<EPI, SRC, BM, BN>(p, pre, L2048, sh);
         fused_epilogue<EPI, SRC, T>(p, acc_h, acc_l, rbase, n0, 0, sh, fl, er);
     }
 }
