@@ -167,7 +167,7 @@ def _reset_knobs(gpu):
 SHAPES = [(64, 64, 64), (100, 80, 48), (300, 200, 320), (257, 130, 96), (640, 320, 1280)]
 
 
-@pytest.mark.parametrize("variant", [0, 1, 2])
+@pytest.mark.parametrize("variant", [0, 1, 2, 3])
 @pytest.mark.parametrize("shape", SHAPES)
 def test_i8_planes_plain_residual(variant, shape):
     """src/test_gemm_hl.cu:55-80 scaled down: random planes, e in [0,12), s in [20,30), residual."""
@@ -176,7 +176,7 @@ def test_i8_planes_plain_residual(variant, shape):
     Case(vg.SRC_I8, M, N, K, seed=hash(shape) % 1000 + variant, residual=True, e_max=11).check(what=f"I8 {shape} v{variant}")
 
 
-@pytest.mark.parametrize("variant", [0, 1, 2])
+@pytest.mark.parametrize("variant", [0, 1, 2, 3])
 @pytest.mark.parametrize("shape", SHAPES)
 def test_i16_plain(variant, shape):
     vg.set_variant(variant)
@@ -186,19 +186,19 @@ def test_i16_plain(variant, shape):
 
 
 @pytest.mark.parametrize("epi", [vg.EPI_PLAIN, vg.EPI_GEGLU, vg.EPI_GELU])
-@pytest.mark.parametrize("variant", [0, 1, 2])
+@pytest.mark.parametrize("variant", [0, 1, 2, 3])
 def test_i16_epilogues_rowmax(epi, variant):
     vg.set_variant(variant)
     Case(vg.SRC_I16, 384, 256, 320, epi=epi, seed=11, rowmax=True, e_max=3, s_range=(16, 24)).check(what=f"epi {epi} v{variant}")
 
 
-@pytest.mark.parametrize("variant", [0, 1, 2])
+@pytest.mark.parametrize("variant", [0, 1, 2, 3])
 def test_split3(variant):
     vg.set_variant(variant)
     Case(vg.SRC_I16, 200, 3 * 96, 128, epi=vg.EPI_SPLIT3, seed=12, Cs=96).check(what=f"split3 v{variant}")
 
 
-@pytest.mark.parametrize("variant", [0, 1])
+@pytest.mark.parametrize("variant", [0, 1, 3])
 @pytest.mark.parametrize("shape", [(96, 64, 1024), (130, 320, 960), (64, 128, 64)])
 def test_x32_source(variant, shape):
     """SRC_X32: int32 rows of random bit width 1..31 quantised on load (src/test_gemm_hl.cu:16,31-36)."""
@@ -207,10 +207,12 @@ def test_x32_source(variant, shape):
     Case(vg.SRC_X32, M, N, K, seed=13).check(what=f"X32 {shape}")
 
 
+@pytest.mark.parametrize("variant", [-1, 3])
 @pytest.mark.parametrize("src", [vg.SRC_CONV32, vg.SRC_CONV16])
 @pytest.mark.parametrize("geom", [(2, 8, 8, 32, 1), (1, 7, 5, 64, 2), (2, 6, 6, 320, 1), (1, 9, 11, 16, 2)])
-def test_conv_sources(src, geom):
+def test_conv_sources(src, geom, variant):
     """Implicit 3x3 im2col (src/test_gemm_hl.cu:12,25-29 cases scaled down), e from conv_e(pixmax)."""
+    vg.set_variant(variant)
     B, H, W, C, stride = geom
     Ho, Wo = (H - 1) // stride + 1, (W - 1) // stride + 1
     Case(src, B * Ho * Wo, 96, 9 * C, seed=14, conv=geom, residual=True).check(what=f"conv {src} {geom}")
@@ -246,10 +248,12 @@ def test_lut_outside_range_takes_exact_path():
         Case(vg.SRC_I16, 256, 128, 64, epi=epi, seed=15, lut=lut, rowmax=True).check(what=f"lut epi {epi}")
 
 
+@pytest.mark.parametrize("variant", [-1, 3])
 @pytest.mark.parametrize("splits", [2, 3, 7])
 @pytest.mark.parametrize("epi", [vg.EPI_PLAIN, vg.EPI_GEGLU])
-def test_splitk(splits, epi):
+def test_splitk(splits, epi, variant):
     """Split-K partials through a workspace reduce to the same bytes."""
+    vg.set_variant(variant)
     vg.set_splitk(splits)
     c = Case(vg.SRC_I16, 200, 192, 1536, epi=epi, seed=16, rowmax=True, residual=epi == vg.EPI_PLAIN)
     nb = vg.workspace_bytes(c.Mp, c.M, c.Np, c.N, c.Kp, epi)

@@ -139,7 +139,7 @@ def test_epilogue_geglu_q(gpu):
     assert_equal(to_np(eo), eo_w, "e")
 
 
-@pytest.mark.parametrize("variant", [-1, 0, 1, 2])
+@pytest.mark.parametrize("variant", [-1, 0, 1, 2, 3])
 @pytest.mark.parametrize("M,N,K,batch", [(128, 128, 64, 1), (257, 100, 320, 1), (2 * 8192, 320, 16, 1), (77, 96, 64, 3)])
 def test_i8gemm(gpu, variant, M, N, K, batch):
     """Gemm::run (src/gemm.cu:46-70): C = A * W^T, int32, strided batch."""

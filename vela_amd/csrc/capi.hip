@@ -64,7 +64,10 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 
 constexpr long long MAX_EXTENT = (1LL << 31) - 64;
 
 struct Tiles { int BM, BN; };
-constexpr Tiles TILES[3] = {{128, 128}, {64, 128}, {128, 64}};
+// variant 3 (128 x 256, eight waves) exists for the DMA sources only; the register-staged sources
+// run it as variant 0
+constexpr int NVARIANT = 4;
+constexpr Tiles TILES[NVARIANT] = {{128, 128}, {64, 128}, {128, 64}, {128, 256}};
 constexpr int NCU = 256;   // MI355X compute units
 
 int cdiv(long long a, long long b) { return int((a + b - 1) / b); }
@@ -73,15 +76,26 @@ int cdiv(long long a, long long b) { return int((a + b - 1) / b); }
 //  * 64x128 tiles (three blocks per CU) are fastest for most shapes;
 //  * 128x128 tiles win for wide, shallow GEMMs (N >= 960, K <= 1280) with plenty of tiles, where the
 //    epilogue dominates and the larger tile halves its fixed per-tile cost;
-//  * deep K (>= 8192) with fewer 128x128 tiles than CUs splits K over ceil(NCU / tiles) blocks per
-//    tile (at least 16 K steps each) and reduces the int32 partials in a second pass.
-bool deep_split_shape(int M, int N, int Kp) {
+//  * deep K with few tiles splits K so that all tiles' splits fill one round of blocks (two per CU
+//    for 128x128, three for 64x128) with at least 16 K steps per split: very few rows (<= 128
+//    64x128 tiles, K >= 4096) run 64x128 tiles in up to six splits, fewer than 256 128x128 tiles
+//    with K >= 8192 run 128x128 tiles; the int32 partials are reduced in a second pass.
+enum SplitRule { SPLIT_NONE, SPLIT_SMALL, SPLIT_DEEP };
+
+SplitRule split_rule(int M, int N, int Kp) {
     const long long tiles0 = (long long)cdiv(M, TILES[0].BM) * cdiv(N, TILES[0].BN);
-    return Kp >= 8192 && tiles0 < NCU;
+    const long long tiles1 = (long long)cdiv(M, TILES[1].BM) * cdiv(N, TILES[1].BN);
+    if (Kp >= 4096 && tiles1 <= 128) return SPLIT_SMALL;
+    if (Kp >= 8192 && tiles0 < NCU) return SPLIT_DEEP;
+    return SPLIT_NONE;
 }
 
 int pick_variant(int M, int N, int Kp) {
-    if (deep_split_shape(M, N, Kp)) return 0;
+    switch (split_rule(M, N, Kp)) {
+    case SPLIT_SMALL: return 1;
+    case SPLIT_DEEP: return 0;
+    default: break;
+    }
     const long long tiles1 = (long long)cdiv(M, TILES[1].BM) * cdiv(N, TILES[1].BN);
     if (N >= 960 && Kp <= 1280 && tiles1 > 3LL * NCU) return 0;
     return 1;
@@ -90,11 +104,13 @@ int pick_variant(int M, int N, int Kp) {
 int pick_splitk(int variant, int M, int N, int Kp) {
     const int nK = (Kp + 63) / 64;
     if (g_splitk > 0) return g_splitk < nK ? g_splitk : nK;
-    if (!deep_split_shape(M, N, Kp)) return 1;
+    const SplitRule rule = split_rule(M, N, Kp);
+    if (rule == SPLIT_NONE) return 1;
     const long long tiles = (long long)cdiv(M, TILES[variant].BM) * cdiv(N, TILES[variant].BN);
-    int s = int((NCU + tiles - 1) / tiles);
+    long long s = 2LL * NCU / tiles;   // one round of blocks
+    if (rule == SPLIT_SMALL && s > 6) s = 6;
     if (s > nK / 16) s = nK / 16;
-    return s < 1 ? 1 : s;
+    return s < 1 ? 1 : int(s);
 }
 
 size_t ws_bytes_for(int variant, int M, int N, int splits) {
@@ -140,7 +156,7 @@ void vgemm_set_splitk(int s) { g_splitk = s < 0 ? 0 : s; }
 
 size_t vgemm_workspace_bytes(int Mp, int Mreal, int Np, int Nreal, int Kp, int epi) {
     (void)Mp; (void)Np; (void)epi;
-    int v = g_variant >= 0 && g_variant < 3 ? g_variant : pick_variant(Mreal, Nreal, Kp);
+    int v = g_variant >= 0 && g_variant < NVARIANT ? g_variant : pick_variant(Mreal, Nreal, Kp);
     return ws_bytes_for(v, Mreal, Nreal, pick_splitk(v, Mreal, Nreal, Kp));
 }
 
@@ -235,7 +251,8 @@ int vgemm_hl2(void* stream, const VgemmASrc* A, int Mp, int Mreal, const int8_t*
     }
     p.vec_store = vec ? 1 : 0;
 
-    int variant = g_variant >= 0 && g_variant < 3 ? g_variant : pick_variant(Mreal, Nreal, Kp);
+    int variant = g_variant >= 0 && g_variant < NVARIANT ? g_variant : pick_variant(Mreal, Nreal, Kp);
+    if (variant == 3 && (A->src == VGEMM_SRC_X32 || A->src == VGEMM_SRC_CONV32)) variant = 0;
     const int BM = TILES[variant].BM, BN = TILES[variant].BN;
     p.mtiles = cdiv(Mreal, BM);
     p.ntiles = cdiv(Nreal, BN);
@@ -309,7 +326,7 @@ int vgemm_i8_run(void* handle, void* stream, const int8_t* A, int lda, long long
     p.Y = C; p.ldy = ldc; p.vec_store = ldc % 4 == 0 ? 1 : 0;
     p.Mreal = M; p.Nreal = N; p.Kp = K; p.K = K;
     p.sA = strideA; p.sW = strideW; p.sC = strideC;
-    const int variant = g_variant >= 0 && g_variant < 3 ? g_variant : pick_variant(M, N, K);
+    const int variant = g_variant >= 0 && g_variant < NVARIANT ? g_variant : pick_variant(M, N, K);
     p.mtiles = cdiv(M, TILES[variant].BM);
     p.ntiles = cdiv(N, TILES[variant].BN);
     p.ksplit = 1; p.kper = (K + 63) / 64;

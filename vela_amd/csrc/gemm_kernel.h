@@ -37,7 +37,9 @@ struct Tile {
     static constexpr int WT = BN * 4 / 256;              // 16-byte W chunks per thread per K step (register path)
     static constexpr int AT = BM * 4 / 256;              // 16-value A chunks per thread per K step (register path)
     static constexpr int STAGE = (BN + 2 * BM) * 64;     // LDS bytes per stage: W, hi, lo planes
-    static_assert(WM * WN == 4, "four waves");
+    static constexpr int NW = WM * WN;                   // waves per block
+    static constexpr int NT = 64 * NW;                   // threads per block
+    static_assert(NW == 4 || NW == 8, "four or eight waves");
     static_assert(MS >= 1 && NS >= 2 && (NS % 2) == 0, "wave tile");
 };
 
@@ -49,6 +51,8 @@ typedef Tile<128, 64, 2, 2> TileV2;
 typedef Tile<128, 128, 4, 1> TileD0;
 typedef Tile<64, 128, 4, 1> TileD1;
 typedef Tile<128, 64, 4, 1> TileD2;
+// eight waves, 4 x 2: each A stripe feeds 256 columns (half the A traffic of 128-column tiles)
+typedef Tile<128, 256, 4, 2> TileD3;
 
 // Byte offset of 16-byte chunk `chunk` (0..3) of a 64-byte LDS row. The XOR makes the rows read
 // by one MFMA fragment load hit distinct bank groups whether the LDS serves 8 or 16 lanes of a
@@ -269,7 +273,7 @@ struct TilePre {
 
 template <int EPI, int SRC, int BM, int BN>
 __device__ __forceinline__ TilePre load_tile_pre(const GemmParams& p, int m0, int n0) {
-    static_assert(BM <= 256 && BN <= 256, "one table row and column per thread");
+    // one table row and one table column per thread (blocks have at least max(BM, BN) threads)
     const int tid = threadIdx.x;
     TilePre t;
     const int n = n0 + wrow_of_lds<EPI, BN>(tid < BN ? tid : 0);
@@ -284,19 +288,20 @@ __device__ __forceinline__ TilePre load_tile_pre(const GemmParams& p, int m0, in
 // byte offset inside sh.lut of the raw table copy (entries 0..2047; entry 2048 comes in a register)
 constexpr unsigned LUT_RAW_OFF = 8192;
 
-template <int EPI, int SRC, int BM, int BN, class S>
+template <int EPI, int SRC, int BM, int BN, int NT, class S>
 __device__ __forceinline__ EpiFlags epi_setup(const GemmParams& p, const TilePre& t, int L2048, S& sh) {
     constexpr bool NEEDLUT = EPI == EPI_GEGLU || EPI == EPI_GELU;
+    static_assert(NT >= BM && NT >= BN, "one table row and column per thread");
     const int tid = threadIdx.x, lane = tid & 63;
     // ---- phase 1: everything that reads LDS or needs no LDS (the raw table is still in place)
-    constexpr int LPT = NEEDLUT ? (2050 + 255) / 256 : 1;   // table entries per thread
+    constexpr int LPT = NEEDLUT ? (2050 + NT - 1) / NT : 1;   // table entries per thread
     int2 lv[LPT];
     int lbad = 0;
     if constexpr (NEEDLUT) {
         const int* raw = reinterpret_cast<const int*>(reinterpret_cast<const char*>(sh.lut) + LUT_RAW_OFF);
 #pragma unroll
         for (int q = 0; q < LPT; ++q) {
-            const int i = tid + 256 * q;
+            const int i = tid + NT * q;
             int2 v = make_int2(0, 0);
             if (i == 2049) v = make_int2(65536, 0);
             else if (i >= 1 && i <= 2049) {
@@ -350,7 +355,7 @@ __device__ __forceinline__ EpiFlags epi_setup(const GemmParams& p, const TilePre
     if constexpr (NEEDLUT) {
 #pragma unroll
         for (int q = 0; q < LPT; ++q) {
-            const int i = tid + 256 * q;
+            const int i = tid + NT * q;
             if (i < 2050) sh.lut[i] = lv[q];
         }
     }
@@ -645,15 +650,29 @@ struct DmaCfg {
     static constexpr int W_BYTES = T::BN * 64;
     static constexpr int A_BYTES = RAW16 ? T::BM * 128 : (TWO ? 2 : 1) * T::BM * 64;
     static constexpr int STAGE = W_BYTES + A_BYTES;
-    static constexpr int NST = NEEDLUT ? 2 : 3;   // LDS stages (keeps two blocks per CU within 160 KB)
-    static constexpr int W_INS = T::BN / 64;      // DMA instructions per wave per stage: W
-    static constexpr int A_INS = A_BYTES / 4096;  //                                     A
+#ifndef VK_DMA_STAGES
+    // LDS stages: three, or two where a GELU table must fit beside them for two blocks per CU
+    static constexpr int NST = NEEDLUT && T::NW == 4 ? 2 : 3;
+#else
+    static constexpr int NST = NEEDLUT && T::NW == 4 ? 2 : VK_DMA_STAGES;
+#endif
+    static constexpr int W_INS = W_BYTES / 1024 / T::NW;   // DMA instructions per wave per stage: W
+    static constexpr int A_INS = A_BYTES / 1024 / T::NW;   //                                     A
     static constexpr int PER_STAGE = W_INS + A_INS;
-    static_assert(W_INS >= 1 && A_INS >= 1 && (A_BYTES % 4096) == 0, "DMA mapping");
+    static_assert(W_INS >= 1 && A_INS >= 1 && (A_BYTES % (1024 * T::NW)) == 0 && (W_BYTES % (1024 * T::NW)) == 0, "DMA mapping");
 };
 
+#ifndef VK_MIN_BLOCKS_SMALL
+#define VK_MIN_BLOCKS_SMALL 2
+#endif
+// blocks per CU the register allocator must allow: 64 x 128 tiles without a GELU table can run more
+template <class T, int EPI>
+constexpr int dma_min_blocks() {
+    return T::NW == 8 ? 1 : (T::BM * T::BN <= 64 * 128 && EPI != EPI_GEGLU && EPI != EPI_GELU ? VK_MIN_BLOCKS_SMALL : 2);
+}
+
 template <int SRC, int EPI, class T>
-__global__ void __launch_bounds__(256, 2) gemm_dma_kernel(const GemmParams p) {
+__global__ void __launch_bounds__(T::NT, (dma_min_blocks<T, EPI>())) gemm_dma_kernel(const GemmParams p) {
     using D = DmaCfg<SRC, EPI, T>;
     constexpr int BM = T::BM, BN = T::BN, MS = T::MS, NS = T::NS, NST = D::NST;
     constexpr bool TWO = D::TWO, FUSED = D::FUSED;
@@ -661,8 +680,10 @@ __global__ void __launch_bounds__(256, 2) gemm_dma_kernel(const GemmParams p) {
     __shared__ __attribute__((aligned(16))) unsigned char smem[NST * D::STAGE];
     __shared__ __attribute__((aligned(16))) EpiShared<FUSED ? BN : 1, D::NEEDLUT> sh;
 
-    // the wave index in a scalar register (the DMA's LDS addresses must be wave-uniform)
+    // the wave index in a scalar register (the DMA's LDS addresses must be wave-uniform); waves
+    // are WM x WN over the tile, wm the row slot and wn the column slot
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave % T::WM, wn = wave / T::WM;
     const TileIdx ti = tile_index(p);
     const int m0 = ti.mt * BM, n0 = ti.nt * BN;
     const int nK = (p.Kp + 63) >> 6;
@@ -678,7 +699,7 @@ __global__ void __launch_bounds__(256, 2) gemm_dma_kernel(const GemmParams p) {
     // rows owned by this wave and their shifts (for the epilogue and the image quantisation), and
     // the epilogue's table inputs: all loaded first, so that they are older than every DMA below
     // (loads complete in order: waiting for a K step's DMA then implies these are in too)
-    const int rbase = m0 + wave * T::WTM;
+    const int rbase = m0 + wm * T::WTM;
     int er[MS];
 #pragma unroll
     for (int ms = 0; ms < MS; ++ms) {
@@ -689,12 +710,13 @@ __global__ void __launch_bounds__(256, 2) gemm_dma_kernel(const GemmParams p) {
     if constexpr (FUSED) pre = load_tile_pre<EPI, SRC, BM, BN>(p, m0, n0);
     const int L2048 = D::NEEDLUT ? p.Lphi[2048] : 0;
     if constexpr (D::NEEDLUT) {
-        // GELU table entries 0..2047 -> LDS (raw), 8 KB: two 1 KB DMA instructions per wave
+        // GELU table entries 0..2047 -> LDS (raw), 8 KB: eight 1 KB DMA instructions per block
         const v4i rL = make_rsrc_words(p.Lphi, 2049u * 4u);
         const unsigned lbase = lds_addr(sh.lut) + LUT_RAW_OFF;
+        constexpr int LJ = 8 / T::NW;
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const unsigned c = unsigned(wave * 2 + j) * 1024u;
+        for (int j = 0; j < LJ; ++j) {
+            const unsigned c = unsigned(wave * LJ + j) * 1024u;
             dma16(rL, unsigned(lane) * 16u, c, lbase + c);
         }
     }
@@ -832,7 +854,7 @@ __global__ void __launch_bounds__(256, 2) gemm_dma_kernel(const GemmParams p) {
         v4i hf[MS], lf[TWO ? MS : 1];
 #pragma unroll
         for (int ms = 0; ms < MS; ++ms) {
-            const int row = wave * T::WTM + ms * 16 + fr;
+            const int row = wm * T::WTM + ms * 16 + fr;
             if constexpr (D::RAW16) {
                 const v4i x0 = *reinterpret_cast<const v4i*>(sA + swz16(row, 2 * fg));
                 const v4i x1 = *reinterpret_cast<const v4i*>(sA + swz16(row, 2 * fg + 1));
@@ -850,7 +872,7 @@ __global__ void __launch_bounds__(256, 2) gemm_dma_kernel(const GemmParams p) {
         }
 #pragma unroll
         for (int ns = 0; ns < NS; ++ns) {
-            const int row = (FUSED ? wsub_row<EPI, T>(0, ns) : ns * 16) + fr;
+            const int row = (FUSED ? wsub_row<EPI, T>(wn, ns) : (wn * NS + ns) * 16) + fr;
             const v4i wf = *reinterpret_cast<const v4i*>(sW + swz(row, fg));
 #pragma unroll
             for (int ms = 0; ms < MS; ++ms) {
@@ -868,8 +890,9 @@ __global__ void __launch_bounds__(256, 2) gemm_dma_kernel(const GemmParams p) {
         for (int u = 0; u < NST; ++u) {
             const int s = s0 + u;
             if (s < n) {
-                // this stage's DMA done (the next stage's may still be in flight), then publish it
-                if (NST == 3 && s + 1 < n) vm_wait<D::PER_STAGE>();
+                // this stage's DMA done (the later stages' may still be in flight), then publish it
+                if (NST >= 4 && s + 2 < n) vm_wait<(NST >= 4 ? 2 : 0) * D::PER_STAGE>();
+                else if (NST >= 3 && s + 1 < n) vm_wait<D::PER_STAGE>();
                 else vm_wait<0>();
                 block_barrier();
                 if (s + NST - 1 < n) issue(kb + s + NST - 1, (u + NST - 1) % NST);
@@ -879,12 +902,12 @@ __global__ void __launch_bounds__(256, 2) gemm_dma_kernel(const GemmParams p) {
     }
 
     if constexpr (EPI == EPI_PARTIAL) {
-        store_partial<T>(p, acc_h, acc_l, rbase, n0, ti.ks);
+        store_partial<T>(p, acc_h, acc_l, rbase, n0 + wn * T::WTN, ti.ks);
     } else if constexpr (EPI == EPI_RAW) {
-        store_raw<T>(p, acc_h, rbase, n0, bt);
+        store_raw<T>(p, acc_h, rbase, n0 + wn * T::WTN, bt);
     } else {
-        const EpiFlags fl = epi_setup<EPI, SRC, BM, BN>(p, pre, L2048, sh);
-        fused_epilogue<EPI, SRC, T>(p, acc_h, acc_l, rbase, n0, 0, sh, fl, er);
+        const EpiFlags fl = epi_setup<EPI, SRC, BM, BN, T::NT>(p, pre, L2048, sh);
+        fused_epilogue<EPI, SRC, T>(p, acc_h, acc_l, rbase, n0, wn, sh, fl, er);
     }
 }
 
@@ -1161,7 +1184,7 @@ __global__ void __launch_bounds__(256) splitk_epilogue_kernel(const GemmParams p
 template <int SRC, int EPI, class T>
 hipError_t launch_dma_t(const GemmParams& p, int batch, hipStream_t st) {
     dim3 grid(unsigned(p.mtiles * p.ntiles * p.ksplit), unsigned(batch));
-    hipLaunchKernelGGL((gemm_dma_kernel<SRC, EPI, T>), grid, dim3(256), 0, st, p);
+    hipLaunchKernelGGL((gemm_dma_kernel<SRC, EPI, T>), grid, dim3(T::NT), 0, st, p);
     return hipGetLastError();
 }
 
@@ -1198,6 +1221,7 @@ hipError_t launch_gemm_src(int variant, int epi, const GemmParams& p, int batch,
         switch (variant) {
         case 1: return launch_gemm_epi<SRC, TileD1, true>(epi, p, batch, st);
         case 2: return launch_gemm_epi<SRC, TileD2, true>(epi, p, batch, st);
+        case 3: return launch_gemm_epi<SRC, TileD3, true>(epi, p, batch, st);
         default: return launch_gemm_epi<SRC, TileD0, true>(epi, p, batch, st);
         }
     } else {

@@ -6,6 +6,7 @@ hipError_t launch_gemm_raw(int variant, const GemmParams& p, int batch, hipStrea
     switch (variant) {
     case 1: return launch_dma_t<SRC_I8, EPI_RAW, TileD1>(p, batch, st);
     case 2: return launch_dma_t<SRC_I8, EPI_RAW, TileD2>(p, batch, st);
+    case 3: return launch_dma_t<SRC_I8, EPI_RAW, TileD3>(p, batch, st);
     default: return launch_dma_t<SRC_I8, EPI_RAW, TileD0>(p, batch, st);
     }
 }
