@@ -218,6 +218,19 @@ def test_conv_sources(src, geom, variant):
     Case(src, B * Ho * Wo, 96, 9 * C, seed=14, conv=geom, residual=True).check(what=f"conv {src} {geom}")
 
 
+@pytest.mark.parametrize("variant", [-1, 0, 3])
+def test_conv16_with_shifts(variant):
+    """SRC_CONV16 with caller-provided shifts e in [0, 17] (the image is quantised on load with
+    quant16_32 per output row, src/gemm_hl.cu:104-114), and an image holding -32768."""
+    vg.set_variant(variant)
+    B, H, W, C, stride = 2, 6, 5, 64, 1
+    c = Case(vg.SRC_CONV16, B * H * W, 128, 9 * C, seed=31, conv=(B, H, W, C, stride), residual=True)
+    c.img[0, :2] = -32768
+    c.e = rng(32).integers(0, 18, c.M).astype(np.int32)
+    c.e[::7] = 0
+    c.check(what=f"conv16 e v{variant}")
+
+
 @pytest.mark.parametrize("src", [vg.SRC_I8, vg.SRC_I16])
 def test_exact_slow_path(src):
     """Shifts s - e outside [1, 52] (left shifts, s = 0, deep right shifts) and |acc * m| beyond 2^52

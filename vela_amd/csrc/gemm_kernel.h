@@ -652,9 +652,9 @@ struct DmaCfg {
     static constexpr int STAGE = W_BYTES + A_BYTES;
 #ifndef VK_DMA_STAGES
     // LDS stages: three, or two where a GELU table must fit beside them for two blocks per CU
-    static constexpr int NST = NEEDLUT && T::NW == 4 ? 2 : 3;
+    static constexpr int NST = NEEDLUT && T::BM * T::BN < 128 * 256 ? 2 : 3;
 #else
-    static constexpr int NST = NEEDLUT && T::NW == 4 ? 2 : VK_DMA_STAGES;
+    static constexpr int NST = NEEDLUT && T::BM * T::BN < 128 * 256 ? 2 : VK_DMA_STAGES;
 #endif
     static constexpr int W_INS = W_BYTES / 1024 / T::NW;   // DMA instructions per wave per stage: W
     static constexpr int A_INS = A_BYTES / 1024 / T::NW;   //                                     A
@@ -665,14 +665,18 @@ struct DmaCfg {
 #ifndef VK_MIN_BLOCKS_SMALL
 #define VK_MIN_BLOCKS_SMALL 2
 #endif
-// blocks per CU the register allocator must allow: 64 x 128 tiles without a GELU table can run more
+// waves per SIMD the register allocator must allow (the second __launch_bounds__ argument):
+// blocks per CU x waves per block / 4. Two blocks per CU, three for 64 x 128 tiles without a GELU
+// table, one for the 128 x 256 tile.
 template <class T, int EPI>
-constexpr int dma_min_blocks() {
-    return T::NW == 8 ? 1 : (T::BM * T::BN <= 64 * 128 && EPI != EPI_GEGLU && EPI != EPI_GELU ? VK_MIN_BLOCKS_SMALL : 2);
+constexpr int dma_waves_per_simd() {
+    const int blocks = T::BM * T::BN >= 128 * 256 ? 1
+                     : (T::BM * T::BN <= 64 * 128 && EPI != EPI_GEGLU && EPI != EPI_GELU ? VK_MIN_BLOCKS_SMALL : 2);
+    return blocks * T::NW / 4;
 }
 
 template <int SRC, int EPI, class T>
-__global__ void __launch_bounds__(T::NT, (dma_min_blocks<T, EPI>())) gemm_dma_kernel(const GemmParams p) {
+__global__ void __launch_bounds__(T::NT, (dma_waves_per_simd<T, EPI>())) gemm_dma_kernel(const GemmParams p) {
     using D = DmaCfg<SRC, EPI, T>;
     constexpr int BM = T::BM, BN = T::BN, MS = T::MS, NS = T::NS, NST = D::NST;
     constexpr bool TWO = D::TWO, FUSED = D::FUSED;
