@@ -91,6 +91,23 @@ def roofline(ops, nbytes, seconds):
             "frac": round(achieved / PEAK_INT8_TOPS, 4)}
 
 
+def vendor_planar_us(L, stream, steps=10):
+    """hipBLASLt (torch._int_mm) on the int8 GEMM of the reference's planar route for this layer:
+    the stacked [hi; lo] planes [2M x K] times W^T [K x N] -> int32 (src/engine.cu:155, 195, 212,
+    276), without the separate epilogue or im2col passes that route also needs. A comparison point
+    for the fused kernel, not part of the product."""
+    import torch
+
+    try:
+        A = torch.randint(-128, 128, (2 * L.M, L.Kp), dtype=torch.int8, device="cuda")
+        W = torch.randint(-128, 128, (L.Np, L.Kp), dtype=torch.int8, device="cuda")
+        Wt = W.t()
+        with torch.cuda.stream(stream):
+            return round(time_launches(lambda: torch._int_mm(A, Wt), stream, steps, 3) * 1e3, 2)
+    except RuntimeError:
+        return None
+
+
 def cpu_time(L, h, reps, rows=None):
     import numpy as np
 
@@ -207,6 +224,7 @@ def main():
     log(f"[bench] {L.name}: {ms * 1e3:.1f} us/launch, {tops:.1f} TOPS ({100 * tops / PEAK_INT8_TOPS:.1f}% of int8 peak)")
     traffic, traffic_src = pmc_traffic()
 
+    vendor_c2 = vendor_planar_us(L, stream)
     roof = roofline(L.ops, L.hbm_bytes, ms * 1e-3)
     roof["traffic"] = traffic
     roof.update({"traffic_source": traffic_src, "kernel": "vk::gemm_dma_kernel<SRC_I16, EPI_GEGLU, Tile<128,128,4,1>>",
@@ -230,6 +248,7 @@ def main():
                    "M": L.M, "K": L.K, "N": L.N, "epilogue": "GEGLU + rowmax", "source": "SRC_I16"},
         "pct_int8_peak": round(100 * tops / PEAK_INT8_TOPS, 2),
         "roofline": roof,
+        "hipblaslt_planar_gemm_us": vendor_c2,
     }
 
     # ---- the other configurations (one line each in "configs")
@@ -244,6 +263,7 @@ def main():
                               "pct_int8_peak": round(100 * Lc.ops / (t * 1e-3) / 1e12 / PEAK_INT8_TOPS, 2),
                               "gbs_algorithmic": round(Lc.hbm_bytes / (t * 1e-3) / 1e9, 1),
                               "roofline": roofline(Lc.ops, Lc.hbm_bytes, t * 1e-3)}
+            table[Lc.name]["hipblaslt_planar_gemm_us"] = vendor_planar_us(Lc, stream)
             if not args.no_cpu:
                 table[Lc.name]["cpu_ms"] = round(cpu_time(Lc, p.h, 3) * 1e3, 2)
             log(f"[bench] {Lc.name}: {table[Lc.name]}")

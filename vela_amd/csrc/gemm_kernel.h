@@ -412,10 +412,12 @@ __device__ __forceinline__ void fused_epilogue_t(const GemmParams& p, const v4i 
         return add_sat(cvt_sat(__builtin_floor(X)), b_);
     };
     // GELU factor (lut16i) for tables with 0 <= L <= 65536
+    // z = x + 2^20 clamped to [-1, 2^21]; index (z >> 10) + 1 = (x >> 10) + 1025 and z & 1023 =
+    // x & 1023 (2^20 is a multiple of 1024), so the offset folds into the LDS address
     auto phi = [&](int x) -> int {
-        const int z = min(max(x, -1048577), 1048576) + 1048576;   // [-1, 2^21]
-        const int2 t = sh.lut[(z >> 10) + 1];
-        return t.x + (__mul24(t.y, z & 1023) >> 10);
+        const int xc = min(max(x, -1048577), 1048576);
+        const int2 t = sh.lut[(xc >> 10) + 1025];
+        return t.x + (__mul24(t.y, xc & 1023) >> 10);
     };
     // floor((y * phi(y) + 2^15) / 2^16) for 0 <= phi <= 65536 (never saturates)
     auto gelu_fast = [&](int y) -> double {
