@@ -91,6 +91,13 @@ int vgemm_supported(int Mp, int Np, int Kp);
 void vgemm_set_variant(int v);
 int vgemm_get_variant(void);
 
+/* Output rows per tile (128) of the halo-reuse 3x3 kernel that vgemm_hl2 runs for a SRC_CONV16 source
+ * with this geometry and epilogue when no variant is forced, or 0 when such calls run the
+ * implicit-im2col tile kernels. The halo kernel takes stride 1, C % 64 == 0, output rows of at most
+ * 16 pixels (eight or more whole rows per tile), H a multiple of the rows per tile, and no GELU-table
+ * epilogue. No counterpart in the reference; for tests and tuning. */
+int vgemm_conv16_halo_rows(int H, int W, int C, int stride, int epi);
+
 /* Split-K: force the number of K partitions for calls that pass a workspace (0 = automatic). */
 void vgemm_set_splitk(int s);
 /* Workspace bytes vgemm_hl2 uses for this shape at the current settings (0 = no split-K). */

@@ -164,5 +164,27 @@ def test_workspace_heuristic():
     lib.vgemm_set_variant(-1)
 
 
+@pytest.mark.parametrize("geom,epi,rows", [
+    ((16, 16, 1280, 1), 0, 128),   # eight output rows per tile
+    ((16, 16, 1280, 1), 4, 128),   # SPLIT3
+    ((16, 8, 64, 1), 0, 128),      # sixteen rows of 8 pixels
+    ((32, 4, 64, 1), 0, 128),      # 32 rows of 4 pixels: a 34 x 6 patch
+    ((64, 2, 64, 1), 0, 0),        # 64 rows of 2 pixels: a 66 x 4 patch does not fit
+    ((32, 32, 640, 1), 0, 0),      # four rows per tile: the tile kernels measured faster
+    ((64, 64, 320, 1), 0, 0),
+    ((8, 8, 1280, 1), 0, 0),       # a tile would span two images
+    ((12, 16, 64, 1), 0, 0),       # 12 rows are not a multiple of 8
+    ((16, 16, 1280, 1), 2, 0),     # GEGLU keeps its table on the tile kernels
+    ((16, 16, 1280, 1), 3, 0),     # GELU likewise
+    ((16, 16, 1280, 2), 0, 0),     # stride 2
+    ((16, 16, 32, 1), 0, 0),       # C % 64 != 0
+])
+def test_conv16_halo_rows(geom, epi, rows):
+    """Selection of the halo-reuse 3x3 kernel: stride 1, C % 64, at least eight whole output rows per
+    128-row tile, a patch of at most 208 pixels, no GELU table."""
+    H, W, C, stride = geom
+    assert _lib.load().vgemm_conv16_halo_rows(H, W, C, stride, epi) == rows
+
+
 def test_version():
     assert b"gfx950" in _lib.load().vgemm_version()

@@ -231,6 +231,57 @@ def test_conv16_with_shifts(variant):
     c.check(what=f"conv16 e v{variant}")
 
 
+# (B, H, W, C) of stride-1 SRC_CONV16 problems that run the halo kernel (128-row tiles of whole
+# output rows)
+HALO_GEOMS = [
+    (3, 16, 16, 64),    # eight output rows per tile, two tiles per image
+    (2, 16, 8, 128),    # sixteen rows of 8 pixels: one tile per image
+    (1, 32, 16, 192),   # three channel chunks
+    (1, 32, 4, 64),     # 32 rows of 4 pixels
+]
+
+
+@pytest.mark.parametrize("epi", [vg.EPI_PLAIN, vg.EPI_SPLIT3])
+@pytest.mark.parametrize("geom", HALO_GEOMS)
+def test_conv16_halo(geom, epi):
+    """The halo-reuse 3x3 kernel (one input patch per 64-channel chunk shared by the nine taps) gives
+    the oracle's bytes: whole-row and whole-image tiles, partial last tiles, partial column tiles,
+    residual and row max (src/gemm_hl.cu:104-114 addressing, :40-52 epilogue)."""
+    B, H, W, C = geom
+    assert vg.conv16_halo_rows(H, W, C, 1, epi) == 128
+    if epi == vg.EPI_SPLIT3:
+        c = Case(vg.SRC_CONV16, B * H * W, 192, 9 * C, epi=epi, seed=50, conv=(B, H, W, C, 1), Cs=64)
+    else:
+        c = Case(vg.SRC_CONV16, B * H * W, 200, 9 * C, seed=51, conv=(B, H, W, C, 1), residual=True, rowmax=True)
+    c.img[0, 0, :3] = -32768
+    c.check(what=f"halo {geom} epi {epi}")
+
+
+@pytest.mark.parametrize("geom", HALO_GEOMS[:3])
+def test_conv16_halo_shifts(geom):
+    """Caller shifts e in [0, 17] per output row: the patch is shared by rows with different e, so the
+    quantisation happens per fragment row as the nine taps read it."""
+    B, H, W, C = geom
+    assert vg.conv16_halo_rows(H, W, C, 1, vg.EPI_PLAIN) == 128
+    c = Case(vg.SRC_CONV16, B * H * W, 128, 9 * C, seed=52, conv=(B, H, W, C, 1), residual=True)
+    c.img[0, 1, :5] = -32768
+    c.e = rng(53).integers(0, 18, c.M).astype(np.int32)
+    c.e[::5] = 0
+    c.check(what=f"halo e {geom}")
+
+
+@pytest.mark.parametrize("splits", [2, 3])
+def test_conv16_halo_splitk(splits):
+    """Split-K over channel chunks (2 + 1 and 1 + 1 + 1 of three chunks) through the workspace."""
+    vg.set_splitk(splits)
+    B, H, W, C = HALO_GEOMS[2]
+    assert vg.conv16_halo_rows(H, W, C, 1, vg.EPI_PLAIN) == 128
+    c = Case(vg.SRC_CONV16, B * H * W, 128, 9 * C, seed=54, conv=(B, H, W, C, 1), residual=True, rowmax=True)
+    nb = vg.workspace_bytes(c.Mp, c.M, c.Np, c.N, c.Kp, 0)
+    assert nb > 0
+    c.check(ws_bytes=nb, what=f"halo splitk {splits}")
+
+
 @pytest.mark.parametrize("src", [vg.SRC_I8, vg.SRC_I16])
 def test_exact_slow_path(src):
     """Shifts s - e outside [1, 52] (left shifts, s = 0, deep right shifts) and |acc * m| beyond 2^52

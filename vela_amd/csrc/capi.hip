@@ -3,6 +3,7 @@
 // src/kernels.cu:733); a failed check returns VGEMM_ERR_ARG where the reference throws.
 #include <cstdarg>
 #include <cstdio>
+#include <algorithm>
 #include <cstring>
 #include <string>
 
@@ -15,6 +16,8 @@ hipError_t launch_gemm_x32(int variant, int epi, const GemmParams& p, int batch,
 hipError_t launch_gemm_conv32(int variant, int epi, const GemmParams& p, int batch, hipStream_t st);
 hipError_t launch_gemm_i16(int variant, int epi, const GemmParams& p, int batch, hipStream_t st);
 hipError_t launch_gemm_conv16(int variant, int epi, const GemmParams& p, int batch, hipStream_t st);
+int conv_halo_bm(int epi, int H, int W, int C, int stride, int Ho, int Wo);
+hipError_t launch_gemm_conv16_halo(int bm, int epi, const GemmParams& p, hipStream_t st);
 hipError_t launch_gemm_raw(int variant, const GemmParams& p, int batch, hipStream_t st);
 hipError_t launch_splitk_epilogue(int epi, const GemmParams& p, hipStream_t st);
 hipError_t launch_quant_rows(hipStream_t st, const int32_t* X, int M, int K, int ldx, int8_t* hi, int8_t* lo, int32_t* e, int Kp);
@@ -154,10 +157,18 @@ void vgemm_set_variant(int v) { g_variant = v; }
 int vgemm_get_variant(void) { return g_variant; }
 void vgemm_set_splitk(int s) { g_splitk = s < 0 ? 0 : s; }
 
+int vgemm_conv16_halo_rows(int H, int W, int C, int stride, int epi) {
+    if (H <= 0 || W <= 0 || C <= 0 || stride <= 0) return 0;
+    return vk::conv_halo_bm(epi, H, W, C, stride, (H - 1) / stride + 1, (W - 1) / stride + 1);
+}
+
 size_t vgemm_workspace_bytes(int Mp, int Mreal, int Np, int Nreal, int Kp, int epi) {
     (void)Mp; (void)Np; (void)epi;
-    int v = g_variant >= 0 && g_variant < NVARIANT ? g_variant : pick_variant(Mreal, Nreal, Kp);
-    return ws_bytes_for(v, Mreal, Nreal, pick_splitk(v, Mreal, Nreal, Kp));
+    if (g_variant >= 0 && g_variant < NVARIANT) return ws_bytes_for(g_variant, Mreal, Nreal, pick_splitk(g_variant, Mreal, Nreal, Kp));
+    // the automatic choice, or the 128- or 64-row tiles of the halo convolution kernel
+    size_t nb = 0;
+    for (int v : {pick_variant(Mreal, Nreal, Kp), 0, 1}) nb = std::max(nb, ws_bytes_for(v, Mreal, Nreal, pick_splitk(v, Mreal, Nreal, Kp)));
+    return nb;
 }
 
 int vgemm_hl2(void* stream, const VgemmASrc* A, int Mp, int Mreal, const int8_t* W, int ldw, int Np, int Nreal, int Kp,
@@ -251,18 +262,26 @@ int vgemm_hl2(void* stream, const VgemmASrc* A, int Mp, int Mreal, const int8_t*
     }
     p.vec_store = vec ? 1 : 0;
 
-    int variant = g_variant >= 0 && g_variant < NVARIANT ? g_variant : pick_variant(Mreal, Nreal, Kp);
+    // stride-1 3x3 convolutions of int16 images with C % 64 == 0 run the halo-reuse kernel unless a
+    // tile variant is forced; its K steps are 64-channel chunks (each covering all nine taps)
+    const int halo_bm = A->src == VGEMM_SRC_CONV16 && g_variant < 0 ? vk::conv_halo_bm(epi, p.H, p.W, p.C, p.stride, p.Ho, p.Wo) : 0;
+    int variant = halo_bm ? (halo_bm == 128 ? 0 : 1) : g_variant >= 0 && g_variant < NVARIANT ? g_variant : pick_variant(Mreal, Nreal, Kp);
     if (variant >= 3 && (A->src == VGEMM_SRC_X32 || A->src == VGEMM_SRC_CONV32)) variant = 0;
     const int BM = TILES[variant].BM, BN = TILES[variant].BN;
     p.mtiles = cdiv(Mreal, BM);
     p.ntiles = cdiv(Nreal, BN);
-    const int nK = (Kp + 63) / 64;
+    const int nK = halo_bm ? p.C / 64 : (Kp + 63) / 64;
     int splits = E->ws ? pick_splitk(variant, Mreal, Nreal, Kp) : 1;
     if (splits > 1 && ws_bytes_for(variant, Mreal, Nreal, splits) > E->ws_bytes) splits = 1;
+    if (splits > nK) splits = nK;
     hipStream_t st = static_cast<hipStream_t>(stream);
+    auto run = [&](int e) {
+        if (halo_bm) return hip_status(vk::launch_gemm_conv16_halo(halo_bm, e, p, st), "gemm_hl halo conv launch");
+        return launch_src(A->src, variant, e, p, st);
+    };
     if (splits <= 1) {
         p.ksplit = 1; p.kper = nK;
-        return launch_src(A->src, variant, epi, p, st);
+        return run(epi);
     }
     if (!aligned16(E->ws)) return fail(VGEMM_ERR_ARG, "gemm_hl: workspace must be 16-byte aligned");
     p.ksplit = splits;
@@ -271,7 +290,7 @@ int vgemm_hl2(void* stream, const VgemmASrc* A, int Mp, int Mreal, const int8_t*
     p.ws = static_cast<int32_t*>(E->ws);
     p.ws_rows = p.mtiles * BM;
     p.ws_ld = p.ntiles * BN;
-    const int rc = launch_src(A->src, variant, vk::EPI_PARTIAL, p, st);
+    const int rc = run(vk::EPI_PARTIAL);
     if (rc) return rc;
     return hip_status(vk::launch_splitk_epilogue(epi, p, st), "gemm_hl split-K epilogue");
 }

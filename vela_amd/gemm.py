@@ -19,7 +19,7 @@ SRC_I8, SRC_X32, SRC_CONV32, SRC_I16, SRC_CONV16 = 0, 1, 2, 3, 4
 __all__ = [
     "ASrc", "AEpi", "VgemmError", "EPI_PLAIN", "EPI_SPLIT3", "EPI_GEGLU", "EPI_GELU", "EPI_QKV",
     "SRC_I8", "SRC_X32", "SRC_CONV32", "SRC_I16", "SRC_CONV16", "k_gemm_hl2", "k_gemm_hl", "k_conv_e",
-    "gemm_hl_supported", "set_variant", "get_variant", "set_splitk", "workspace_bytes", "Gemm",
+    "gemm_hl_supported", "set_variant", "get_variant", "set_splitk", "conv16_halo_rows", "workspace_bytes", "Gemm",
     "k_quant_rows", "k_epilogue", "k_pixmax", "k_im2col3", "k_epilogue_split", "k_epilogue_geglu_q",
     "fill_u32", "Graph", "ptr", "stream_ptr",
 ]
@@ -80,6 +80,11 @@ def get_variant() -> int:
 def set_splitk(s: int) -> None:
     """Force the split-K partition count for calls with a workspace (0 = automatic)."""
     load().vgemm_set_splitk(s)
+
+
+def conv16_halo_rows(H: int, W: int, C: int, stride: int, epi: int = EPI_PLAIN) -> int:
+    """Rows per tile of the halo-reuse 3x3 kernel for this SRC_CONV16 geometry (0: not used)."""
+    return int(load().vgemm_conv16_halo_rows(H, W, C, stride, epi))
 
 
 def workspace_bytes(Mp: int, Mreal: int, Np: int, Nreal: int, Kp: int, epi: int = EPI_PLAIN) -> int:
