@@ -1,0 +1,82 @@
+"""GPU parity of the row-stationary kernel (shallow K, many rows: the C2 GEGLU up-projection path)
+against the CPU oracle, byte for byte.
+
+The kernel is forced with variant 4 on shapes where it applies (int16 rows or int8 planes, Kp <= 640,
+output columns a multiple of four). Cases follow src/test_gemm_hl.cu:53-86 (random operands, e
+shifts, residual) and cover what is particular to this kernel: the two geometries (Kp <= 320 with
+32 rows per wave, Kp <= 640 with 16), K not a multiple of 64, partial row stripes and W chunks,
+blocks that stream many chunks (large M) or one chunk (small M), and the three epilogue forms
+(b folded into the FP64 constant, the general FP64 form, the int64 formula).
+"""
+import numpy as np
+import pytest
+
+from tests.test_gpu_gemm import Case, rng
+from vela_amd import gemm as vg
+
+pytestmark = pytest.mark.gpu
+
+STRIPE = 4
+
+
+@pytest.fixture(autouse=True)
+def _stripe(gpu):
+    vg.set_variant(STRIPE)
+    vg.set_splitk(0)
+    yield
+    vg.set_variant(-1)
+    vg.set_splitk(0)
+
+
+# (M, N, K): geometry 0 (Kp <= 320) and 1 (Kp <= 640), partial stripes/chunks, one-chunk and
+# many-chunk blocks
+SHAPES = [(300, 200, 320), (257, 136, 64), (130, 96, 200), (200, 128, 328), (129, 64, 640), (4100, 640, 320), (2100, 320, 600)]
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+@pytest.mark.parametrize("src", [vg.SRC_I16, vg.SRC_I8])
+def test_stripe_plain_residual(src, shape):
+    M, N, K = shape
+    Case(src, M, N, K, seed=60 + K % 97, residual=True, rowmax=True, s_range=(16, 24)).check(what=f"stripe {src} {shape}")
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+@pytest.mark.parametrize("src", [vg.SRC_I16, vg.SRC_I8])
+def test_stripe_shifts(src, shape):
+    """Per-row shifts e in [0, 11] (the general FP64 form, src/test_gemm_hl.cu:60-62)."""
+    M, N, K = shape
+    Case(src, M, N, K, seed=70 + K % 89, residual=True, e_max=11).check(what=f"stripe e {src} {shape}")
+
+
+@pytest.mark.parametrize("epi", [vg.EPI_PLAIN, vg.EPI_GEGLU, vg.EPI_GELU])
+@pytest.mark.parametrize("K", [320, 512])
+def test_stripe_epilogues(epi, K):
+    """Each epilogue in each form: folded (e = 0, small b), general (e != 0), b near +-2^31, a GEGLU
+    product far beyond 2^31, and the int64 formula (shifts outside [1, 52], wrapping m)."""
+    forms = [
+        ("fold", dict(s_range=(16, 24))),
+        ("e", dict(s_range=(16, 24), e_max=3)),
+        ("b near 2^31", dict(s_range=(16, 20), m_range=(1 << 10, 1 << 12), b_range=(-(2**31), 2**31))),
+        ("large y", dict(s_range=(16, 16), m_range=(1 << 16, 1 << 18))),
+        ("left shifts", dict(s_range=(-6, 3), m_range=(1, 1 << 10), e_max=5)),
+        ("deep shifts", dict(s_range=(50, 70))),
+        ("wrapping m", dict(s_range=(20, 40), m_range=((1 << 30), (1 << 31) - 1))),
+    ]
+    for i, (name, kw) in enumerate(forms):
+        Case(vg.SRC_I16, 384, 256, K, epi=epi, seed=80 + i, rowmax=True, residual=epi == vg.EPI_PLAIN, **kw).check(what=f"{name} epi {epi} K {K}")
+
+
+def test_stripe_lut_outside_range():
+    lut = rng(5).integers(-70000, 140000, 2049).astype(np.int32)
+    for epi in (vg.EPI_GEGLU, vg.EPI_GELU):
+        Case(vg.SRC_I16, 256, 128, 320, epi=epi, seed=90, lut=lut, rowmax=True).check(what=f"stripe lut epi {epi}")
+
+
+def test_stripe_c2_rows():
+    """The C2 geometry (K = 320, N = 2560 interleaved a/g columns, GEGLU + row max) on 4096 rows,
+    with activations holding -32768 and 32767 and a Laplace-like spread."""
+    c = Case(vg.SRC_I16, 4096, 2560, 320, epi=vg.EPI_GEGLU, seed=91, rowmax=True, s_range=(16, 24))
+    c.q[0, :] = -32768
+    c.q[1, :] = 32767
+    c.q[2, ::2] = -32768
+    c.check(what="stripe C2 rows")

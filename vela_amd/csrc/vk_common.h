@@ -40,6 +40,7 @@ struct GemmParams {
     int Cs; int32_t* Y1; int32_t* Y2;
     const int32_t* Lphi; uint32_t* rowmax;
     int vec_store;             // output rows/pointers allow 16-byte stores
+    unsigned y_bytes;          // byte extent of Y (and of the residual) from row 0 to the last output element
     // split-K partials: ws[(split * 2 + plane) * ws_rows + row][col], row stride ws_ld
     int ksplit, kper;
     int32_t* ws; int ws_rows, ws_ld;
