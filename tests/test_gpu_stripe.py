@@ -1,12 +1,13 @@
 """GPU parity of the row-stationary kernel (shallow K, many rows: the C2 GEGLU up-projection path)
 against the CPU oracle, byte for byte.
 
-The kernel is forced with variant 4 on shapes where it applies (int16 rows or int8 planes, Kp <= 640,
-output columns a multiple of four). Cases follow src/test_gemm_hl.cu:53-86 (random operands, e
-shifts, residual) and cover what is particular to this kernel: the two geometries (Kp <= 320 with
-32 rows per wave, Kp <= 640 with 16), K not a multiple of 64, partial row stripes and W chunks,
-blocks that stream many chunks (large M) or one chunk (small M), and the three epilogue forms
-(b folded into the FP64 constant, the general FP64 form, the int64 formula).
+The kernel is forced with variant 4 on shapes where it applies (int16 rows or int8 planes, Kp <= 320,
+output columns a multiple of four); shapes with a deeper K run the tile kernels under the same
+setting, which these cases then cover as well. Cases follow src/test_gemm_hl.cu:53-86 (random
+operands, e shifts, residual) and cover what is particular to this kernel: K not a multiple of 64,
+partial row stripes and W chunks, blocks that stream many chunks (large M) or one chunk (small M),
+and its two epilogue forms (the integer form, and the int64 formula for blocks with row shifts,
+shifts outside [0, 31], possible saturation or a table outside [0, 65536]).
 """
 import numpy as np
 import pytest
@@ -28,8 +29,8 @@ def _stripe(gpu):
     vg.set_splitk(0)
 
 
-# (M, N, K): geometry 0 (Kp <= 320) and 1 (Kp <= 640), partial stripes/chunks, one-chunk and
-# many-chunk blocks
+# (M, N, K): Kp <= 320 (the kernel) and deeper K (tile kernels), partial stripes/chunks, one-chunk
+# and many-chunk blocks
 SHAPES = [(300, 200, 320), (257, 136, 64), (130, 96, 200), (200, 128, 328), (129, 64, 640), (4100, 640, 320), (2100, 320, 600)]
 
 

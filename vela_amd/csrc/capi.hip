@@ -19,7 +19,7 @@ hipError_t launch_gemm_conv16(int variant, int epi, const GemmParams& p, int bat
 int conv_halo_bm(int epi, int H, int W, int C, int stride, int Ho, int Wo);
 hipError_t launch_gemm_conv16_halo(int bm, int epi, const GemmParams& p, hipStream_t st);
 hipError_t launch_gemm_raw(int variant, const GemmParams& p, int batch, hipStream_t st);
-hipError_t launch_stripe(int src, int shape, int epi, const GemmParams& p, hipStream_t st);
+hipError_t launch_stripe(int src, int epi, const GemmParams& p, hipStream_t st);
 hipError_t launch_splitk_epilogue(int epi, const GemmParams& p, hipStream_t st);
 hipError_t launch_quant_rows(hipStream_t st, const int32_t* X, int M, int K, int ldx, int8_t* hi, int8_t* lo, int32_t* e, int Kp);
 hipError_t launch_pixmax(hipStream_t st, const int32_t* X, int rows, int C, uint32_t* pm);
@@ -76,41 +76,34 @@ constexpr int NCU = 256;   // MI355X compute units
 
 int cdiv(long long a, long long b) { return int((a + b - 1) / b); }
 
-// Variant 4 forces the row-stationary kernel (stripe_kernel.h) where it applies.
+// Variant 4 forces the row-stationary kernel (stripe_kernel.h) where it applies: int16 rows or int8
+// planes, epilogue PLAIN / GEGLU / GELU, Kp <= 320, output columns in whole groups of four and
+// 16-byte aligned output, Y extent below 2^31. Blocks of 128 rows stream 64-row W chunks.
 constexpr int VARIANT_STRIPE = 4;
-
-// Geometry of the row-stationary kernel for a problem, or -1 where it does not apply: int16 rows or
-// int8 planes, epilogue PLAIN / GEGLU / GELU, Kp <= 640, output columns in whole groups of four
-// and 16-byte stores, Y extent below 2^31. Shape 0: Kp <= 320, 128-row blocks, 64-row W chunks;
-// shape 1: Kp <= 640, 64-row blocks, 32-row W chunks.
-struct StripeGeom { int shape, BM, CH; };
-constexpr StripeGeom STRIPE_GEOM[2] = {{0, 128, 64}, {1, 64, 32}};
+constexpr int STRIPE_BM = 128, STRIPE_CH = 64;
 constexpr int STRIPE_NCOLS = 1280;   // W rows per block, at most
 
-int stripe_shape(int src, int epi, const vk::GemmParams& p) {
-    if (src != VGEMM_SRC_I16 && src != VGEMM_SRC_I8) return -1;
-    if (epi != VGEMM_EPI_PLAIN && epi != VGEMM_EPI_GEGLU && epi != VGEMM_EPI_GELU) return -1;
-    if (p.Kp > 640 || !p.vec_store) return -1;
+bool stripe_applies(int src, int epi, const vk::GemmParams& p) {
+    if (src != VGEMM_SRC_I16 && src != VGEMM_SRC_I8) return false;
+    if (epi != VGEMM_EPI_PLAIN && epi != VGEMM_EPI_GEGLU && epi != VGEMM_EPI_GELU) return false;
+    if (p.Kp > 320 || !p.vec_store) return false;
     const int nout = epi == VGEMM_EPI_GEGLU ? p.Nreal / 2 : p.Nreal;
-    if (nout % 4) return -1;
+    if (nout % 4) return false;
     const long long yext = ((long long)(p.Mreal - 1) * p.ldy + nout) * 4;
-    if (yext > MAX_EXTENT) return -1;
-    return p.Kp <= 320 ? 0 : 1;
+    return yext <= MAX_EXTENT;
 }
 
 // Automatic use: many rows (the kernel keeps a block's rows in registers and streams all of its
-// columns, so it needs a few hundred row stripes to fill the GPU).
-bool stripe_auto(const vk::GemmParams& p, int shape) {
-    return cdiv(p.Mreal, STRIPE_GEOM[shape].BM) >= 2 * NCU / 4 && p.Mreal >= 16384;
-}
+// columns, so it needs a few hundred row stripes to fill the GPU), and no per-row shifts (rows with
+// e != 0 leave the kernel's integer epilogue for its slow int64 form; the tile kernels cover them).
+bool stripe_auto(const vk::GemmParams& p) { return cdiv(p.Mreal, STRIPE_BM) >= 2 * NCU / 4 && p.Mreal >= 16384 && !p.e; }
 
 // Blocks = row stripes x column ranges: as few column ranges as the table allows, raised until
 // there are two blocks per CU.
-void stripe_grid(vk::GemmParams& p, int shape) {
-    const StripeGeom g = STRIPE_GEOM[shape];
-    const int nch = cdiv(p.Nreal, g.CH);
-    const int mt = cdiv(p.Mreal, g.BM);
-    int cs = std::max(cdiv(nch, STRIPE_NCOLS / g.CH), std::min(nch, cdiv(2 * NCU, mt)));
+void stripe_grid(vk::GemmParams& p) {
+    const int nch = cdiv(p.Nreal, STRIPE_CH);
+    const int mt = cdiv(p.Mreal, STRIPE_BM);
+    int cs = std::max(cdiv(nch, STRIPE_NCOLS / STRIPE_CH), std::min(nch, cdiv(2 * NCU, mt)));
     const int kper = cdiv(nch, cs);
     cs = cdiv(nch, kper);
     p.mtiles = mt;
@@ -308,12 +301,11 @@ int vgemm_hl2(void* stream, const VgemmASrc* A, int Mp, int Mreal, const int8_t*
     hipStream_t st = static_cast<hipStream_t>(stream);
 
     // shallow GEMMs with many rows: the row-stationary kernel (forced by variant 4 where it applies)
-    const int sshape = stripe_shape(A->src, epi, p);
-    if (sshape >= 0 && (g_variant == VARIANT_STRIPE || (g_variant < 0 && stripe_auto(p, sshape)))) {
+    if (stripe_applies(A->src, epi, p) && (g_variant == VARIANT_STRIPE || (g_variant < 0 && stripe_auto(p)))) {
         const int nout = epi == VGEMM_EPI_GEGLU ? Nreal / 2 : Nreal;
         p.y_bytes = unsigned(((long long)(Mreal - 1) * E->ldy + nout) * 4);
-        stripe_grid(p, sshape);
-        return hip_status(vk::launch_stripe(A->src, sshape, epi, p, st), "gemm_hl stripe launch");
+        stripe_grid(p);
+        return hip_status(vk::launch_stripe(A->src, epi, p, st), "gemm_hl stripe launch");
     }
 
     // stride-1 3x3 convolutions of int16 images with C % 64 == 0 run the halo-reuse kernel unless a

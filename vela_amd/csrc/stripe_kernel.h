@@ -1,90 +1,93 @@
-// Row-stationary ("stripe") hi/lo GEMM for shallow K (Kp <= 640) with int16 rows (SRC_I16) or int8
+// Row-stationary ("stripe") hi/lo GEMM for shallow K (Kp <= 320) with int16 rows (SRC_I16) or int8
 // planes (SRC_I8), epilogues PLAIN (+ residual), GEGLU and GELU, with or without the row maximum.
 //
-// A block owns BM activation rows and a range of W rows (output columns). Each wave loads its rows
-// once, splits them into hi/lo MFMA fragments and keeps those in registers for the whole block;
-// W streams through LDS in chunks of CH rows (a 2-stage ring filled by buffer-load DMA), and each
-// chunk is multiplied and requantised before the next. So an activation row is read from memory
-// and split once per block instead of once per 128-column tile, the GELU table and the per-column
-// constants are set up once per block, and the row maximum of a wave's rows over the block's
-// columns needs one atomic per row at the end.
+// A block owns 128 activation rows (32 per wave) and a range of W rows (output columns). Each wave
+// loads its rows once, splits them into hi/lo MFMA fragments and keeps those in registers for the
+// whole block; W streams through LDS in chunks of 64 rows (a 2-stage ring filled by buffer-load
+// DMA), and each chunk is multiplied and requantised before the next. So an activation row is read
+// and split once per block, the GELU table and the per-column constants are set up once per block,
+// and the row maximum needs one atomic per row and wave at the end.
 //
-// Epilogue (src/gemm_hl.cu:40-52, 279-302). When every row of the block has e == 0 and no element
-// can saturate (checked per block from max |m| 2^-s and max |b|), b is folded into the FMA constant:
-// y = floor(A m 2^-s + (128 wsum m 2^-s + 1/2 + b)), exact in FP64 because Kp |m| < 2^30. GEGLU then
-// takes phi(g) from the table as (1024 L[i] + (L[i+1] - L[i]) f) >> 10 (one 24-bit multiply-add),
-// ge = floor((g phi + 2^15) 2^-16) and y = sat32(floor(a 2^-16 ge + 1/2)); both products are exact
-// below 2^53 or saturate monotonically. Other blocks run the general FP64 form with separate
-// saturating adds, or the reference's int64 formula element by element when a shift or multiplier
-// is outside the FP64 range.
+// MFMA: v_mfma_i32_32x32x32_i8 with the activations as the A operand and W as the B operand, so lane
+// l holds output column l % 32 of a 32-column subtile for rows 8g + 4(l / 32) + v (g, v = 0..3): the
+// per-column constants of a lane are one LDS read per chunk, and each output store instruction
+// writes two 128-byte row segments.
+//
+// Epilogue (src/gemm_hl.cu:40-52, 279-302), two exact forms chosen per block:
+//  * integer: every row has e == 0, every shift s lies in [0, 31] and no element can saturate
+//    (checked from max |m| 2^-s and max |b|). Then y = (A m + C) >> s with A = 256 Chi + Clo
+//    (int32, Kp <= 496) and C = 128 wsum m + 2^(s-1) + b 2^s, one v_mad_i64_i32 and one funnel
+//    shift; GELU/GEGLU take phi(g) from the table as (1024 L[i] + (L[i+1] - L[i]) f) >> 10, then
+//    ge = (g phi + 2^15) >> 16 (never saturates, phi <= 65536) and y = sat32((a ge + 2^15) >> 16),
+//    the saturation being detected per wave and handled on a separate branch.
+//  * otherwise the reference's int64 formula element by element (one element per loop iteration,
+//    so that this rarely used form adds few registers to the kernel). The host sends calls with
+//    per-row shifts to the tile kernels, whose FP64 form covers them at speed.
 //
 // Memory ordering: the W DMA of chunk c + 1 is issued right after the barrier of chunk c, and the
 // only vector-memory instructions after it in chunk c are that chunk's output stores, a fixed
 // number per lane (every lane stores unconditionally; rows and columns outside the output go to
 // an out-of-range buffer offset, which the hardware drops). So waiting for at most that many
-// outstanding operations completes the DMA. Blocks whose epilogue loads from memory (residual, b
-// of the general form, the int64 form) wait for all of them instead.
+// outstanding operations completes the DMA. Blocks whose epilogue loads from memory (residual, the
+// int64 form) wait for all of them instead.
 #pragma once
+#include <type_traits>
+
 #include "gemm_kernel.h"
 
 namespace vk {
 
-template <int MS_, int NKM_, int CH_>
-struct Stripe {
-    static constexpr int MS = MS_;       // 16-row MFMA subtiles per wave (rows per wave = 16 MS)
-    static constexpr int NKM = NKM_;     // 64-deep K steps held in registers (Kp <= 64 NKM)
-    static constexpr int CH = CH_;       // W rows per chunk
-    static constexpr int NS = CH / 16;   // 16-column MFMA subtiles per chunk
-    static constexpr int BM = 64 * MS;   // four waves stacked along M
-    static constexpr int KSTEP = CH * 64;            // LDS bytes of one K step of a chunk
-    static constexpr int STAGE = NKM * KSTEP;        // LDS bytes of one chunk
-    static constexpr int NCOLS = 1280;               // W rows (table columns) per block, at most
-    static constexpr int CMAX = NCOLS / CH;          // chunks per block, at most
-    static constexpr int CPT = NCOLS / 256;          // table columns per thread
-    static constexpr int DMA_INS = STAGE / 1024 / 4; // DMA instructions per wave per chunk
-    static_assert(STAGE % 4096 == 0 && NS % 2 == 0, "stripe geometry");
-};
-typedef Stripe<2, 5, 64> StripeA;    // Kp <= 320: 32 rows per wave, 64-row chunks
-typedef Stripe<1, 10, 32> StripeB;   // Kp <= 640: 16 rows per wave, 32-row chunks
+typedef int v16i __attribute__((ext_vector_type(16)));
 
-struct alignas(16) ColConst {
-    double ms;   // m 2^-s
-    double wm;   // 128 wsum m 2^-s; + 1/2 when e == 0; + b as well when the block folds b
+struct StripeCfg {
+    static constexpr int BM = 128;                  // rows per block: four waves of 32
+    static constexpr int NKS = 10;                  // 32-deep K substeps held in registers (Kp <= 320)
+    static constexpr int CH = 64;                   // W rows per chunk
+    static constexpr int NSUB = CH / 32;            // 32-column MFMA subtiles per chunk
+    static constexpr int KSTEP = CH * 64;           // LDS bytes of one 64-deep K step of a chunk
+    static constexpr int STAGE = (NKS / 2) * KSTEP; // LDS bytes of one chunk
+    static constexpr int NCOLS = 1280;              // W rows (table columns) per block, at most
+    static constexpr int CPT = NCOLS / 256;         // table columns per thread
+    static constexpr int DMA_INS = STAGE / 1024 / 4;// DMA instructions per wave per chunk
+    static_assert(STAGE % 4096 == 0, "stripe geometry");
 };
 
-template <class S, bool LUT>
+template <bool LUT>
 struct StripeShared {
-    unsigned char w[2][S::STAGE];
-    ColConst tab[S::NCOLS];
+    unsigned char w[2][StripeCfg::STAGE];
+    int4 tab[StripeCfg::NCOLS];   // per column {m, s, C lo, C hi} of the integer form
     int2 lut[LUT ? 2050 : 1];   // lut[i + 1] = (1024 L[i], L[i+1] - L[i]); lut[0] below, lut[2049] above the table
+    int erow[StripeCfg::BM];    // per-row shifts of the block (int64 form)
     unsigned long long umax;
-    int flag[8];                // emin, emax, smin, smax, column bound failed, table range failed, max |b|, b not foldable
+    int flag[8];                // emin, emax, smin, smax, column bound failed, table range failed, max |b|, |wsum| > 128 Kp
 };
 
 // byte offset inside sh.lut of the raw table as the DMA delivers it (entries 0..2047)
 constexpr unsigned STRIPE_LUT_RAW = 8192;
 
-template <int SRC, int EPI, class S>
+enum { FORM_INT = 0, FORM_EXACT = 1 };
+
+template <int SRC, int EPI>
 __global__ void __launch_bounds__(256, 2) stripe_kernel(const GemmParams p) {
-    constexpr int MS = S::MS, NS = S::NS, NKM = S::NKM, CH = S::CH, BM = S::BM;
+    using S = StripeCfg;
+    constexpr int CH = S::CH, NKS = S::NKS, BM = S::BM;
     constexpr bool NEEDLUT = EPI == EPI_GEGLU || EPI == EPI_GELU;
     constexpr bool GEGLU = EPI == EPI_GEGLU;
-    constexpr bool SMALLK = NKM * 64 <= 496;   // |256 Chi + Clo| < 2^31
-    constexpr int NOUT = GEGLU ? NS / 2 : NS;  // output subtiles per chunk
-    constexpr int STORES = NOUT * MS;          // output stores per lane per chunk
+    constexpr int NOUT = GEGLU ? 1 : S::NSUB;  // output subtiles per chunk
+    constexpr int STORES = NOUT * 16;          // output stores per lane per chunk
     static_assert(SRC == SRC_I16 || SRC == SRC_I8, "stripe sources");
     static_assert(EPI == EPI_PLAIN || EPI == EPI_GEGLU || EPI == EPI_GELU, "stripe epilogues");
 
-    __shared__ __attribute__((aligned(16))) StripeShared<S, NEEDLUT> sh;
+    __shared__ __attribute__((aligned(16))) StripeShared<NEEDLUT> sh;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int fr = lane & 15, fg = lane >> 4;
+    const int lc = lane & 31, lh = lane >> 5;   // MFMA column / row group of this lane
     const TileIdx ti = tile_index(p);
     const int m0 = ti.mt * BM;
     const int nch = (p.Nreal + CH - 1) / CH;
     const int cb = ti.nt * p.kper, ce = min(nch, cb + p.kper);   // this block's chunks
-    const int nK = (p.Kp + 63) >> 6;
-    const int rbase = m0 + wave * 16 * MS;
+    const int nk32 = (p.Kp + 31) >> 5;   // K substeps with data
+    const int rbase = m0 + wave * 32;
     const int nlim = GEGLU ? (p.Nreal >> 1) : p.Nreal;
     if (cb >= ce) return;   // (the host sizes the grid so that every block has a chunk)
 
@@ -94,55 +97,43 @@ __global__ void __launch_bounds__(256, 2) stripe_kernel(const GemmParams p) {
         sh.umax = 0;
     }
 
-    // ---- the wave's activation rows: loads first (they are older than every DMA below)
-    int er[MS];
-    unsigned yoff[MS];   // byte offset of the output row, or out of range
-#pragma unroll
-    for (int ms = 0; ms < MS; ++ms) {
-        const int r = rbase + ms * 16 + fr;
-        er[ms] = (r < p.Mreal && p.e) ? p.e[r] : 0;
-        yoff[ms] = r < p.Mreal ? unsigned(r) * unsigned(p.ldy) * 4u : OOB;
-    }
-    v4i hf[MS][NKM], lf[MS][NKM];
+    // ---- the wave's activation rows (A operand: lane row lc, K bytes [32t + 16lh, +16) of substep t):
+    // loads first, so that they are older than every DMA below
+    v4i hf[NKS], lf[NKS];
     {
         const __amdgpu_buffer_rsrc_t rA0 = make_rsrc(p.a0, p.a0_bytes);
         const __amdgpu_buffer_rsrc_t rA1 = make_rsrc(SRC == SRC_I8 ? p.a1 : p.a0, SRC == SRC_I8 ? p.a1_bytes : p.a0_bytes);
-        v4i raw[MS][NKM][SRC == SRC_I16 ? 2 : 1];
+        const int r = rbase + lc;
+        const bool rok = r < p.Mreal;
+        v4i raw[NKS][SRC == SRC_I16 ? 2 : 1];
 #pragma unroll
-        for (int ms = 0; ms < MS; ++ms) {
-            const int r = rbase + ms * 16 + fr;
-            const bool rok = r < p.Mreal;
-#pragma unroll
-            for (int ks = 0; ks < NKM; ++ks) {
-                const int k0 = ks * 64 + 16 * fg;
-                if (ks < nK) {
-                    if constexpr (SRC == SRC_I16) {
-                        // 16 int16 values = two 16-byte pieces; K % 8 == 0, so each piece is all in or all out
-                        const unsigned off = (unsigned(r) * unsigned(p.lda) + unsigned(k0)) * 2u;
-                        raw[ms][ks][0] = bload16(rA0, rok && k0 < p.K ? off : OOB);
-                        raw[ms][ks][1] = bload16(rA0, rok && k0 + 8 < p.K ? off + 16u : OOB);
-                    } else {
-                        const unsigned off = unsigned(r) * unsigned(p.lda) + unsigned(k0);
-                        const bool ok = rok && k0 < p.Kp;
-                        hf[ms][ks] = bload16(rA0, ok ? off : OOB);
-                        lf[ms][ks] = bload16(rA1, ok ? off : OOB);
-                    }
+        for (int t = 0; t < NKS; ++t) {
+            const int k0 = t * 32 + 16 * lh;
+            if (t < nk32) {
+                if constexpr (SRC == SRC_I16) {
+                    // 16 int16 values = two 16-byte pieces; K % 8 == 0, so each piece is all in or all out
+                    const unsigned off = (unsigned(r) * unsigned(p.lda) + unsigned(k0)) * 2u;
+                    raw[t][0] = bload16(rA0, rok && k0 < p.K ? off : OOB);
+                    raw[t][1] = bload16(rA0, rok && k0 + 8 < p.K ? off + 16u : OOB);
                 } else {
-                    if constexpr (SRC == SRC_I16) raw[ms][ks][0] = raw[ms][ks][1] = v4i{0, 0, 0, 0};
-                    else hf[ms][ks] = lf[ms][ks] = v4i{0, 0, 0, 0};
+                    const unsigned off = unsigned(r) * unsigned(p.lda) + unsigned(k0);
+                    const bool ok = rok && k0 < p.Kp;
+                    hf[t] = bload16(rA0, ok ? off : OOB);
+                    lf[t] = bload16(rA1, ok ? off : OOB);
                 }
+            } else {
+                if constexpr (SRC == SRC_I16) raw[t][0] = raw[t][1] = v4i{0, 0, 0, 0};
+                else hf[t] = lf[t] = v4i{0, 0, 0, 0};
             }
         }
         if constexpr (SRC == SRC_I16) {
 #pragma unroll
-            for (int ms = 0; ms < MS; ++ms)
-#pragma unroll
-                for (int ks = 0; ks < NKM; ++ks) {
-                    const v4i x0 = raw[ms][ks][0], x1 = raw[ms][ks][1];
-                    const unsigned d[8] = {unsigned(x0[0]), unsigned(x0[1]), unsigned(x0[2]), unsigned(x0[3]),
-                                           unsigned(x1[0]), unsigned(x1[1]), unsigned(x1[2]), unsigned(x1[3])};
-                    split16x16(d, hf[ms][ks], lf[ms][ks]);
-                }
+            for (int t = 0; t < NKS; ++t) {
+                const v4i x0 = raw[t][0], x1 = raw[t][1];
+                const unsigned d[8] = {unsigned(x0[0]), unsigned(x0[1]), unsigned(x0[2]), unsigned(x0[3]),
+                                       unsigned(x1[0]), unsigned(x1[1]), unsigned(x1[2]), unsigned(x1[3])};
+                split16x16(d, hf[t], lf[t]);
+            }
         }
     }
 
@@ -158,35 +149,39 @@ __global__ void __launch_bounds__(256, 2) stripe_kernel(const GemmParams p) {
     }
     const int L2048 = NEEDLUT ? p.Lphi[2048] : 0;
     const v4i rW = make_rsrc_words(p.w, p.w_bytes);
-    // instruction j of this wave fills K step ks, LDS rows 16 rg .. 16 rg + 15 of a chunk; lane l
-    // reads 16 bytes of W row w_row (chunk-relative) at K offset w_k (its swizzled position)
+    // instruction j of this wave fills K step ks = q / 4, LDS rows 16 rg .. 16 rg + 15 (rg = q % 4) of
+    // a chunk, q = 5 wave + j; lane l reads 16 bytes of W row wrow(16 rg + l / 4) at its swizzled K
+    // position. With l4 = l / 4: wrow(16 rg + l4) = wrow(l4) + a constant of rg, and the swizzle key
+    // of row 16 rg + l4 is (key(l4) + 2 rg) mod 4, so three per-lane values cover every instruction.
     constexpr int RG = CH / 16;
-    unsigned w_off[S::DMA_INS];
-    int w_row[S::DMA_INS];
-#pragma unroll
-    for (int j = 0; j < S::DMA_INS; ++j) {
-        const int q = wave * S::DMA_INS + j, ks = q / RG, rg = q - ks * RG;
-        const int lr = 16 * rg + (lane >> 2);
-        w_row[j] = wrow_of_lds<EPI, CH>(lr);
-        const int wk = ks * 64 + 16 * ((lane & 3) ^ swz_key(lr));
-        w_off[j] = wk < p.Kp ? unsigned(w_row[j]) * unsigned(p.ldw) + unsigned(wk) : OOB;
-    }
+    static_assert(RG == 4 && S::DMA_INS * 4 == (NKS / 2) * RG, "DMA mapping");
+    const int l4 = lane >> 2;
+    const int wb = GEGLU ? 2 * l4 : l4;                                   // wrow(l4)
+    const int wk0 = 16 * ((lane & 3) ^ swz_key(l4));                      // K offset, rg even
+    const int wk1 = 16 * ((lane & 3) ^ ((swz_key(l4) + 2) & 3));          // K offset, rg odd
+    const unsigned wlane = unsigned(wb) * unsigned(p.ldw);
     auto issue = [&](int c, int stage) {
         const int n0 = c * CH;
         const unsigned sbase = lds_addr(sh.w[stage]);
+        const bool rows_in = n0 + CH <= p.Nreal;   // the whole chunk lies inside W (uniform)
 #pragma unroll
         for (int j = 0; j < S::DMA_INS; ++j) {
             const int q = wave * S::DMA_INS + j, ks = q / RG, rg = q - ks * RG;
-            const bool ok = n0 + w_row[j] < p.Nreal;
-            dma16(rW, ok ? w_off[j] : OOB, unsigned(n0) * unsigned(p.ldw), sbase + unsigned(ks * S::KSTEP + rg * 1024));
+            // wrow(16 rg + l4) - wrow(l4): GEGLU rows 2 lr (lr < 32) and 2 (lr - 32) + 1
+            const int rgo = GEGLU ? (rg < 2 ? 32 * rg : 32 * (rg - 2) + 1) : 16 * rg;
+            const int wk = ks * 64 + ((rg & 1) ? wk1 : wk0);
+            unsigned off = wlane + unsigned(wk) + unsigned(rgo) * unsigned(p.ldw);
+            if (ks * 64 + 64 > p.Kp && wk >= p.Kp) off = OOB;
+            if (!rows_in && n0 + wb + rgo >= p.Nreal) off = OOB;
+            dma16(rW, off, unsigned(n0) * unsigned(p.ldw), sbase + unsigned(ks * S::KSTEP + rg * 1024));
         }
     };
-    if (cb < ce) issue(cb, 0);
+    issue(cb, 0);
 
     // ---- block set-up: column constants of chunks [cb, ce), the expanded GELU table, flags
     vm_wait<S::DMA_INS>();   // the table DMA (older than chunk cb's)
     block_barrier();
-    EpiFlags fl;
+    int form;
     {
         constexpr int LPT = NEEDLUT ? (2050 + 255) / 256 : 1;
         int2 lv[LPT];
@@ -207,38 +202,37 @@ __global__ void __launch_bounds__(256, 2) stripe_kernel(const GemmParams p) {
             }
         }
         const int ncols = (ce - cb) * CH;
-        int bb[S::CPT];
-        int smn = INT_MAX, smx = INT_MIN, bad = 0, bmx = 0, nofold = 0;
+        int4 cc[S::CPT];
+        int smn = INT_MAX, smx = INT_MIN, bad = 0, bmx = 0, wbad = 0;
         double um = 0.0;
 #pragma unroll
         for (int q = 0; q < S::CPT; ++q) {
             const int j = tid + 256 * q;
-            bb[q] = 0;
+            cc[q] = make_int4(0, 0, 0, 0);
             if (j < ncols) {
                 const int n = cb * CH + (j / CH) * CH + wrow_of_lds<EPI, CH>(j % CH);
-                double ms = 0.0, wmv = 0.0;
                 if (n < p.Nreal) {
                     const int4 c = p.cst[n];
+                    cc[q] = c;
                     const i64 mag = (c.x < 0 ? -i64(c.x) : i64(c.x)) * i64(p.Kp);
                     if (mag >= (1LL << 30) || c.y < -1000 || c.y > 1000) bad = 1;
+                    // the bounds below take |acc| <= 2^22 Kp, which needs |wsum| <= 128 Kp
+                    if (uabs(c.w) > 128u * unsigned(p.Kp)) wbad = 1;
                     smn = min(smn, c.y);
                     smx = max(smx, c.y);
-                    if (c.y >= -1000 && c.y <= 1000) {
-                        ms = ldexp(double(c.x), -c.y);
-                        wmv = ldexp(128.0 * (double(c.w) * double(c.x)), -c.y);
-                        // |acc m 2^-s| <= 2^22 Kp |m| 2^-s, since |acc| <= 32768 * 128 * Kp
-                        um = max(um, ldexp(4194304.0 * double(p.Kp) * fabs(double(c.x)), -c.y));
-                        // wm + 1/2 + b is exact when |b| 2^s < 2^51 (numerator below 2^53)
-                        if (ldexp(fabs(double(c.z)), c.y) >= 2251799813685248.0) nofold = 1;
-                    }
-                    bb[q] = c.z;
+                    // |acc m 2^-s| <= 2^22 Kp |m| 2^-s, since |acc| <= 32768 * 128 * Kp
+                    if (c.y >= -1000 && c.y <= 1000) um = max(um, ldexp(4194304.0 * double(p.Kp) * fabs(double(c.x)), -c.y));
+                    else um = 1e300;
                     bmx = max(bmx, int(min(uabs(c.z), 0x7fffffffu)));
                 }
-                sh.tab[j] = ColConst{ms, wmv};
             }
         }
         int emn = INT_MAX, emx = INT_MIN;
-        if (tid < BM && m0 + tid < p.Mreal) emn = emx = p.e ? p.e[m0 + tid] : 0;
+        if (tid < BM) {
+            const int er = (m0 + tid < p.Mreal && p.e) ? p.e[m0 + tid] : 0;
+            sh.erow[tid] = er;
+            if (m0 + tid < p.Mreal) emn = emx = er;
+        }
 #pragma unroll
         for (int o = 32; o; o >>= 1) {
             emn = min(emn, __shfl_xor(emn, o));
@@ -246,8 +240,8 @@ __global__ void __launch_bounds__(256, 2) stripe_kernel(const GemmParams p) {
             smn = min(smn, __shfl_xor(smn, o));
             smx = max(smx, __shfl_xor(smx, o));
             bad |= __shfl_xor(bad, o);
+            wbad |= __shfl_xor(wbad, o);
             bmx = max(bmx, __shfl_xor(bmx, o));
-            nofold |= __shfl_xor(nofold, o);
             um = max(um, __shfl_xor(um, o));
             if constexpr (NEEDLUT) lbad |= __shfl_xor(lbad, o);
         }
@@ -255,9 +249,9 @@ __global__ void __launch_bounds__(256, 2) stripe_kernel(const GemmParams p) {
             if (emn <= emx) { atomicMin(&sh.flag[0], emn); atomicMax(&sh.flag[1], emx); }
             if (smn <= smx) { atomicMin(&sh.flag[2], smn); atomicMax(&sh.flag[3], smx); }
             if (bad) atomicOr(&sh.flag[4], 1);
+            if (wbad) atomicOr(&sh.flag[7], 1);
             if (lbad) atomicOr(&sh.flag[5], 1);
             atomicMax(&sh.flag[6], bmx);
-            if (nofold) atomicOr(&sh.flag[7], 1);
             atomicMax(&sh.umax, __double_as_longlong(um));
         }
         __syncthreads();   // raw table read by everyone, all flags in
@@ -269,16 +263,22 @@ __global__ void __launch_bounds__(256, 2) stripe_kernel(const GemmParams p) {
             }
         }
         const i64 emin = sh.flag[0], emax = sh.flag[1], smin = sh.flag[2], smax = sh.flag[3];
-        fl.fast = !sh.flag[4] && (smin - emax >= 1) && (smax - emin <= 52) && emin >= -1000 && emax <= 1000;
-        if (NEEDLUT && sh.flag[5]) fl.fast = false;
-        fl.ezero = emin > emax || (emin == 0 && emax == 0);
-        fl.fold = fl.fast && fl.ezero && !sh.flag[7] && __longlong_as_double(sh.umax) + double(sh.flag[6]) + 2.0 < 2147483647.0;
-        if (fl.ezero) {
-            // the FMA constant of the e == 0 forms: wm + 1/2, and + b when folded (exact, see above)
+        const bool lut_ok = !NEEDLUT || !sh.flag[5];
+        const bool ezero = emin > emax || (emin == 0 && emax == 0);
+        // no element saturates: |y| <= max 2^22 Kp |m| 2^-s + 1 + max |b| < 2^31
+        const bool nosat = __longlong_as_double(sh.umax) + double(sh.flag[6]) + 2.0 < 2147483647.0;
+        form = ezero && smin >= 0 && smax <= 31 && nosat && lut_ok && !sh.flag[7] ? FORM_INT : FORM_EXACT;
+        form = __builtin_amdgcn_readfirstlane(form);
 #pragma unroll
-            for (int q = 0; q < S::CPT; ++q) {
-                const int j = tid + 256 * q;
-                if (j < ncols) sh.tab[j].wm = (sh.tab[j].wm + 0.5) + (fl.fold ? double(bb[q]) : 0.0);
+        for (int q = 0; q < S::CPT; ++q) {
+            const int j = tid + 256 * q;
+            if (j < ncols) {
+                const int4 c = cc[q];
+                if (form == FORM_INT) {
+                    // C = 128 wsum m + 2^(s-1) + b 2^s (|C| < 2^63: |wsum| <= 128 Kp, s <= 31)
+                    const i64 C = 128LL * i64(c.w) * i64(c.x) + (c.y ? (1LL << (c.y - 1)) : 0) + i64(c.z) * (1LL << c.y);
+                    sh.tab[j] = make_int4(c.x, c.y, int(unsigned(u64(C))), int(unsigned(u64(C) >> 32)));
+                }
             }
         }
         __syncthreads();
@@ -286,25 +286,32 @@ __global__ void __launch_bounds__(256, 2) stripe_kernel(const GemmParams p) {
 
     const __amdgpu_buffer_rsrc_t rY = make_rsrc(p.Y, p.y_bytes);
     const __amdgpu_buffer_rsrc_t rR = make_rsrc(p.R ? p.R : p.Y, p.y_bytes);
-    // per-wave row maximum so far: max |y| = max(ymax, -ymin)
-    int ymax[MS], ymin[MS];
+    const unsigned ldy4 = unsigned(p.ldy) * 4u;
+    // this lane's rows are rbase + 4 lh + 8g + v
+    const unsigned rowoff = unsigned(rbase + 4 * lh) * ldy4;
+    // running max of |y| for the lane's 16 rows (max(y, -y) is |y| as an unsigned value, also for INT_MIN)
+    v16i yabs;
 #pragma unroll
-    for (int ms = 0; ms < MS; ++ms) { ymax[ms] = 0; ymin[ms] = 0; }
-    double pr[MS];
-#pragma unroll
-    for (int ms = 0; ms < MS; ++ms) pr[ms] = ldexp(1.0, min(max(er[ms], -1000), 1000));
-    const bool lean = fl.fold && !p.R;   // the epilogue issues stores only
+    for (int i = 0; i < 16; ++i) yabs[i] = 0;
+    const bool lean = form == FORM_INT && !p.R;   // the epilogue issues stores only
+    const bool lut_lds = NEEDLUT && !sh.flag[5];  // the expanded table in LDS is valid (0 <= L <= 65536)
 
-    // GELU factor: z = x + 2^20 clamped to [-1, 2^21]; entry (z >> 10) + 1 = (x >> 10) + 1025 and
-    // z & 1023 = x & 1023; (1024 L[i] + d f) >> 10 = L[i] + ((d f) >> 10) (|d f| < 2^27)
+    // phi(x) for tables with 0 <= L <= 65536: x clamped to [-2^20 - 1, 2^20], entry (x >> 10) + 1025
     auto phi = [&](int x) -> int {
         const int xc = min(max(x, -1048577), 1048576);
         const int2 t = sh.lut[(xc >> 10) + 1025];
         return (t.x + __mul24(t.y, xc & 1023)) >> 10;
     };
-    auto comb = [&](int h, int l) -> double {
-        if constexpr (SMALLK) return double((h << 8) + l);
-        else return __builtin_fma(double(h), 256.0, double(l));
+    // (a b + 2^15) >> 16 as a 64-bit product: the high word and the 32-bit result
+    auto mulsh16 = [&](int a, int b, unsigned& hi) -> int {
+        const i64 t = i64(a) * i64(b) + 32768;
+        hi = unsigned(u64(t) >> 32);
+        return int(__builtin_amdgcn_alignbit(hi, unsigned(u64(t)), 16));
+    };
+    // the integer requantisation (A m + C) >> s of an element, exact when it fits in int32
+    auto req = [&](int A, const int4& k) -> int {
+        const i64 t = i64(A) * i64(k.x) + i64((u64(unsigned(k.w)) << 32) | unsigned(k.z));
+        return int(__builtin_amdgcn_alignbit(unsigned(u64(t) >> 32), unsigned(u64(t)), unsigned(k.y)));
     };
 
     for (int c = cb; c < ce; ++c) {
@@ -315,148 +322,156 @@ __global__ void __launch_bounds__(256, 2) stripe_kernel(const GemmParams p) {
         block_barrier();
         if (c + 1 < ce) issue(c + 1, stage ^ 1);
 
-        v4i acc_h[NS][MS], acc_l[NS][MS];
+        v16i acc_h[S::NSUB], acc_l[S::NSUB];
 #pragma unroll
-        for (int ns = 0; ns < NS; ++ns)
+        for (int u = 0; u < S::NSUB; ++u)
 #pragma unroll
-            for (int ms = 0; ms < MS; ++ms) {
-                acc_h[ns][ms] = v4i{0, 0, 0, 0};
-                acc_l[ns][ms] = v4i{0, 0, 0, 0};
-            }
+            for (int i = 0; i < 16; ++i) { acc_h[u][i] = 0; acc_l[u][i] = 0; }
         const unsigned char* sW = sh.w[stage];
+        // all ten K steps: past Kp both operands hold zeros (A registers cleared, W bytes out of range).
+        // The W fragments of step t + 2 are read from LDS before the MFMAs of step t, so that their
+        // latency hides behind four MFMAs of this wave.
+        auto wfrag = [&](int t, int u) -> v4i {
+            return *reinterpret_cast<const v4i*>(sW + (t >> 1) * S::KSTEP + swz(32 * u + lc, 2 * (t & 1) + lh));
+        };
+        constexpr int PF = 2;
+        v4i wq[PF][S::NSUB];
 #pragma unroll
-        for (int ks = 0; ks < NKM; ++ks) {
-            if (ks < nK) {
+        for (int t = 0; t < PF; ++t)
 #pragma unroll
-                for (int ns = 0; ns < NS; ++ns) {
-                    const v4i wf = *reinterpret_cast<const v4i*>(sW + ks * S::KSTEP + swz(ns * 16 + fr, fg));
+            for (int u = 0; u < S::NSUB; ++u) wq[t][u] = wfrag(t, u);
+        __builtin_amdgcn_sched_group_barrier(0x100, PF * S::NSUB, 0);
 #pragma unroll
-                    for (int ms = 0; ms < MS; ++ms) {
-                        acc_h[ns][ms] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf, hf[ms][ks], acc_h[ns][ms], 0, 0, 0);
-                        acc_l[ns][ms] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf, lf[ms][ks], acc_l[ns][ms], 0, 0, 0);
-                    }
-                }
+        for (int t = 0; t < NKS; ++t) {
+            v4i wf[S::NSUB];
+#pragma unroll
+            for (int u = 0; u < S::NSUB; ++u) {
+                wf[u] = wq[t % PF][u];
+                if (t + PF < NKS) wq[t % PF][u] = wfrag(t + PF, u);
             }
+#pragma unroll
+            for (int u = 0; u < S::NSUB; ++u) {
+                acc_h[u] = __builtin_amdgcn_mfma_i32_32x32x32_i8(hf[t], wf[u], acc_h[u], 0, 0, 0);
+                acc_l[u] = __builtin_amdgcn_mfma_i32_32x32x32_i8(lf[t], wf[u], acc_l[u], 0, 0, 0);
+            }
+            // keep that order in the schedule: the reads of step t + 2, then the MFMAs of step t
+            if (t + PF < NKS) __builtin_amdgcn_sched_group_barrier(0x100, S::NSUB, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 2 * S::NSUB, 0);
         }
 
-        // ---- epilogue of chunk c: output subtile i covers table rows i*16 + 4 fg + v (GEGLU: a
-        // columns; the g columns are CH/2 further), output columns ocol0 + i*16 + 4 fg + v
+        // ---- epilogue of chunk c: output subtile u is table rows tb + 32u + lc (GEGLU: a columns,
+        // g columns 32 further), output column ocol0 + 32u + lc
         const int tb = (c - cb) * CH;
         const int ocol0 = GEGLU ? c * (CH / 2) : c * CH;
 #pragma unroll
-        for (int i = 0; i < NOUT; ++i) {
-            const int lr = i * 16 + 4 * fg;
-            const int ncol = ocol0 + lr;
-            const bool cok = ncol < nlim;   // nlim % 4 == 0: the lane's four columns are all in or all out
-            const int ig = GEGLU ? i + NS / 2 : i;
-            ColConst ca[4], cg[4];
+        for (int u = 0; u < NOUT; ++u) {
+            const int ncol = ocol0 + 32 * u + lc;
+            const bool cok = ncol < nlim;
+            // byte offset of the lane's row rbase + 4 lh and column; + slot rows below. Rows at or past
+            // Mreal land at or past the end of the Y buffer and columns past the output at OOB, so the
+            // hardware drops those stores (and residual loads read zeros there)
+            const unsigned vbase = cok ? rowoff + unsigned(ncol) * 4u : OOB;
+            if (form == FORM_INT) {
+                const int4 ka = sh.tab[tb + 32 * u + lc];
+                const int4 kg = sh.tab[tb + (GEGLU ? 32 : 32 * u) + lc];
+                auto run = [&](auto hasr, auto rmax) {
+                    constexpr bool HASR = decltype(hasr)::value, RMAX = decltype(rmax)::value;
 #pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                ca[v] = sh.tab[tb + lr + v];
-                if constexpr (GEGLU) cg[v] = sh.tab[tb + CH / 2 + lr + v];
-            }
-#pragma unroll
-            for (int ms = 0; ms < MS; ++ms) {
-                int y[4];
-                if (fl.fold) {
-#pragma unroll
-                    for (int v = 0; v < 4; ++v) {
-                        const double ya = __builtin_floor(__builtin_fma(comb(acc_h[i][ms][v], acc_l[i][ms][v]), ca[v].ms, ca[v].wm));
+                    for (int i = 0; i < 16; ++i) {
+                        const unsigned voff = vbase + unsigned(8 * (i >> 2) + (i & 3)) * ldy4;
+                        const int ya = req((acc_h[u][i] << 8) + acc_l[u][i], ka);
+                        int y;
                         if constexpr (GEGLU) {
-                            const double yg = __builtin_floor(__builtin_fma(comb(acc_h[ig][ms][v], acc_l[ig][ms][v]), cg[v].ms, cg[v].wm));
-                            const double ge = __builtin_floor(__builtin_fma(yg, double(phi(int(yg))), 32768.0) * (1.0 / 65536.0));
-                            y[v] = cvt_sat(__builtin_floor(__builtin_fma(ya * (1.0 / 65536.0), ge, 0.5)));
+                            const int yg = req((acc_h[1][i] << 8) + acc_l[1][i], kg);
+                            unsigned h0, hi;
+                            const int ge = mulsh16(yg, phi(yg), h0);
+                            y = mulsh16(ya, ge, hi);
+                            // |a ge| >= 2^47: the result saturates. A wave-uniform branch, rarely taken;
+                            // the empty asm keeps the test on the high word and the branch a branch.
+                            asm volatile("" : "+v"(hi));
+                            const bool ovf = hi + 32768u > 65535u;
+                            if (__builtin_amdgcn_ballot_w64(ovf)) {
+                                asm volatile("; saturating GEGLU product");
+                                y = ovf ? (int(hi) >> 31) ^ 0x7fffffff : y;
+                            }
                         } else if constexpr (EPI == EPI_GELU) {
-                            y[v] = int(__builtin_floor(__builtin_fma(ya, double(phi(int(ya))), 32768.0) * (1.0 / 65536.0)));
+                            unsigned h0;
+                            y = mulsh16(ya, phi(ya), h0);
                         } else {
-                            y[v] = int(ya);
+                            y = ya;
                         }
+                        if constexpr (HASR) y = add_sat(y, int(__builtin_amdgcn_raw_buffer_load_b32(rR, int(voff), 0, 0)));
+                        __builtin_amdgcn_raw_buffer_store_b32(y, rY, int(voff), 0, 0);
+                        // max(y, -y) is |y| as an unsigned value, also for INT_MIN. Columns past the
+                        // output have m = s = C = 0 in the table and zero W rows, so their y is 0.
+                        if constexpr (RMAX) yabs[i] = int(max(unsigned(yabs[i]), unsigned(max(y, int(0u - unsigned(y))))));
                     }
-                } else if (fl.fast) {
-                    // general FP64 form: floor(A m 2^-(s-e) + 1/2) saturated, + b saturated
-#pragma unroll
-                    for (int v = 0; v < 4; ++v) {
-                        auto one = [&](int h, int l, const ColConst& k, int col) -> int {
-                            const int n = cok ? col : 0;
-                            const int b = p.cst[n].z;
-                            double X;
-                            if (fl.ezero) X = __builtin_fma(comb(h, l), k.ms, k.wm);
-                            else X = __builtin_fma(__builtin_fma(comb(h, l), k.ms, k.wm), pr[ms], 0.5);
-                            return add_sat(cvt_sat(__builtin_floor(X)), b);
-                        };
-                        const int na = GEGLU ? 2 * (ncol + v) : ncol + v;
-                        const int ya = one(acc_h[i][ms][v], acc_l[i][ms][v], ca[v], na);
-                        if constexpr (GEGLU) {
-                            const int yg = one(acc_h[ig][ms][v], acc_l[ig][ms][v], cg[v], na + 1);
-                            const double ge = __builtin_floor(__builtin_fma(double(yg), double(phi(yg)), 32768.0) * (1.0 / 65536.0));
-                            y[v] = cvt_sat(__builtin_floor(__builtin_fma(double(ya), ge, 32768.0) * (1.0 / 65536.0)));
-                        } else if constexpr (EPI == EPI_GELU) {
-                            y[v] = int(__builtin_floor(__builtin_fma(double(ya), double(phi(ya)), 32768.0) * (1.0 / 65536.0)));
-                        } else {
-                            y[v] = ya;
-                        }
-                    }
+                };
+                if (EPI == EPI_PLAIN && p.R) {
+                    if (p.rowmax) run(std::true_type{}, std::true_type{});
+                    else run(std::true_type{}, std::false_type{});
                 } else {
-                    // the reference's int64 formula
-#pragma unroll
-                    for (int v = 0; v < 4; ++v) {
-                        const int col = cok ? ncol + v : 0;
-                        if constexpr (GEGLU) {
-                            const int4 ka = p.cst[2 * col], kg = p.cst[2 * col + 1];
-                            const int ya = epi1_exact(acc_h[i][ms][v], acc_l[i][ms][v], ka.x, ka.y, ka.z, ka.w, er[ms]);
-                            const int yg = epi1_exact(acc_h[ig][ms][v], acc_l[ig][ms][v], kg.x, kg.y, kg.z, kg.w, er[ms]);
-                            y[v] = geglu_exact(ya, yg, p.Lphi);
-                        } else {
-                            const int4 k = p.cst[col];
-                            int yy = epi1_exact(acc_h[i][ms][v], acc_l[i][ms][v], k.x, k.y, k.z, k.w, er[ms]);
-                            if constexpr (EPI == EPI_GELU) yy = gelu_exact(yy, p.Lphi);
-                            y[v] = yy;
-                        }
-                    }
+                    if (p.rowmax) run(std::false_type{}, std::true_type{});
+                    else run(std::false_type{}, std::false_type{});
                 }
-                const unsigned off = cok ? yoff[ms] + unsigned(ncol) * 4u : OOB;
-                if constexpr (EPI == EPI_PLAIN) {
-                    if (p.R) {
-                        const v4i rv = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rR, int(off), 0, 0));
-#pragma unroll
-                        for (int v = 0; v < 4; ++v) y[v] = add_sat(y[v], rv[v]);
+            } else {
+                // the reference's int64 formula, one element per iteration (its row maximum goes
+                // straight to memory)
+                const int col = cok ? ncol : 0;
+                const int4 ca = p.cst[GEGLU ? 2 * col : col];
+                const int4 cg = GEGLU ? p.cst[2 * col + 1] : ca;
+#pragma unroll 1
+                for (int i = 0; i < 16; ++i) {
+                    const int slot = 8 * (i >> 2) + (i & 3);
+                    const unsigned voff = vbase + unsigned(slot) * ldy4;
+                    const int er = sh.erow[wave * 32 + 4 * lh + slot];
+                    const int ya = epi1_exact(acc_h[u][i], acc_l[u][i], ca.x, ca.y, ca.z, ca.w, er);
+                    int y;
+                    if constexpr (GEGLU) {
+                        const int yg = epi1_exact(acc_h[1][i], acc_l[1][i], cg.x, cg.y, cg.z, cg.w, er);
+                        const i64 pg = lut_lds ? phi(yg) : lut16i(yg, p.Lphi);
+                        const i64 ge = sat32(rshr(i64(yg) * pg, 16));
+                        y = int(sat32(rshr(i64(ya) * ge, 16)));
+                    } else if constexpr (EPI == EPI_GELU) {
+                        const i64 pa = lut_lds ? phi(ya) : lut16i(ya, p.Lphi);
+                        y = int(sat32(rshr(i64(ya) * pa, 16)));
+                    } else {
+                        y = ya;
                     }
-                }
-                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned, v4i{y[0], y[1], y[2], y[3]}),
-                                                       rY, int(off), 0, 0);
-                if (p.rowmax && cok) {
-                    ymax[ms] = max(max(ymax[ms], y[0]), max(y[1], max(y[2], y[3])));
-                    ymin[ms] = min(min(ymin[ms], y[0]), min(y[1], min(y[2], y[3])));
+                    if (EPI == EPI_PLAIN && p.R) y = add_sat(y, int(__builtin_amdgcn_raw_buffer_load_b32(rR, int(voff), 0, 0)));
+                    __builtin_amdgcn_raw_buffer_store_b32(y, rY, int(voff), 0, 0);
+                    const int r = rbase + 4 * lh + slot;
+                    if (p.rowmax && cok && r < p.Mreal && y) atomicMax(p.rowmax + r, uabs(y));
                 }
             }
         }
     }
 
     if (p.rowmax) {
-        // lanes fr, fr + 16, fr + 32, fr + 48 hold the same row: one atomic per row and wave
+        // lanes with the same lh hold the same 16 rows: reduce over the 32 columns, one atomic per row
 #pragma unroll
-        for (int ms = 0; ms < MS; ++ms) {
-            uint32_t m = max(uint32_t(ymax[ms]), uabs(ymin[ms]));
-            m = max(m, uint32_t(__shfl_xor(int(m), 16)));
-            m = max(m, uint32_t(__shfl_xor(int(m), 32)));
-            const int r = rbase + ms * 16 + fr;
-            if (fg == 0 && r < p.Mreal && m) atomicMax(p.rowmax + r, m);
+        for (int i = 0; i < 16; ++i) {
+            uint32_t m = uint32_t(yabs[i]);
+#pragma unroll
+            for (int o = 1; o < 32; o <<= 1) m = max(m, uint32_t(__shfl_xor(int(m), o)));
+            const int r = rbase + 4 * lh + 8 * (i >> 2) + (i & 3);
+            if (lc == 0 && r < p.Mreal && m) atomicMax(p.rowmax + r, m);
         }
     }
 }
 
-template <int SRC, class S>
+template <int SRC>
 hipError_t launch_stripe_t(int epi, const GemmParams& p, hipStream_t st) {
     const dim3 grid(unsigned(p.mtiles * p.ntiles));
     switch (epi) {
-    case EPI_PLAIN: hipLaunchKernelGGL((stripe_kernel<SRC, EPI_PLAIN, S>), grid, dim3(256), 0, st, p); break;
-    case EPI_GEGLU: hipLaunchKernelGGL((stripe_kernel<SRC, EPI_GEGLU, S>), grid, dim3(256), 0, st, p); break;
-    case EPI_GELU: hipLaunchKernelGGL((stripe_kernel<SRC, EPI_GELU, S>), grid, dim3(256), 0, st, p); break;
+    case EPI_PLAIN: hipLaunchKernelGGL((stripe_kernel<SRC, EPI_PLAIN>), grid, dim3(256), 0, st, p); break;
+    case EPI_GEGLU: hipLaunchKernelGGL((stripe_kernel<SRC, EPI_GEGLU>), grid, dim3(256), 0, st, p); break;
+    case EPI_GELU: hipLaunchKernelGGL((stripe_kernel<SRC, EPI_GELU>), grid, dim3(256), 0, st, p); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
 }
 
-hipError_t launch_stripe(int src, int shape, int epi, const GemmParams& p, hipStream_t st);
+hipError_t launch_stripe(int src, int epi, const GemmParams& p, hipStream_t st);
 
 }  // namespace vk
