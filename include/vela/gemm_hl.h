@@ -39,8 +39,8 @@ struct ASrc {
     const int16_t* img16 = nullptr;               // SRC_CONV16
 };
 
-// src/gemm_hl.h:18-26: the epilogue. gnstat and the EPI_QKV outputs are not implemented by this
-// library (the call throws when they are used); ws/ws_bytes add an optional split-K workspace.
+// src/gemm_hl.h:18-26: the epilogue (gnstat points at GnStat records of include/vela/kernels.h);
+// ws/ws_bytes add an optional split-K workspace.
 struct AEpi {
     int epi = EPI_PLAIN; int32_t* Y = nullptr; int ldy = 0; const int32_t* residual = nullptr;
     int Cs = 0; int32_t* Y1 = nullptr; int32_t* Y2 = nullptr; const int32_t* Lphi = nullptr;

@@ -1,6 +1,7 @@
 // The producers and epilogues of the reference's src/kernels.h (emanwrxsti/vela) that feed and
 // finish the GEMM path, as drop-in meow:: functions over libvgemm.so (include/vgemm.h). Only the
-// GEMM-path kernels are here; norms, attention and the rest of src/kernels.h are not part of this
+// GEMM-path kernels are here (with k_gn_init, which prepares the statistics records the epilogues
+// fill); the norms themselves, attention and the rest of src/kernels.h are not part of this
 // library. Errors throw std::runtime_error.
 #pragma once
 #include <hip/hip_runtime.h>
@@ -19,20 +20,29 @@ inline void kcheck(int rc) {
 }
 }  // namespace detail
 
-struct GnStat;   // src/kernels.h:9 (GroupNorm statistics are not implemented here)
+// src/kernels.h:9: the GroupNorm statistics record (same fields and layout as VgemmGnStat)
+struct GnStat {
+    int64_t sum;
+    int mn, mx;
+    int64_t mean;
+    int e;
+    int64_t ss, sd;
+};
+static_assert(sizeof(GnStat) == sizeof(VgemmGnStat), "GnStat layout");
 
 // src/kernels.h:11-12
 inline void k_quant_rows(hipStream_t st, const int32_t* X, int M, int K, int ldx, int8_t* hi, int8_t* lo, int32_t* e, int Kp) {
     detail::kcheck(vgemm_quant_rows(st, X, M, K, ldx, hi, lo, e, Kp));
 }
 
-// src/kernels.h:13-16 (gs must be null: GroupNorm statistics are not implemented)
+// src/kernels.h:13-16 (gs: per-(sample, group) sum/min/max of Y, 32 groups, N % 32 == 0, (T*N) % 1024 == 0)
 inline void k_epilogue(hipStream_t st, const int32_t* Chi, const int32_t* Clo, int M, int N, int ldc, const int4* cst, const int32_t* e,
                        int32_t* Y, int ldy, const int32_t* residual = nullptr, GnStat* gs = nullptr, int T = 0) {
-    (void)T;
-    if (gs) throw std::runtime_error("k_epilogue: GroupNorm statistics are not implemented");
-    detail::kcheck(vgemm_epilogue(st, Chi, Clo, M, N, ldc, reinterpret_cast<const int32_t*>(cst), e, Y, ldy, residual));
+    detail::kcheck(vgemm_epilogue(st, Chi, Clo, M, N, ldc, reinterpret_cast<const int32_t*>(cst), e, Y, ldy, residual, gs, T));
 }
+
+// src/kernels.h:25 (src/kernels.cu:173)
+inline void k_gn_init(hipStream_t st, GnStat* gs, int cnt) { detail::kcheck(vgemm_gn_init(st, gs, cnt)); }
 
 // src/kernels.h:17-18
 inline void k_pixmax(hipStream_t st, const int32_t* X, int rows, int C, uint32_t* pm) { detail::kcheck(vgemm_pixmax(st, X, rows, C, pm)); }

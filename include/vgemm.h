@@ -49,15 +49,32 @@ typedef struct VgemmASrc {
     const int16_t* img16;                                                  /* SRC_CONV16 (C % 8 == 0, C <= 16384) */
 } VgemmASrc;
 
+/* GroupNorm statistics record: meow::GnStat (src/kernels.h:9), same fields and layout (48 bytes). The
+ * GEMM epilogue accumulates sum, mn and mx; mean, e, ss and sd belong to the normalisation after it. */
+typedef struct VgemmGnStat {
+    int64_t sum;
+    int32_t mn, mx;
+    int64_t mean;
+    int32_t e;
+    int64_t ss, sd;
+} VgemmGnStat;
+
 /* Epilogue description: meow::AEpi (src/gemm_hl.h:18-26) in the same order, plus an optional
- * split-K workspace (ws, ws_bytes; none = no split-K). The QKV and GroupNorm-statistics fields are
- * accepted and rejected with VGEMM_ERR_UNSUPPORTED when used. */
+ * split-K workspace (ws, ws_bytes; none = no split-K).
+ *   gnstat/gnT (EPI_PLAIN): add the sum, min and max of every output y (after the residual) to
+ *     gnstat[(row / gnT) * 32 + col / (Nreal / 32)]; Nreal % 32 == 0, gnT % 64 == 0; the caller
+ *     initialises the records (vgemm_gn_init). src/gemm_hl.cu:175-177, 285-287, 306-309.
+ *   EPI_QKV: Nreal = 3C, C = 64*heads, rows = B*T. Columns [0, C) (q) and [C, 2C) (k) are quantised per
+ *     row and head (e = row_exp(max |y| over the head's 64 columns)) into hi/lo int8
+ *     [(b*heads + head)*Tp + t][64] with e and the int64 sums of hi, lo and q per row and head
+ *     (Tp = TpQ for q, TpK for k; rows t >= T are not written); columns [2C, 3C) (v) go to Y2 [rows x C]
+ *     as int32. Y is not used. src/gemm_hl.cu:179-241. */
 typedef struct VgemmAEpi {
     int epi; int32_t* Y; int ldy; const int32_t* residual;
     int Cs; int32_t* Y1; int32_t* Y2; const int32_t* Lphi;
     uint32_t* rowmax;                   /* optional: atomicMax of |y| per output row (caller zeroes it) */
-    void* gnstat; int gnT;              /* GroupNorm statistics: not supported */
-    int heads, T, TpQ, TpK, C;          /* EPI_QKV: not supported */
+    void* gnstat; int gnT;              /* optional GroupNorm statistics (VgemmGnStat records) */
+    int heads, T, TpQ, TpK, C;          /* EPI_QKV geometry */
     int8_t *qhi, *qlo, *khi, *klo; int32_t *qe, *ke;
     int64_t *qhs, *qls, *qts, *khs, *kls, *kts;
     void* ws; size_t ws_bytes;          /* optional split-K workspace (device memory) */
@@ -114,9 +131,11 @@ int vgemm_i8_run(void* handle, void* stream, const int8_t* A, int lda, long long
 /* A-operand producers and cuBLASLt-path epilogues (src/kernels.h:11-21, 68-70). */
 /* meow::k_quant_rows (src/kernels.h:12-13): per-row quantisation of X[M,K] into hi/lo [Mp32 x Kp] + e. */
 int vgemm_quant_rows(void* stream, const int32_t* X, int M, int K, int ldx, int8_t* hi, int8_t* lo, int32_t* e, int Kp);
-/* meow::k_epilogue without GroupNorm statistics (src/kernels.h:14-17). */
+/* meow::k_epilogue (src/kernels.h:14-17). gs (VgemmGnStat records, or null): add the sum, min and max
+ * of every output (after the residual) to gs[(row / T) * 32 + col / (N / 32)]; needs N % 32 == 0 and
+ * (T*N) % 1024 == 0. */
 int vgemm_epilogue(void* stream, const int32_t* Chi, const int32_t* Clo, int M, int N, int ldc, const int32_t* cst,
-                   const int32_t* e, int32_t* Y, int ldy, const int32_t* residual);
+                   const int32_t* e, int32_t* Y, int ldy, const int32_t* residual, void* gs, int T);
 /* meow::k_pixmax (src/kernels.h:18-19). */
 int vgemm_pixmax(void* stream, const int32_t* X, int rows, int C, uint32_t* pm);
 /* meow::k_im2col3 (src/kernels.h:20-21). */
@@ -139,6 +158,10 @@ int vgemm_graph_destroy(void* exec);
 /* Fill `count` uint32 words with `value` by a kernel (capture-safe replacement for the
  * cudaMemsetAsync that zeroes rowmax buffers, src/engine.cu:161). */
 int vgemm_fill_u32(void* stream, uint32_t* p, size_t count, uint32_t value);
+
+/* meow::k_gn_init (src/kernels.h:25, src/kernels.cu:173): sum = ss = 0, mn = INT_MAX, mx = INT_MIN for
+ * `count` VgemmGnStat records, by a kernel (capture-safe). */
+int vgemm_gn_init(void* stream, void* gs, int count);
 
 /* Last error message of this thread ("" if none). */
 const char* vgemm_last_error(void);

@@ -70,6 +70,8 @@ _SIGS = {
     "orc_i8gemm": (None, [P, I, LL, P, I, LL, P, I, LL, I, I, I, I]),
     "orc_prep_weight": (None, [P, I, I, I, P, P, P, I, I, P, P]),
     "orc_interleave2": (None, [P, P, P, P, I, I, P, P]),
+    "orc_gn_accumulate": (None, [P, I, I, I, I, P, P, P]),
+    "orc_qkv_heads": (None, [P, I, I, I, I, I, I, I] + [P] * 13),
 }
 
 _lib = None
@@ -280,6 +282,38 @@ def epilogue_geglu_q(Chi, Clo, M, F, ldc, cst, e, L, Kp):
     hi = np.zeros((M, Kp), np.int8); lo = np.zeros((M, Kp), np.int8); eo = np.zeros(M, np.int32)
     lib().orc_epilogue_geglu_q(a(Chi), a(Clo), M, F, ldc, a(cst), a(e), a(L), a(hi), a(lo), a(eo), Kp)
     return hi, lo, eo
+
+
+def gn_stats(Y, M, N, T, ldy=None):
+    """GroupNorm sum/min/max records of Y [M x N] over samples of T rows and 32 column groups
+    (fresh records, as after k_gn_init): dict of int64 arrays [ceil(M / T) * 32]."""
+    Y = np.ascontiguousarray(Y, np.int32)
+    ldy = ldy or Y.shape[1]
+    cnt = (M + T - 1) // T * 32
+    s = np.zeros(cnt, np.int64)
+    mn = np.full(cnt, 2**31 - 1, np.int32)
+    mx = np.full(cnt, -(2**31), np.int32)
+    lib().orc_gn_accumulate(a(Y), M, N, ldy, T, a(s), a(mn), a(mx))
+    return {"sum": s, "mn": mn.astype(np.int64), "mx": mx.astype(np.int64)}
+
+
+def qkv_heads(Y, M, C, heads, T, TpQ, TpK, fill=0x5A):
+    """EPI_QKV outputs from the plain output Y [M x 3C]. Buffers start filled with `fill` bytes (rows
+    t >= T are left so). Returns dict: q/k -> (hi, lo [B*heads*Tp x 64], e, hs, ls, ts), v -> [M x C]."""
+    Y = np.ascontiguousarray(Y, np.int32)
+    B = (M + T - 1) // T
+    out = {}
+    for part, Tp in (("q", TpQ), ("k", TpK)):
+        G = B * heads * Tp
+        f8 = np.int8(np.uint8(fill).view(np.int8))
+        out[part] = (np.full((G, 64), f8, np.int8), np.full((G, 64), f8, np.int8),
+                     np.full(G, np.uint32(fill * 0x01010101).view(np.int32), np.int32),
+                     *(np.full(G, np.uint64(fill * 0x0101010101010101).view(np.int64), np.int64) for _ in range(3)))
+    V = np.zeros((M, C), np.int32)
+    q, k = out["q"], out["k"]
+    lib().orc_qkv_heads(a(Y), M, Y.shape[1], C, heads, T, TpQ, TpK, *(a(x) for x in q), *(a(x) for x in k), a(V))
+    out["v"] = V
+    return out
 
 
 def prep_weight(w, N, K, conv3, m, s, b, Np, Kp):

@@ -256,6 +256,69 @@ void orc_epilogue_geglu_q(const int32_t* Chi, const int32_t* Clo, int M, int F, 
     }
 }
 
+/* GroupNorm statistics of an epilogue's output (EPI_PLAIN): src/gemm_hl.cu:285-287, 306-309 and
+ * src/kernels.cu:63-95. Every y[r][n] of the (post-residual) output is added to record
+ * (r / T) * 32 + n / (N / 32): sum += y, mn = min(mn, y), mx = max(mx, y). The records are
+ * accumulated into, as the reference's atomics do after k_gn_init. */
+void orc_gn_accumulate(const int32_t* Y, int M, int N, int ldy, int T, int64_t* sum, int32_t* mn, int32_t* mx) {
+    const int cg = N / 32;
+    for (int r = 0; r < M; ++r) {
+        const int b = r / T;
+        for (int n = 0; n < N; ++n) {
+            const int32_t y = Y[(size_t)r * ldy + n];
+            const int k = b * 32 + n / cg;
+            sum[k] += y;
+            if (y < mn[k]) mn[k] = y;
+            if (y > mx[k]) mx[k] = y;
+        }
+    }
+}
+
+/* The EPI_QKV outputs from the plain output Y [M x 3C] (src/gemm_hl.cu:179-241): columns
+ * [0, C) are q, [C, 2C) k, [2C, 3C) v, C = 64 * heads, row r = b * T + t. v is copied to V [M x C].
+ * q and k are quantised per (row, head): e = row_exp(max |y| over the head's 64 values),
+ * q16 = quant16_32(y, e), hi = q16 >> 8, lo = (q16 & 255) - 128, stored at row
+ * (b * heads + head) * Tp + t of the [*, 64] planes, with e and the sums of hi, lo and q16 over the 64
+ * values (the k_quant_heads layout, src/kernels.cu:611-631). Rows t >= T of the planes are not
+ * written. */
+void orc_qkv_heads(const int32_t* Y, int M, int ldy, int C, int heads, int T, int TpQ, int TpK,
+                   int8_t* qhi, int8_t* qlo, int32_t* qe, int64_t* qhs, int64_t* qls, int64_t* qts,
+                   int8_t* khi, int8_t* klo, int32_t* ke, int64_t* khs, int64_t* kls, int64_t* kts, int32_t* V) {
+    for (int r = 0; r < M; ++r) {
+        const int32_t* y = Y + (size_t)r * ldy;
+        for (int c = 0; c < C; ++c) V[(size_t)r * C + c] = y[2 * C + c];
+        const int b = r / T, t = r % T;
+        for (int part = 0; part < 2; ++part) {
+            const int Tp = part ? TpK : TpQ;
+            int8_t* hp = part ? khi : qhi;
+            int8_t* lp = part ? klo : qlo;
+            for (int h = 0; h < heads; ++h) {
+                const int32_t* v = y + part * C + 64 * h;
+                int64_t m = 0;
+                for (int d = 0; d < 64; ++d) {
+                    const int64_t av = v[d] < 0 ? -(int64_t)v[d] : v[d];
+                    if (av > m) m = av;
+                }
+                const int ee = orc_row_exp(m);
+                const size_t gt = (size_t)(b * heads + h) * Tp + t;
+                int64_t hs = 0, ls = 0, ts = 0;
+                for (int d = 0; d < 64; ++d) {
+                    const int32_t q = orc_quant16_32(v[d], ee);
+                    int8_t hb, lb;
+                    orc_split16(q, &hb, &lb);
+                    hp[gt * 64 + d] = hb;
+                    lp[gt * 64 + d] = lb;
+                    hs += hb; ls += lb; ts += q;
+                }
+                (part ? ke : qe)[gt] = ee;
+                (part ? khs : qhs)[gt] = hs;
+                (part ? kls : qls)[gt] = ls;
+                (part ? kts : qts)[gt] = ts;
+            }
+        }
+    }
+}
+
 /* ------------------------------------------------------------------ the GEMMs */
 
 /* One row of A as hi/lo planes. SRC_I8: src/gemm_hl.cu:87-97. SRC_X32: src/gemm_hl.cu:99-121

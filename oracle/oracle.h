@@ -80,6 +80,13 @@ void orc_epilogue_split(const int32_t* Chi, const int32_t* Clo, int M, int N, in
 void orc_epilogue_geglu_q(const int32_t* Chi, const int32_t* Clo, int M, int F, int ldc, const int32_t* cst,
                           const int32_t* e, const int32_t* L, int8_t* hi, int8_t* lo, int32_t* eo, int Kp);
 
+/* GroupNorm statistics (EPI_PLAIN, k_epilogue with gs): accumulate into sum/mn/mx [(M / T) * 32] */
+void orc_gn_accumulate(const int32_t* Y, int M, int N, int ldy, int T, int64_t* sum, int32_t* mn, int32_t* mx);
+/* EPI_QKV outputs from the plain output Y [M x 3C]: head-quantised q/k planes and V [M x C] */
+void orc_qkv_heads(const int32_t* Y, int M, int ldy, int C, int heads, int T, int TpQ, int TpK,
+                   int8_t* qhi, int8_t* qlo, int32_t* qe, int64_t* qhs, int64_t* qls, int64_t* qts,
+                   int8_t* khi, int8_t* klo, int32_t* ke, int64_t* khs, int64_t* kls, int64_t* kts, int32_t* V);
+
 /* ---- the GEMMs */
 /* one row of the A operand as hi/lo planes (Kp bytes each) and its shift e; returns 0 or -1 */
 int orc_a_row(const OrcGemm* g, int r, int8_t* hi, int8_t* lo, int32_t* e);

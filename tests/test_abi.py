@@ -1,5 +1,5 @@
 """The C ABI of libvgemm.so without a GPU: the library loads, exports every entry point that
-include/vgemm.h declares, the ctypes mirror of VgemmASrc / VgemmAEpi has the C layout (checked
+include/vgemm.h declares, the ctypes mirror of VgemmASrc / VgemmAEpi / VgemmGnStat has the C layout (checked
 against a gcc-compiled probe of the header), and argument checks fail the way the reference throws
 (src/gemm_hl.cu:351,357; src/gemm.cu:41) before any device work."""
 import ctypes
@@ -42,7 +42,8 @@ PROBE = r"""
 #include "vgemm.h"
 #define F(T, f) printf(#T " " #f " %zu\n", offsetof(T, f));
 int main(void) {
-    printf("VgemmASrc sizeof %zu\nVgemmAEpi sizeof %zu\n", sizeof(VgemmASrc), sizeof(VgemmAEpi));
+    printf("VgemmASrc sizeof %zu\nVgemmAEpi sizeof %zu\nVgemmGnStat sizeof %zu\n", sizeof(VgemmASrc), sizeof(VgemmAEpi),
+           sizeof(VgemmGnStat));
     %FIELDS%
     return 0;
 }
@@ -51,7 +52,7 @@ int main(void) {
 
 def test_struct_layout_matches_c(tmp_path):
     lines = []
-    for T, cls in (("VgemmASrc", _lib.ASrc), ("VgemmAEpi", _lib.AEpi)):
+    for T, cls in (("VgemmASrc", _lib.ASrc), ("VgemmAEpi", _lib.AEpi), ("VgemmGnStat", _lib.GnStat)):
         for f, _ in cls._fields_:
             lines.append(f"F({T}, {f})")
     src = tmp_path / "probe.c"
@@ -62,7 +63,7 @@ def test_struct_layout_matches_c(tmp_path):
     for line in subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.splitlines():
         T, f, v = line.split()
         got[(T, f)] = int(v)
-    for T, cls in (("VgemmASrc", _lib.ASrc), ("VgemmAEpi", _lib.AEpi)):
+    for T, cls in (("VgemmASrc", _lib.ASrc), ("VgemmAEpi", _lib.AEpi), ("VgemmGnStat", _lib.GnStat)):
         assert got[(T, "sizeof")] == ctypes.sizeof(cls), T
         for f, _ in cls._fields_:
             assert got[(T, f)] == getattr(cls, f).offset, f"{T}.{f}"
@@ -116,8 +117,11 @@ def test_hl2_shape_errors(kw, code, msg):
     (dict(src=3, q16=FAKE, K=60, ld16=64), {}, -1, "SRC_I16"),
     (dict(src=1, x=FAKE, K=64, ldx=64), {}, -1, "SRC_X32"),
     (dict(src=9), {}, -1, "unknown A source"),
-    (dict(src=0, hi=FAKE, lo=FAKE, ld8=64), dict(epi=4), -3, "EPI_QKV"),
-    (dict(src=0, hi=FAKE, lo=FAKE, ld8=64), dict(gnstat=FAKE), -3, "GroupNorm"),
+    (dict(src=0, hi=FAKE, lo=FAKE, ld8=64), dict(epi=4), -1, "EPI_QKV needs C = 64*heads"),
+    (dict(src=0, hi=FAKE, lo=FAKE, ld8=64), dict(epi=4, heads=1, C=64, T=8, TpQ=8, TpK=8), -1, "Nreal = 3C"),
+    (dict(src=0, hi=FAKE, lo=FAKE, ld8=64), dict(gnstat=FAKE), -1, "GroupNorm statistics need"),
+    (dict(src=0, hi=FAKE, lo=FAKE, ld8=64), dict(gnstat=FAKE, gnT=96), -1, "gnT % 64"),
+    (dict(src=0, hi=FAKE, lo=FAKE, ld8=64), dict(gnstat=FAKE, gnT=64, epi=3, Lphi=FAKE), -1, "need EPI_PLAIN"),
     (dict(src=0, hi=FAKE, lo=FAKE, ld8=64), dict(epi=2), -1, "Lphi"),
     (dict(src=0, hi=FAKE, lo=FAKE, ld8=64), dict(epi=2, Lphi=FAKE, residual=FAKE), -1, "no residual"),
     (dict(src=0, hi=FAKE, lo=FAKE, ld8=64), dict(epi=1, Cs=30), -1, "SPLIT3"),
@@ -129,6 +133,39 @@ def test_hl2_argument_errors(asrc, aepi, code, msg):
     Kp = 80 if asrc.get("K") == 72 else 64
     rc, err = call_hl2(A, E, Kp=Kp, ldw=Kp)
     assert rc == code and msg in err, err
+
+
+QKV = dict(epi=4, heads=1, C=64, T=40, TpQ=128, TpK=64, Y2=FAKE, qhi=FAKE, qlo=FAKE, khi=FAKE, klo=FAKE, qe=FAKE, ke=FAKE,
+           qhs=FAKE, qls=FAKE, qts=FAKE, khs=FAKE, kls=FAKE, kts=FAKE)
+
+
+@pytest.mark.parametrize("aepi,msg", [
+    (dict(QKV, TpK=32), "TpK >= T"),
+    (dict(QKV, T=0), "T > 0"),
+    (dict(QKV, kts=None), "every q/k output"),
+    (dict(QKV, Y2=FAKE + 4), "16-byte aligned Y2"),
+    (dict(QKV, qlo=FAKE + 2), "4-byte aligned"),
+    (dict(QKV, residual=FAKE), "no residual"),
+    (dict(QKV, rowmax=FAKE), "no residual, rowmax"),
+])
+def test_hl2_qkv_errors(aepi, msg):
+    """EPI_QKV (src/gemm_hl.cu:179-241) needs N = 3C with C = 64 heads and every q/k output."""
+    A = _lib.ASrc(src=0, hi=FAKE, lo=FAKE, ld8=64)
+    E = _lib.AEpi(**{"Y": None, "ldy": 0, **aepi})
+    rc, err = call_hl2(A, E, Np=192, Nreal=192)
+    assert rc == -1 and msg in err, err
+
+
+def test_epilogue_and_gn_init_errors():
+    """k_epilogue with statistics needs 32 whole groups and whole 1024-element blocks per sample."""
+    lib = _lib.load()
+    base = [None, FAKE, FAKE, 64, 128, 128, FAKE, FAKE, FAKE, 128, None]
+    assert lib.vgemm_epilogue(*base, FAKE, 0) == -1
+    assert "GroupNorm" in lib.vgemm_last_error().decode()
+    assert lib.vgemm_epilogue(*base[:4], 96, 96, *base[6:9], 96, None, FAKE, 48) == -1   # 96 * 48 % 1024 != 0
+    assert lib.vgemm_epilogue(*base[:4], 100, 100, *base[6:9], 100, None, FAKE, 64) == -1  # N % 4
+    assert lib.vgemm_gn_init(None, None, 4) == -1
+    assert lib.vgemm_gn_init(None, FAKE, 0) == -1
 
 
 def test_empty_problem_is_a_no_op():
@@ -166,7 +203,8 @@ def test_workspace_heuristic():
 
 @pytest.mark.parametrize("geom,epi,rows", [
     ((16, 16, 1280, 1), 0, 128),   # eight output rows per tile
-    ((16, 16, 1280, 1), 4, 128),   # SPLIT3
+    ((16, 16, 1280, 1), 1, 128),   # SPLIT3
+    ((16, 16, 1280, 1), 4, 0),     # QKV runs on the 128 x 128 tile kernels
     ((16, 8, 64, 1), 0, 128),      # sixteen rows of 8 pixels
     ((32, 4, 64, 1), 0, 128),      # 32 rows of 4 pixels: a 34 x 6 patch
     ((64, 2, 64, 1), 0, 0),        # 64 rows of 2 pixels: a 66 x 4 patch does not fit

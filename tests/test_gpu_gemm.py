@@ -97,9 +97,9 @@ class Case:
                     Lphi=self.lut, Y=Y, residual=Y if self.res is not None else None, rowmax=rm, **kw)
         return Y, rm
 
-    def run_gpu(self, ws_bytes=0):
+    def asrc(self, keep):
+        """The device A operand of this case; device buffers are kept alive in `keep`."""
         A = vg.ASrc(src=self.src)
-        keep = {}
         keep["e"] = dev(self.e)
         A.e = vg.ptr(keep["e"])
         if self.src == vg.SRC_I8:
@@ -120,6 +120,11 @@ class Case:
                 A.img16 = vg.ptr(keep["img"])
             A.H, A.W, A.C, A.stride = H, W, C, stride
             A.Ho, A.Wo, A.K = (H - 1) // stride + 1, (W - 1) // stride + 1, 9 * C
+        return A
+
+    def run_gpu(self, ws_bytes=0):
+        keep = {}
+        A = self.asrc(keep)
         w, cst = dev(self.w), dev(self.cst)
         lut = dev(self.lut)
         E = vg.AEpi(epi=self.epi, Lphi=vg.ptr(lut))

@@ -40,6 +40,17 @@ class ASrc(ctypes.Structure):
             setattr(self, k, v)
 
 
+class GnStat(ctypes.Structure):
+    """VgemmGnStat (include/vgemm.h) == meow::GnStat (src/kernels.h:9), 48 bytes."""
+
+    _fields_ = [("sum", LL), ("mn", I), ("mx", I), ("mean", LL), ("e", I), ("ss", LL), ("sd", LL)]
+
+
+GNSTAT_BYTES = ctypes.sizeof(GnStat)
+# field offsets, for reading records out of a device buffer viewed as bytes
+GNSTAT_OFFSETS = {name: getattr(GnStat, name).offset for name, _ in GnStat._fields_}
+
+
 class AEpi(ctypes.Structure):
     """VgemmAEpi (include/vgemm.h) == meow::AEpi (src/gemm_hl.h:18-26) plus the split-K workspace."""
 
@@ -77,7 +88,7 @@ SIGNATURES = [
     ("vgemm_i8_destroy", I, [P]),
     ("vgemm_i8_run", I, [P, P, P, I, LL, P, I, LL, P, I, LL, I, I, I, I]),
     ("vgemm_quant_rows", I, [P, P, I, I, I, P, P, P, I]),
-    ("vgemm_epilogue", I, [P, P, P, I, I, I, P, P, P, I, P]),
+    ("vgemm_epilogue", I, [P, P, P, I, I, I, P, P, P, I, P, P, I]),
     ("vgemm_pixmax", I, [P, P, I, I, P]),
     ("vgemm_im2col3", I, [P, P, P, I, I, I, I, I, P, P, P, I]),
     ("vgemm_epilogue_split", I, [P, P, P, I, I, I, P, P, I, P, P, P]),
@@ -87,6 +98,7 @@ SIGNATURES = [
     ("vgemm_graph_launch", I, [P, P]),
     ("vgemm_graph_destroy", I, [P]),
     ("vgemm_fill_u32", I, [P, P, SZ, U32]),
+    ("vgemm_gn_init", I, [P, P, I]),
     ("vgemm_last_error", ctypes.c_char_p, []),
     ("vgemm_version", ctypes.c_char_p, []),
 ]

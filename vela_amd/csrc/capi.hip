@@ -27,12 +27,13 @@ hipError_t launch_conv_e(hipStream_t st, const uint32_t* pm, int B, int H, int W
 hipError_t launch_im2col3(hipStream_t st, const int32_t* X, const uint32_t* pm, int B, int H, int W, int C, int stride, int8_t* hi, int8_t* lo,
                           int32_t* e, int Kp);
 hipError_t launch_epilogue(hipStream_t st, const int32_t* Chi, const int32_t* Clo, int M, int N, int ldc, const int4* cst, const int32_t* e,
-                           int32_t* Y, int ldy, const int32_t* R);
+                           int32_t* Y, int ldy, const int32_t* R, GnStat* gs, int T);
 hipError_t launch_epilogue_split(hipStream_t st, const int32_t* Chi, const int32_t* Clo, int M, int N, int ldc, const int4* cst,
                                  const int32_t* e, int Cs, int32_t* Y0, int32_t* Y1, int32_t* Y2);
 hipError_t launch_epilogue_geglu_q(hipStream_t st, const int32_t* Chi, const int32_t* Clo, int M, int F, int ldc, const int4* cst,
                                    const int32_t* e, const int32_t* L, int8_t* hi, int8_t* lo, int32_t* eo, int Kp);
 hipError_t launch_fill_u32(hipStream_t st, uint32_t* p, size_t n, uint32_t value);
+hipError_t launch_gn_init(hipStream_t st, GnStat* gs, int n);
 }  // namespace vk
 
 namespace {
@@ -216,10 +217,23 @@ int vgemm_hl2(void* stream, const VgemmASrc* A, int Mp, int Mreal, const int8_t*
     if (!vgemm_supported(Mp, Np, Kp)) return fail(VGEMM_ERR_ARG, "gemm_hl: unsupported shape (Mp %d, Np %d, Kp %d)", Mp, Np, Kp);
     if (Mreal < 0 || Mreal > Mp || Nreal < 0 || Nreal > Np) return fail(VGEMM_ERR_ARG, "gemm_hl: Mreal/Nreal outside Mp/Np");
     if (!W || !cst || ldw < Kp || ldw % 16 || !aligned16(W)) return fail(VGEMM_ERR_ARG, "gemm_hl: W must be 16-byte aligned with ldw >= Kp, ldw %% 16 == 0");
-    if (E->epi == VGEMM_EPI_QKV) return fail(VGEMM_ERR_UNSUPPORTED, "gemm_hl: EPI_QKV is not implemented");
-    if (E->gnstat) return fail(VGEMM_ERR_UNSUPPORTED, "gemm_hl: GroupNorm statistics are not implemented");
-    if (E->epi < 0 || E->epi > VGEMM_EPI_GELU) return fail(VGEMM_ERR_ARG, "gemm_hl: unknown epilogue %d", E->epi);
-    if (!E->Y) return fail(VGEMM_ERR_ARG, "gemm_hl: null Y");
+    if (E->epi < 0 || E->epi > VGEMM_EPI_QKV) return fail(VGEMM_ERR_ARG, "gemm_hl: unknown epilogue %d", E->epi);
+    if (E->epi != VGEMM_EPI_QKV && !E->Y) return fail(VGEMM_ERR_ARG, "gemm_hl: null Y");
+    // GroupNorm statistics (src/gemm_hl.h:22, src/engine.h:110): EPI_PLAIN, 32 groups of whole
+    // columns, a block's rows in at most two samples
+    if (E->gnstat && (E->epi != VGEMM_EPI_PLAIN || Nreal % 32 || E->gnT <= 0 || E->gnT % 64))
+        return fail(VGEMM_ERR_ARG, "gemm_hl: GroupNorm statistics need EPI_PLAIN, Nreal %% 32 == 0 and gnT %% 64 == 0");
+    if (E->epi == VGEMM_EPI_QKV) {
+        // src/engine.cu:318-326: N = 3C, C = 64 heads, rows = B*T, Tp >= T
+        if (E->heads <= 0 || E->C != 64 * E->heads || Nreal != 3 * E->C || E->T <= 0 || E->TpQ < E->T || E->TpK < E->T)
+            return fail(VGEMM_ERR_ARG, "gemm_hl: EPI_QKV needs C = 64*heads, Nreal = 3C, T > 0, TpQ >= T, TpK >= T");
+        const void* ptrs[] = {E->Y2, E->qhi, E->qlo, E->khi, E->klo, E->qe, E->ke, E->qhs, E->qls, E->qts, E->khs, E->kls, E->kts};
+        for (const void* q : ptrs)
+            if (!q) return fail(VGEMM_ERR_ARG, "gemm_hl: EPI_QKV needs Y2 and every q/k output");
+        if (!aligned16(E->Y2) || ((uintptr_t)E->qhi | (uintptr_t)E->qlo | (uintptr_t)E->khi | (uintptr_t)E->klo) & 3)
+            return fail(VGEMM_ERR_ARG, "gemm_hl: EPI_QKV needs a 16-byte aligned Y2 and 4-byte aligned hi/lo planes");
+        if (E->residual || E->rowmax || E->gnstat) return fail(VGEMM_ERR_ARG, "gemm_hl: EPI_QKV takes no residual, rowmax or statistics");
+    }
     if (Mreal == 0 || Nreal == 0) return ok();
 
     vk::GemmParams p;
@@ -277,6 +291,11 @@ int vgemm_hl2(void* stream, const VgemmASrc* A, int Mp, int Mreal, const int8_t*
     const int epi = E->epi;
     p.Y = E->Y; p.ldy = E->ldy; p.R = E->residual; p.Lphi = E->Lphi; p.rowmax = E->rowmax;
     p.Cs = E->Cs; p.Y1 = E->Y1; p.Y2 = E->Y2;
+    p.gnstat = static_cast<vk::GnStat*>(E->gnstat); p.gnT = E->gnT;
+    p.heads = E->heads; p.qT = E->T; p.TpQ = E->TpQ; p.TpK = E->TpK; p.qC = E->C;
+    p.qhi = E->qhi; p.qlo = E->qlo; p.khi = E->khi; p.klo = E->klo; p.qe = E->qe; p.ke = E->ke;
+    p.qhs = reinterpret_cast<long long*>(E->qhs); p.qls = reinterpret_cast<long long*>(E->qls); p.qts = reinterpret_cast<long long*>(E->qts);
+    p.khs = reinterpret_cast<long long*>(E->khs); p.kls = reinterpret_cast<long long*>(E->kls); p.kts = reinterpret_cast<long long*>(E->kts);
     bool vec = aligned16(E->Y);
     switch (epi) {
     case VGEMM_EPI_PLAIN:
@@ -298,12 +317,15 @@ int vgemm_hl2(void* stream, const VgemmASrc* A, int Mp, int Mreal, const int8_t*
         if (E->rowmax || E->residual) return fail(VGEMM_ERR_ARG, "gemm_hl: EPI_SPLIT3 takes no residual or rowmax");
         vec = vec && (!E->Y1 || aligned16(E->Y1)) && (!E->Y2 || aligned16(E->Y2));
         break;
+    case VGEMM_EPI_QKV:
+        vec = true;
+        break;
     }
     p.vec_store = vec ? 1 : 0;
     hipStream_t st = static_cast<hipStream_t>(stream);
 
     // shallow GEMMs with many rows: the row-stationary kernel (forced by variant 4 where it applies)
-    if (stripe_applies(A->src, epi, p) && (g_variant == VARIANT_STRIPE || (g_variant < 0 && stripe_auto(p)))) {
+    if (stripe_applies(A->src, epi, p) && !p.gnstat && (g_variant == VARIANT_STRIPE || (g_variant < 0 && stripe_auto(p)))) {
         const int nout = epi == VGEMM_EPI_GEGLU ? Nreal / 2 : Nreal;
         p.y_bytes = unsigned(((long long)(Mreal - 1) * E->ldy + nout) * 4);
         stripe_grid(p);
@@ -315,11 +337,13 @@ int vgemm_hl2(void* stream, const VgemmASrc* A, int Mp, int Mreal, const int8_t*
     const int halo_bm = A->src == VGEMM_SRC_CONV16 && g_variant < 0 ? vk::conv_halo_bm(epi, p.H, p.W, p.C, p.stride, p.Ho, p.Wo) : 0;
     int variant = halo_bm ? (halo_bm == 128 ? 0 : 1) : g_variant >= 0 && g_variant < NVARIANT ? g_variant : pick_variant(Mreal, Nreal, Kp);
     if (variant >= 3 && (A->src == VGEMM_SRC_X32 || A->src == VGEMM_SRC_CONV32)) variant = 0;
+    if (epi == VGEMM_EPI_QKV) variant = 0;   // whole heads per wave (the reference forces its 64 x 64 tile, src/gemm_hl.cu:358)
     const int BM = TILES[variant].BM, BN = TILES[variant].BN;
     p.mtiles = cdiv(Mreal, BM);
     p.ntiles = cdiv(Nreal, BN);
     const int nK = halo_bm ? p.C / 64 : (Kp + 63) / 64;
-    int splits = E->ws ? pick_splitk(variant, Mreal, Nreal, Kp) : 1;
+    // the split-K epilogue pass carries neither the QKV layout nor the GroupNorm statistics
+    int splits = E->ws && epi != VGEMM_EPI_QKV && !E->gnstat ? pick_splitk(variant, Mreal, Nreal, Kp) : 1;
     if (splits > 1 && ws_bytes_for(variant, Mreal, Nreal, splits) > E->ws_bytes) splits = 1;
     if (splits > nK) splits = nK;
     auto run = [&](int e) {
@@ -407,11 +431,14 @@ int vgemm_quant_rows(void* stream, const int32_t* X, int M, int K, int ldx, int8
 }
 
 int vgemm_epilogue(void* stream, const int32_t* Chi, const int32_t* Clo, int M, int N, int ldc, const int32_t* cst, const int32_t* e, int32_t* Y,
-                   int ldy, const int32_t* residual) {
+                   int ldy, const int32_t* residual, void* gs, int T) {
     if (N % 4 || ldc % 4 || ldy % 4) return fail(VGEMM_ERR_ARG, "epilogue: N/ld must be multiples of 4");
     if (!Chi || !Clo || !cst || !e || !Y || M <= 0 || N <= 0) return fail(VGEMM_ERR_ARG, "epilogue: bad arguments");
     if (!aligned16(Chi) || !aligned16(Clo) || !aligned16(Y) || (residual && !aligned16(residual))) return fail(VGEMM_ERR_ARG, "epilogue: pointers must be 16-byte aligned");
-    return hip_status(vk::launch_epilogue(static_cast<hipStream_t>(stream), Chi, Clo, M, N, ldc, reinterpret_cast<const int4*>(cst), e, Y, ldy, residual),
+    // src/kernels.h:16: 32 groups of whole columns, a block's 1024 elements in one sample
+    if (gs && (N % 32 || T <= 0 || ((long long)T * N) % 1024)) return fail(VGEMM_ERR_ARG, "epilogue: GroupNorm statistics need N %% 32 == 0 and (T*N) %% 1024 == 0");
+    return hip_status(vk::launch_epilogue(static_cast<hipStream_t>(stream), Chi, Clo, M, N, ldc, reinterpret_cast<const int4*>(cst), e, Y, ldy, residual,
+                                          static_cast<vk::GnStat*>(gs), T),
                       "epilogue launch");
 }
 
@@ -477,6 +504,11 @@ int vgemm_fill_u32(void* stream, uint32_t* p, size_t count, uint32_t value) {
     if (!p && count) return fail(VGEMM_ERR_ARG, "fill_u32: null pointer");
     if (!count) return ok();
     return hip_status(vk::launch_fill_u32(static_cast<hipStream_t>(stream), p, count, value), "fill_u32 launch");
+}
+
+int vgemm_gn_init(void* stream, void* gs, int count) {
+    if (!gs || count <= 0) return fail(VGEMM_ERR_ARG, "gn_init: bad arguments");
+    return hip_status(vk::launch_gn_init(static_cast<hipStream_t>(stream), static_cast<vk::GnStat*>(gs), count), "gn_init launch");
 }
 
 const char* vgemm_last_error(void) { return g_err.c_str(); }

@@ -207,6 +207,9 @@ __global__ void __launch_bounds__(256, 2) conv_halo_kernel(const GemmParams p) {
     } else {
         const EpiFlags fl = epi_setup<EPI, SRC_CONV16, BM, BN, 256>(p, pre, 0, sh);
         fused_epilogue<EPI, SRC_CONV16, T>(p, acc_h, acc_l, rbase, n0, 0, sh, fl, er);
+        if constexpr (EPI == EPI_PLAIN) {
+            if (p.gnstat) gn_flush(p, sh);
+        }
     }
 }
 

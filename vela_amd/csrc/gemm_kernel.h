@@ -24,6 +24,7 @@
 // shift. Otherwise it runs the reference's int64 formula element by element.
 #pragma once
 #include <climits>
+#include <type_traits>
 
 #include "vk_common.h"
 
@@ -141,7 +142,44 @@ struct EpiShared {
     int2 lut[LUT ? 2050 : 1];   // lut[i + 1] = (L[i], L[i+1] - L[i]); lut[0] below the table, lut[2049] above
     unsigned long long umax;    // bits of max over columns of 2^22*Kp*|m|*2^-s (a positive double)
     int flag[8];        // emin, emax, smin, smax, column bound failed, table range failed, max |b|, b not foldable
+    // GroupNorm statistics of the block's outputs: [sample slot][group], slot 0 = sample gsb0
+    long long gsum[2][32];
+    int gmin[2][32], gmax[2][32];
+    int gsb0;
 };
+
+// GroupNorm accumulators of a block (src/gemm_hl.cu:175-177, 285-287, 306-309): cleared before the
+// epilogue (by threads 0..63, before a barrier), one LDS atomic per group and value, then flushed
+// to GnStat[sample * 32 + group] by one global atomic each. A block spans at most two samples
+// (gnT % 64 == 0, at most 128 rows), a wave's rows lie in one. A slot is empty when its min and max
+// both keep their initial values; the reference tests min != INT_MAX alone, which also skips a
+// (tile, group) whose every output saturated to INT_MAX (its 64 x 64 tiles differ from these, so
+// that corner case cannot be reproduced tile for tile: the statistics here are the exact ones).
+template <class S>
+__device__ __forceinline__ void gn_clear(const GemmParams& p, int m0, S& sh) {
+    const int tid = threadIdx.x;
+    if (tid < 64) {
+        sh.gsum[tid >> 5][tid & 31] = 0;
+        sh.gmin[tid >> 5][tid & 31] = INT_MAX;
+        sh.gmax[tid >> 5][tid & 31] = INT_MIN;
+    }
+    if (tid == 0) sh.gsb0 = p.gnT > 0 ? m0 / p.gnT : 0;
+}
+
+template <class S>
+__device__ __forceinline__ void gn_flush(const GemmParams& p, S& sh) {
+    __syncthreads();
+    const int tid = threadIdx.x;
+    if (tid < 64) {
+        const int slot = tid >> 5, g = tid & 31;
+        if (sh.gmin[slot][g] != INT_MAX || sh.gmax[slot][g] != INT_MIN) {   // the slot holds values
+            GnStat* gs = p.gnstat + (sh.gsb0 + slot) * 32 + g;
+            atomicAdd(reinterpret_cast<unsigned long long*>(&gs->sum), static_cast<unsigned long long>(sh.gsum[slot][g]));
+            atomicMin(&gs->mn, sh.gmin[slot][g]);
+            atomicMax(&gs->mx, sh.gmax[slot][g]);
+        }
+    }
+}
 
 struct EpiFlags {
     bool fast, ezero, fold;
@@ -157,6 +195,9 @@ __device__ __forceinline__ EpiFlags block_prologue(const GemmParams& p, int m0, 
         sh.flag[0] = INT_MAX; sh.flag[1] = INT_MIN; sh.flag[2] = INT_MAX; sh.flag[3] = INT_MIN;
         sh.flag[4] = 0; sh.flag[5] = 0; sh.flag[6] = 0; sh.flag[7] = 0;
         sh.umax = 0;
+    }
+    if constexpr (EPI == EPI_PLAIN) {
+        if (p.gnstat) gn_clear(p, m0, sh);
     }
     __syncthreads();
     // per-row shift range (one LDS atomic per wave)
@@ -269,6 +310,7 @@ struct TilePre {
     int4 c;
     int e;
     bool cok, eok;
+    int m0;
 };
 
 template <int EPI, int SRC, int BM, int BN>
@@ -282,6 +324,7 @@ __device__ __forceinline__ TilePre load_tile_pre(const GemmParams& p, int m0, in
     const int r = m0 + tid;
     t.eok = tid < BM && r < p.Mreal;
     t.e = t.eok ? (SRC == SRC_X32 ? rowexp_u32(p.xrowmax[r]) : (p.e ? p.e[r] : 0)) : 0;
+    t.m0 = m0;
     return t;
 }
 
@@ -348,6 +391,9 @@ __device__ __forceinline__ EpiFlags epi_setup(const GemmParams& p, const TilePre
         sh.flag[0] = INT_MAX; sh.flag[1] = INT_MIN; sh.flag[2] = INT_MAX; sh.flag[3] = INT_MIN;
         sh.flag[4] = 0; sh.flag[5] = 0; sh.flag[6] = 0; sh.flag[7] = 0;
         sh.umax = 0;
+    }
+    if constexpr (EPI == EPI_PLAIN) {
+        if (p.gnstat) gn_clear(p, t.m0, sh);
     }
     __syncthreads();   // raw table read by everyone, flags reset
     // ---- phase 2: tables, expanded GELU table, flags
@@ -457,6 +503,10 @@ __device__ __forceinline__ void fused_epilogue_t(const GemmParams& p, const v4i 
             }
         }
         const bool full = ncol + 3 < nlim;
+        // GroupNorm statistics of this lane's four columns over its rows (EPI_PLAIN)
+        const bool gn = EPI == EPI_PLAIN && p.gnstat != nullptr;
+        long long gsum[4] = {0, 0, 0, 0};
+        int gmn[4] = {INT_MAX, INT_MAX, INT_MAX, INT_MAX}, gmx[4] = {INT_MIN, INT_MIN, INT_MIN, INT_MIN};
 #pragma unroll
         for (int ms = 0; ms < MS; ++ms) {
             const int r = rbase + ms * 16 + fr;
@@ -548,6 +598,31 @@ __device__ __forceinline__ void fused_epilogue_t(const GemmParams& p, const v4i 
                     for (int v = 0; v < 4; ++v)
                         if (ncol + v < nlim) { ymax[ms] = max(ymax[ms], y[v]); ymin[ms] = min(ymin[ms], y[v]); }
                 }
+                if (gn) {
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) {
+                        gsum[v] += y[v];
+                        gmn[v] = min(gmn[v], y[v]);
+                        gmx[v] = max(gmx[v], y[v]);
+                    }
+                }
+            }
+        }
+        if (gn) {
+            // group of column c: c / (Nreal / 32); the wave's rows lie in one sample (gnT % 64 == 0)
+            S& shw = const_cast<S&>(sh);
+            const int cg = p.Nreal >> 5;
+            const int slot = rbase / p.gnT - shw.gsb0;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                // a lane holds values unless min and max are both still at their initial values
+                // (min == INT_MAX alone would drop columns whose values all saturated to INT_MAX)
+                if (ncol + v < nlim && (gmn[v] != INT_MAX || gmx[v] != INT_MIN)) {
+                    const int g = (ncol + v) / cg;
+                    atomicAdd(reinterpret_cast<unsigned long long*>(&shw.gsum[slot][g]), static_cast<unsigned long long>(gsum[v]));
+                    atomicMin(&shw.gmin[slot][g], gmn[v]);
+                    atomicMax(&shw.gmax[slot][g], gmx[v]);
+                }
             }
         }
     }
@@ -579,6 +654,94 @@ __device__ __forceinline__ void fused_epilogue(const GemmParams& p, const v4i (&
     } else {
         if (smallK) fused_epilogue_t<EPI, SRC, T, false, true, false>(p, acc_h, acc_l, rbase, n0, wn, sh, f.fast, er);
         else fused_epilogue_t<EPI, SRC, T, false, false, false>(p, acc_h, acc_l, rbase, n0, wn, sh, f.fast, er);
+    }
+}
+
+// EPI_QKV (src/gemm_hl.cu:179-241): output columns n = part*C + 64*head + d. Part 2 (v) goes to
+// Y2[r][64*head + d] as int32; parts 0 and 1 (q, k) are quantised per row and head to 16 bits with
+// e = row_exp(max |y| over the head's 64 columns), split into hi/lo bytes at
+// [(b*heads + head)*Tp + t][d] (b = r / T, t = r % T, Tp = TpQ or TpK), with e and the sums of hi,
+// lo and q per row and head (the k_quant_heads layout, src/kernels.cu:611-631). Each head lies in
+// one wave (64-aligned columns, 4 subtiles); y is the reference's int64 formula. Pad rows t >= T are
+// not written (the caller pads them, src/engine.cu:329-330).
+template <class T>
+__device__ __forceinline__ void qkv_epilogue(const GemmParams& p, const v4i (&acc_h)[T::NS][T::MS], const v4i (&acc_l)[T::NS][T::MS],
+                                             int rbase, int n0, int wn, const int (&er)[T::MS]) {
+    constexpr int MS = T::MS, NS = T::NS;
+    static_assert(NS % 4 == 0, "whole heads per wave");
+    const int lane = threadIdx.x & 63, fr = lane & 15, fg = lane >> 4;
+    const int cw = n0 + wn * T::WTN;   // first column of the wave (wsub_row is the identity here)
+#pragma unroll
+    for (int hh = 0; hh < NS / 4; ++hh) {
+        const int c0 = cw + hh * 64;
+        if (c0 >= p.Nreal) continue;
+        const int part = c0 / p.qC, head = (c0 - part * p.qC) >> 6;
+        int4 cc[4][4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) cc[j][v] = p.cst[c0 + 16 * j + 4 * fg + v];
+#pragma unroll
+        for (int ms = 0; ms < MS; ++ms) {
+            const int r = rbase + ms * 16 + fr;
+            const bool rok = r < p.Mreal;
+            int y[4][4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int v = 0; v < 4; ++v)
+                    y[j][v] = epi1_exact(acc_h[4 * hh + j][ms][v], acc_l[4 * hh + j][ms][v], cc[j][v].x, cc[j][v].y, cc[j][v].z,
+                                         cc[j][v].w, er[ms]);
+            if (part == 2) {
+                if (rok) {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        *reinterpret_cast<v4i*>(p.Y2 + size_t(r) * p.qC + head * 64 + 16 * j + 4 * fg) = v4i{y[j][0], y[j][1], y[j][2], y[j][3]};
+                }
+                continue;
+            }
+            // lanes fr, fr + 16, fr + 32, fr + 48 hold the row's 64 values of this head
+            uint32_t m = 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) m = max(m, uabs(y[j][v]));
+            m = max(m, uint32_t(__shfl_xor(int(m), 16)));
+            m = max(m, uint32_t(__shfl_xor(int(m), 32)));
+            const int ee = rowexp_u32(m);
+            const int b = rok ? r / p.qT : 0, t = r - b * p.qT;
+            const size_t gt = size_t(b * p.heads + head) * (part ? p.TpK : p.TpQ) + t;
+            int8_t* hp = part ? p.khi : p.qhi;
+            int8_t* lp = part ? p.klo : p.qlo;
+            int hs = 0, ls = 0, ts = 0;   // |sum of 64 values| < 2^22
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                unsigned hw = 0, lw = 0;
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const int q = quant16_32(y[j][v], ee);
+                    const int h = q >> 8, l = (q & 255) - 128;
+                    hw |= unsigned(h & 255) << (8 * v);
+                    lw |= unsigned(l & 255) << (8 * v);
+                    hs += h;
+                    ls += l;
+                    ts += q;
+                }
+                if (rok) {
+                    *reinterpret_cast<unsigned*>(hp + gt * 64 + 16 * j + 4 * fg) = hw;
+                    *reinterpret_cast<unsigned*>(lp + gt * 64 + 16 * j + 4 * fg) = lw;
+                }
+            }
+            hs += __shfl_xor(hs, 16); hs += __shfl_xor(hs, 32);
+            ls += __shfl_xor(ls, 16); ls += __shfl_xor(ls, 32);
+            ts += __shfl_xor(ts, 16); ts += __shfl_xor(ts, 32);
+            if (rok && fg == 0) {
+                (part ? p.ke : p.qe)[gt] = ee;
+                (part ? p.khs : p.qhs)[gt] = hs;
+                (part ? p.kls : p.qls)[gt] = ls;
+                (part ? p.kts : p.qts)[gt] = ts;
+            }
+        }
     }
 }
 
@@ -911,9 +1074,14 @@ __global__ void __launch_bounds__(T::NT, (dma_waves_per_simd<T, EPI>())) gemm_dm
         store_partial<T>(p, acc_h, acc_l, rbase, n0 + wn * T::WTN, ti.ks);
     } else if constexpr (EPI == EPI_RAW) {
         store_raw<T>(p, acc_h, rbase, n0 + wn * T::WTN, bt);
+    } else if constexpr (EPI == EPI_QKV) {
+        qkv_epilogue<T>(p, acc_h, acc_l, rbase, n0, wn, er);
     } else {
         const EpiFlags fl = epi_setup<EPI, SRC, BM, BN, T::NT>(p, pre, L2048, sh);
         fused_epilogue<EPI, SRC, T>(p, acc_h, acc_l, rbase, n0, wn, sh, fl, er);
+        if constexpr (EPI == EPI_PLAIN) {
+            if (p.gnstat) gn_flush(p, sh);
+        }
     }
 }
 
@@ -1091,8 +1259,13 @@ __global__ void __launch_bounds__(256) gemm_hl_kernel(const GemmParams p) {
     if constexpr (EPI == EPI_PARTIAL) {
         // columns in natural order: W rows were not permuted for partials
         store_partial<T>(p, acc_h, acc_l, rbase, n0 + wn * T::WTN, ti.ks);
+    } else if constexpr (EPI == EPI_QKV) {
+        qkv_epilogue<T>(p, acc_h, acc_l, rbase, n0, wn, er);
     } else {
         fused_epilogue<EPI, SRC, T>(p, acc_h, acc_l, rbase, n0, wn, sh, fl, er);
+        if constexpr (EPI == EPI_PLAIN) {
+            if (p.gnstat) gn_flush(p, sh);
+        }
     }
 }
 
@@ -1214,6 +1387,10 @@ hipError_t launch_gemm_epi(int epi, const GemmParams& p, int batch, hipStream_t 
     case EPI_GEGLU: return VK_LAUNCH(EPI_GEGLU);
     case EPI_GELU: return VK_LAUNCH(EPI_GELU);
     case EPI_PARTIAL: return VK_LAUNCH(EPI_PARTIAL);
+    case EPI_QKV:
+        // whole heads per wave: the 128 x 128 tiles only (the host selects variant 0)
+        if constexpr (std::is_same<T, TileD0>::value || std::is_same<T, TileV0>::value) return VK_LAUNCH(EPI_QKV);
+        else return hipErrorInvalidValue;
     default: return hipErrorInvalidValue;
     }
 #undef VK_LAUNCH

@@ -9,7 +9,7 @@ hipError_t launch_gemm_conv16(int variant, int epi, const GemmParams& p, int bat
 }
 
 int conv_halo_bm(int epi, int H, int W, int C, int stride, int Ho, int Wo) {
-    if (epi == EPI_GEGLU || epi == EPI_GELU) return 0;
+    if (epi == EPI_GEGLU || epi == EPI_GELU || epi == EPI_QKV) return 0;
     return halo_fits(H, W, C, stride, Ho, Wo) ? HaloCfg::BM : 0;
 }
 

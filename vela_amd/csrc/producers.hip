@@ -1,5 +1,7 @@
 // A-operand producers and the planar-path epilogues of the reference (src/kernels.cu), as HIP
 // kernels for gfx950. They are memory-bound; all arithmetic is the reference's exact int64 form.
+#include <climits>
+
 #include "vk_common.h"
 
 namespace vk {
@@ -111,26 +113,62 @@ __global__ void __launch_bounds__(256) im2col3_kernel(const int32_t* __restrict_
     }
 }
 
-// k_epilogue without GroupNorm statistics (src/kernels.cu:70-95): four columns per thread.
+// k_epilogue (src/kernels.cu:70-95): four columns per thread. With GN, the per-(sample, group)
+// sum, min and max of the outputs are gathered in LDS and flushed by one global atomic each per
+// block; a block's 1024 elements lie in one sample ((T * N) % 1024 == 0, checked on the host).
+// A group is flushed when it holds values (min or max moved from its initial value); the reference's
+// test of min != INT_MAX alone would skip a block's group whose outputs all saturated to INT_MAX.
+template <bool GN>
 __global__ void __launch_bounds__(256) epilogue_kernel(const int32_t* __restrict__ Chi, const int32_t* __restrict__ Clo, int M, int N, int ldc,
                                                        const int4* __restrict__ cst, const int32_t* __restrict__ e, int32_t* Y, int ldy,
-                                                       const int32_t* R) {
+                                                       const int32_t* R, GnStat* gs, int T) {
+    __shared__ long long gsum[32];
+    __shared__ int gmin[32], gmax[32];
+    if (GN) {
+        if (threadIdx.x < 32) { gsum[threadIdx.x] = 0; gmin[threadIdx.x] = INT_MAX; gmax[threadIdx.x] = INT_MIN; }
+        __syncthreads();
+    }
     const int tpr = N >> 2;
     const size_t idx = size_t(blockIdx.x) * 256 + threadIdx.x;
-    if (idx >= size_t(M) * tpr) return;
-    const int r = int(idx / tpr), n = int(idx - size_t(r) * tpr) * 4;
-    const int er = e[r];
-    const int4 hv = *reinterpret_cast<const int4*>(Chi + size_t(r) * ldc + n);
-    const int4 lv = *reinterpret_cast<const int4*>(Clo + size_t(r) * ldc + n);
-    const int hh[4] = {hv.x, hv.y, hv.z, hv.w}, ll[4] = {lv.x, lv.y, lv.z, lv.w};
-    int y[4];
+    const bool live = idx < size_t(M) * tpr;
+    if (!GN && !live) return;
+    int r = 0, n = 0;
+    int y[4] = {0, 0, 0, 0};
+    if (live) {
+        r = int(idx / tpr);
+        n = int(idx - size_t(r) * tpr) * 4;
+        const int er = e[r];
+        const int4 hv = *reinterpret_cast<const int4*>(Chi + size_t(r) * ldc + n);
+        const int4 lv = *reinterpret_cast<const int4*>(Clo + size_t(r) * ldc + n);
+        const int hh[4] = {hv.x, hv.y, hv.z, hv.w}, ll[4] = {lv.x, lv.y, lv.z, lv.w};
 #pragma unroll
-    for (int j = 0; j < 4; ++j) { const int4 c = cst[n + j]; y[j] = epi1_exact(hh[j], ll[j], c.x, c.y, c.z, c.w, er); }
-    if (R) {
-        const int4 rv = *reinterpret_cast<const int4*>(R + size_t(r) * ldy + n);
-        y[0] = add_sat(y[0], rv.x); y[1] = add_sat(y[1], rv.y); y[2] = add_sat(y[2], rv.z); y[3] = add_sat(y[3], rv.w);
+        for (int j = 0; j < 4; ++j) { const int4 c = cst[n + j]; y[j] = epi1_exact(hh[j], ll[j], c.x, c.y, c.z, c.w, er); }
+        if (R) {
+            const int4 rv = *reinterpret_cast<const int4*>(R + size_t(r) * ldy + n);
+            y[0] = add_sat(y[0], rv.x); y[1] = add_sat(y[1], rv.y); y[2] = add_sat(y[2], rv.z); y[3] = add_sat(y[3], rv.w);
+        }
+        *reinterpret_cast<int4*>(Y + size_t(r) * ldy + n) = make_int4(y[0], y[1], y[2], y[3]);
     }
-    *reinterpret_cast<int4*>(Y + size_t(r) * ldy + n) = make_int4(y[0], y[1], y[2], y[3]);
+    if (GN) {
+        if (live) {
+            const int cg = N >> 5;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int g = (n + j) / cg;
+                atomicAdd(reinterpret_cast<unsigned long long*>(&gsum[g]), static_cast<unsigned long long>(static_cast<long long>(y[j])));
+                atomicMin(&gmin[g], y[j]);
+                atomicMax(&gmax[g], y[j]);
+            }
+        }
+        __syncthreads();
+        if (threadIdx.x < 32 && (gmin[threadIdx.x] != INT_MAX || gmax[threadIdx.x] != INT_MIN)) {
+            const int b = int(size_t(blockIdx.x) * 256 / size_t(tpr) / size_t(T));
+            GnStat* s = gs + b * 32 + threadIdx.x;
+            atomicAdd(reinterpret_cast<unsigned long long*>(&s->sum), static_cast<unsigned long long>(gsum[threadIdx.x]));
+            atomicMin(&s->mn, gmin[threadIdx.x]);
+            atomicMax(&s->mx, gmax[threadIdx.x]);
+        }
+    }
 }
 
 // k_epilogue_split (src/kernels.cu:97-104)
@@ -209,8 +247,10 @@ hipError_t launch_im2col3(hipStream_t st, const int32_t* X, const uint32_t* pm, 
     return hipGetLastError();
 }
 hipError_t launch_epilogue(hipStream_t st, const int32_t* Chi, const int32_t* Clo, int M, int N, int ldc, const int4* cst, const int32_t* e,
-                           int32_t* Y, int ldy, const int32_t* R) {
-    hipLaunchKernelGGL(epilogue_kernel, dim3(blocks_for(size_t(M) * (N / 4), 256)), dim3(256), 0, st, Chi, Clo, M, N, ldc, cst, e, Y, ldy, R);
+                           int32_t* Y, int ldy, const int32_t* R, GnStat* gs, int T) {
+    const dim3 grid(blocks_for(size_t(M) * (N / 4), 256));
+    if (gs) hipLaunchKernelGGL(epilogue_kernel<true>, grid, dim3(256), 0, st, Chi, Clo, M, N, ldc, cst, e, Y, ldy, R, gs, T);
+    else hipLaunchKernelGGL(epilogue_kernel<false>, grid, dim3(256), 0, st, Chi, Clo, M, N, ldc, cst, e, Y, ldy, R, gs, T);
     return hipGetLastError();
 }
 hipError_t launch_epilogue_split(hipStream_t st, const int32_t* Chi, const int32_t* Clo, int M, int N, int ldc, const int4* cst,
@@ -223,6 +263,22 @@ hipError_t launch_epilogue_geglu_q(hipStream_t st, const int32_t* Chi, const int
     hipLaunchKernelGGL(epilogue_geglu_q_kernel, dim3(unsigned(M)), dim3(256), 0, st, Chi, Clo, F, ldc, cst, e, L, hi, lo, eo, Kp);
     return hipGetLastError();
 }
+// k_gn_init (src/kernels.cu:173): sum 0, mn INT_MAX, mx INT_MIN, ss 0 for cnt statistics records
+__global__ void __launch_bounds__(256) gn_init_kernel(GnStat* __restrict__ gs, int n) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) {
+        gs[i].sum = 0;
+        gs[i].mn = INT_MAX;
+        gs[i].mx = INT_MIN;
+        gs[i].ss = 0;
+    }
+}
+
+hipError_t launch_gn_init(hipStream_t st, GnStat* gs, int n) {
+    hipLaunchKernelGGL(gn_init_kernel, dim3(unsigned((n + 255) / 256)), dim3(256), 0, st, gs, n);
+    return hipGetLastError();
+}
+
 hipError_t launch_fill_u32(hipStream_t st, uint32_t* p, size_t n, uint32_t value) {
     const unsigned g = unsigned(n / 256 + 1 < 4096 ? n / 256 + 1 : 4096);
     hipLaunchKernelGGL(fill_u32_kernel, dim3(g), dim3(256), 0, st, p, n, value);

@@ -11,7 +11,7 @@ import ctypes
 
 import torch
 
-from ._lib import AEpi, ASrc, VgemmError, check, load
+from ._lib import GNSTAT_BYTES, GNSTAT_OFFSETS, AEpi, ASrc, VgemmError, check, load
 
 EPI_PLAIN, EPI_SPLIT3, EPI_GEGLU, EPI_GELU, EPI_QKV = 0, 1, 2, 3, 4
 SRC_I8, SRC_X32, SRC_CONV32, SRC_I16, SRC_CONV16 = 0, 1, 2, 3, 4
@@ -21,7 +21,7 @@ __all__ = [
     "SRC_I8", "SRC_X32", "SRC_CONV32", "SRC_I16", "SRC_CONV16", "k_gemm_hl2", "k_gemm_hl", "k_conv_e",
     "gemm_hl_supported", "set_variant", "get_variant", "set_splitk", "conv16_halo_rows", "workspace_bytes", "Gemm",
     "k_quant_rows", "k_epilogue", "k_pixmax", "k_im2col3", "k_epilogue_split", "k_epilogue_geglu_q",
-    "fill_u32", "Graph", "ptr", "stream_ptr",
+    "fill_u32", "Graph", "ptr", "stream_ptr", "GNSTAT_BYTES", "gn_stats_alloc", "k_gn_init", "gn_stats_read",
 ]
 
 
@@ -120,9 +120,10 @@ def k_quant_rows(X, M: int, K: int, ldx: int, hi, lo, e, Kp: int, stream=None) -
     check(load().vgemm_quant_rows(stream_ptr(stream), ptr(X), M, K, ldx, ptr(hi), ptr(lo), ptr(e), Kp))
 
 
-def k_epilogue(Chi, Clo, M: int, N: int, ldc: int, cst, e, Y, ldy: int, residual=None, stream=None) -> None:
-    """meow::k_epilogue without GroupNorm statistics (src/kernels.h:14-17)."""
-    check(load().vgemm_epilogue(stream_ptr(stream), ptr(Chi), ptr(Clo), M, N, ldc, ptr(cst), ptr(e), ptr(Y), ldy, ptr(residual)))
+def k_epilogue(Chi, Clo, M: int, N: int, ldc: int, cst, e, Y, ldy: int, residual=None, gs=None, T: int = 0, stream=None) -> None:
+    """meow::k_epilogue (src/kernels.h:14-17); gs: GroupNorm statistics records (gn_stats_alloc)."""
+    check(load().vgemm_epilogue(stream_ptr(stream), ptr(Chi), ptr(Clo), M, N, ldc, ptr(cst), ptr(e), ptr(Y), ldy, ptr(residual),
+                                ptr(gs), T))
 
 
 def k_pixmax(X, rows: int, C: int, pm, stream=None) -> None:
@@ -144,6 +145,27 @@ def k_epilogue_geglu_q(Chi, Clo, M: int, F: int, ldc: int, cst, e, Lphi, hi, lo,
     """meow::k_epilogue_geglu_q (src/kernels.h:70)."""
     check(load().vgemm_epilogue_geglu_q(stream_ptr(stream), ptr(Chi), ptr(Clo), M, F, ldc, ptr(cst), ptr(e), ptr(Lphi), ptr(hi), ptr(lo),
                                         ptr(eo), Kp))
+
+
+def gn_stats_alloc(count: int, device="cuda") -> torch.Tensor:
+    """Device memory for `count` GnStat records (48 bytes each, 16-byte aligned), as a uint8 tensor."""
+    return torch.empty(count * GNSTAT_BYTES, dtype=torch.uint8, device=device)
+
+
+def k_gn_init(gs, count: int, stream=None) -> None:
+    """meow::k_gn_init (src/kernels.h:25): sum = ss = 0, mn = INT_MAX, mx = INT_MIN."""
+    check(load().vgemm_gn_init(stream_ptr(stream), ptr(gs), count))
+
+
+def gn_stats_read(gs, count: int) -> dict:
+    """The sum, mn and mx fields of `count` records as int64 numpy arrays (a host copy)."""
+    raw = gs[: count * GNSTAT_BYTES].cpu().numpy().reshape(count, GNSTAT_BYTES)
+    out = {}
+    for name, dt in (("sum", "<i8"), ("mn", "<i4"), ("mx", "<i4")):
+        o = GNSTAT_OFFSETS[name]
+        w = 8 if dt == "<i8" else 4
+        out[name] = raw[:, o:o + w].copy().view(dt).reshape(count).astype("int64")
+    return out
 
 
 def fill_u32(t, value: int = 0, stream=None) -> None:
