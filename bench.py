@@ -14,7 +14,8 @@ replay, every other config's time, and the CPU baseline: the oracle restatement 
 integer semantics (the reference has no CPU GEMM of its own), timed on this host's cores.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-unet] [--no-cpu] [--no-configs]
-       python bench.py --only {c1,c2,c2plain,c3,c4a,c4b,c4c,copy}   (one kernel, for profiler runs)
+       python bench.py --only {c1,c2,c2plain,c3,c4a,c4b,c4c,copy,unet<i>}   (one kernel, for profiler runs)
+       python bench.py --unet-layers   (each C5 layer timed alone)
 """
 from __future__ import annotations
 
@@ -40,6 +41,8 @@ COPY_BYTES = 256 << 20       # the calibration copy of --only copy: 256 MiB read
 def only_layer(name):
     from vela_amd import configs as cf
 
+    if name.startswith("unet"):
+        return cf.unet_layers()[int(name[4:])]
     return {"c1": cf.c1, "c2": lambda: cf.c2(cf.EPI_GEGLU), "c2plain": lambda: cf.c2(cf.EPI_PLAIN), "c3": cf.c3,
             "c4a": lambda: cf.c4()[0], "c4b": lambda: cf.c4()[1], "c4c": lambda: cf.c4()[2]}[name]()
 
@@ -68,7 +71,7 @@ def time_launches(fn, stream, steps, warmup):
 
 def pmc_traffic():
     """HBM bytes per launch of the C2 kernel from the committed rocprofv3 counter summary, if present."""
-    p = ROOT / "profiles" / "c2_geglu_pmc.json"
+    p = ROOT / "profiles" / "stripe_kernel_c2_geglu_pmc.json"
     if p.exists():
         try:
             d = json.loads(p.read_text())
@@ -176,8 +179,12 @@ def main():
     ap.add_argument("--no-unet", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-configs", action="store_true")
-    ap.add_argument("--only", choices=ONLY_NAMES, help="time one configuration only (for profiler runs)")
+    ap.add_argument("--only", help="time one configuration only (for profiler runs): one of " + ", ".join(ONLY_NAMES) +
+                    ", or unet<i> for layer i of the C5 set")
+    ap.add_argument("--unet-layers", action="store_true", help="time each C5 layer alone (one JSON line per layer)")
     args = ap.parse_args()
+    if args.only and args.only not in ONLY_NAMES and not (args.only.startswith("unet") and args.only[4:].isdigit()):
+        ap.error(f"--only: unknown configuration {args.only}")
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (the GEMM shards by rows with no "
               "communication; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
@@ -203,6 +210,20 @@ def main():
         log(f"[bench] copy {COPY_BYTES >> 20} MiB: {t * 1e3:.2f} us/launch, {2 * COPY_BYTES / (t * 1e-3) / 1e9:.0f} GB/s")
         print(json.dumps({"workload": "copy", "bytes_read": COPY_BYTES, "bytes_written": COPY_BYTES, "us": round(t * 1e3, 3)}), flush=True)
         return
+    if args.unet_layers:
+        total = 0.0
+        for i, L in enumerate(cf.unet_layers()):
+            p = cf.DeviceProblem(L)
+            p.reset()
+            torch.cuda.synchronize()
+            t = time_launches(lambda: p.run(stream=stream), stream, args.steps, args.warmup)
+            total += t
+            print(json.dumps({"i": i, "layer": L.name, "kind": L.kind, "M": L.M, "K": L.K, "N": L.N, "epi": L.epi,
+                              "residual": L.residual, "us": round(t * 1e3, 2),
+                              "tops": round(L.ops / (t * 1e-3) / 1e12, 1)}), flush=True)
+            del p
+        log(f"[bench] C5 layers launched one at a time: {total:.3f} ms in total")
+        return
     if args.only:
         L = only_layer(args.only)
         p = cf.DeviceProblem(L)
@@ -227,7 +248,7 @@ def main():
     vendor_c2 = vendor_planar_us(L, stream)
     roof = roofline(L.ops, L.hbm_bytes, ms * 1e-3)
     roof["traffic"] = traffic
-    roof.update({"traffic_source": traffic_src, "kernel": "vk::gemm_dma_kernel<SRC_I16, EPI_GEGLU, Tile<128,128,4,1>>",
+    roof.update({"traffic_source": traffic_src, "kernel": "vk::stripe_kernel<SRC_I16, EPI_GEGLU>",
                  "algorithmic_ops_per_launch": L.ops, "algorithmic_bytes_per_launch": L.hbm_bytes,
                  "mfma_frac": round(tops / PEAK_INT8_TOPS, 4),
                  "hbm_frac": round(L.hbm_bytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)})
@@ -276,7 +297,7 @@ def main():
 
         log("[bench] C5: building the 194-GEMM UNet set")
         gs = GemmSet()
-        gs.capture()
+        gs.capture(reseed=False)   # GEMMs + rowmax fills only: no residual re-seeding copies
         t = time_launches(gs.replay, gs.stream, max(5, args.steps // 2), 2)
         out["unet_gemm_set_ms"] = round(t, 4)
         out["unet_gemm_set"] = {"gemms": len(gs.layers), "ms": round(t, 4), "tops": round(gs.ops / (t * 1e-3) / 1e12, 2),

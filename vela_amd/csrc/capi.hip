@@ -352,7 +352,7 @@ int vgemm_hl2(void* stream, const VgemmASrc* A, int Mp, int Mreal, const int8_t*
     };
     if (splits <= 1) {
         p.ksplit = 1; p.kper = nK;
-        return run(epi);
+        return run(p.gnstat ? vk::EPI_PLAIN_GN : epi);
     }
     if (!aligned16(E->ws)) return fail(VGEMM_ERR_ARG, "gemm_hl: workspace must be 16-byte aligned");
     p.ksplit = splits;

@@ -54,7 +54,7 @@ __global__ void __launch_bounds__(256, 2) conv_halo_kernel(const GemmParams p) {
 
     __shared__ __attribute__((aligned(16))) unsigned char smemW[NSTW * HC::W_BYTES];
     __shared__ __attribute__((aligned(16))) unsigned char smemP[2 * HC::P_BYTES];
-    __shared__ __attribute__((aligned(16))) EpiShared<FUSED ? BN : 1, false> sh;
+    __shared__ __attribute__((aligned(16))) EpiShared<FUSED ? BN : 1, false, EPI == EPI_PLAIN_GN> sh;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const TileIdx ti = tile_index(p);
@@ -207,9 +207,7 @@ __global__ void __launch_bounds__(256, 2) conv_halo_kernel(const GemmParams p) {
     } else {
         const EpiFlags fl = epi_setup<EPI, SRC_CONV16, BM, BN, 256>(p, pre, 0, sh);
         fused_epilogue<EPI, SRC_CONV16, T>(p, acc_h, acc_l, rbase, n0, 0, sh, fl, er);
-        if constexpr (EPI == EPI_PLAIN) {
-            if (p.gnstat) gn_flush(p, sh);
-        }
+        if constexpr (EPI == EPI_PLAIN_GN) gn_flush(p, sh);
     }
 }
 
@@ -217,6 +215,7 @@ inline hipError_t launch_conv_halo(int epi, const GemmParams& p, hipStream_t st)
     dim3 grid(unsigned(p.mtiles * p.ntiles * p.ksplit));
     switch (epi) {
     case EPI_PLAIN: hipLaunchKernelGGL(conv_halo_kernel<EPI_PLAIN>, grid, dim3(256), 0, st, p); break;
+    case EPI_PLAIN_GN: hipLaunchKernelGGL(conv_halo_kernel<EPI_PLAIN_GN>, grid, dim3(256), 0, st, p); break;
     case EPI_SPLIT3: hipLaunchKernelGGL(conv_halo_kernel<EPI_SPLIT3>, grid, dim3(256), 0, st, p); break;
     case EPI_PARTIAL: hipLaunchKernelGGL(conv_halo_kernel<EPI_PARTIAL>, grid, dim3(256), 0, st, p); break;
     default: return hipErrorInvalidValue;

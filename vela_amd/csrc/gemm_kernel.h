@@ -133,19 +133,25 @@ __device__ __forceinline__ void quant16_pairs(unsigned* d, int e) {
 
 // ---------------------------------------------------------------- epilogue shared state
 
+// GroupNorm accumulators of a block (EPI_PLAIN_GN only): [sample slot][group], slot 0 = sample gsb0
+template <bool GN>
+struct GnShared {};
+template <>
+struct GnShared<true> {
+    long long gsum[2][32];
+    int gmin[2][32], gmax[2][32];
+    int gsb0;
+};
+
 // Per-block epilogue constants, GELU table and exactness flags, in LDS.
-template <int BN, bool LUT>
-struct EpiShared {
+template <int BN, bool LUT, bool GN = false>
+struct EpiShared : GnShared<GN> {
     double ms[BN];      // m * 2^-s
     double wm[BN];      // 128 * wsum * m * 2^-s; + 1/2 when e == 0, and + b as well when the block folds b
     int b[BN];
     int2 lut[LUT ? 2050 : 1];   // lut[i + 1] = (L[i], L[i+1] - L[i]); lut[0] below the table, lut[2049] above
     unsigned long long umax;    // bits of max over columns of 2^22*Kp*|m|*2^-s (a positive double)
     int flag[8];        // emin, emax, smin, smax, column bound failed, table range failed, max |b|, b not foldable
-    // GroupNorm statistics of the block's outputs: [sample slot][group], slot 0 = sample gsb0
-    long long gsum[2][32];
-    int gmin[2][32], gmax[2][32];
-    int gsb0;
 };
 
 // GroupNorm accumulators of a block (src/gemm_hl.cu:175-177, 285-287, 306-309): cleared before the
@@ -196,9 +202,7 @@ __device__ __forceinline__ EpiFlags block_prologue(const GemmParams& p, int m0, 
         sh.flag[4] = 0; sh.flag[5] = 0; sh.flag[6] = 0; sh.flag[7] = 0;
         sh.umax = 0;
     }
-    if constexpr (EPI == EPI_PLAIN) {
-        if (p.gnstat) gn_clear(p, m0, sh);
-    }
+    if constexpr (EPI == EPI_PLAIN_GN) gn_clear(p, m0, sh);
     __syncthreads();
     // per-row shift range (one LDS atomic per wave)
     {
@@ -392,9 +396,7 @@ __device__ __forceinline__ EpiFlags epi_setup(const GemmParams& p, const TilePre
         sh.flag[4] = 0; sh.flag[5] = 0; sh.flag[6] = 0; sh.flag[7] = 0;
         sh.umax = 0;
     }
-    if constexpr (EPI == EPI_PLAIN) {
-        if (p.gnstat) gn_clear(p, t.m0, sh);
-    }
+    if constexpr (EPI == EPI_PLAIN_GN) gn_clear(p, t.m0, sh);
     __syncthreads();   // raw table read by everyone, flags reset
     // ---- phase 2: tables, expanded GELU table, flags
     if (tid < BN) { sh.ms[tid] = ms; sh.wm[tid] = wmv; sh.b[tid] = bb; }
@@ -503,8 +505,8 @@ __device__ __forceinline__ void fused_epilogue_t(const GemmParams& p, const v4i 
             }
         }
         const bool full = ncol + 3 < nlim;
-        // GroupNorm statistics of this lane's four columns over its rows (EPI_PLAIN)
-        const bool gn = EPI == EPI_PLAIN && p.gnstat != nullptr;
+        // GroupNorm statistics of this lane's four columns over its rows (EPI_PLAIN_GN)
+        constexpr bool gn = EPI == EPI_PLAIN_GN;
         long long gsum[4] = {0, 0, 0, 0};
         int gmn[4] = {INT_MAX, INT_MAX, INT_MAX, INT_MAX}, gmx[4] = {INT_MIN, INT_MIN, INT_MIN, INT_MIN};
 #pragma unroll
@@ -598,7 +600,7 @@ __device__ __forceinline__ void fused_epilogue_t(const GemmParams& p, const v4i 
                     for (int v = 0; v < 4; ++v)
                         if (ncol + v < nlim) { ymax[ms] = max(ymax[ms], y[v]); ymin[ms] = min(ymin[ms], y[v]); }
                 }
-                if (gn) {
+                if constexpr (gn) {
 #pragma unroll
                     for (int v = 0; v < 4; ++v) {
                         gsum[v] += y[v];
@@ -608,7 +610,7 @@ __device__ __forceinline__ void fused_epilogue_t(const GemmParams& p, const v4i 
                 }
             }
         }
-        if (gn) {
+        if constexpr (gn) {
             // group of column c: c / (Nreal / 32); the wave's rows lie in one sample (gnT % 64 == 0)
             S& shw = const_cast<S&>(sh);
             const int cg = p.Nreal >> 5;
@@ -847,7 +849,7 @@ __global__ void __launch_bounds__(T::NT, (dma_waves_per_simd<T, EPI>())) gemm_dm
     constexpr bool TWO = D::TWO, FUSED = D::FUSED;
 
     __shared__ __attribute__((aligned(16))) unsigned char smem[NST * D::STAGE];
-    __shared__ __attribute__((aligned(16))) EpiShared<FUSED ? BN : 1, D::NEEDLUT> sh;
+    __shared__ __attribute__((aligned(16))) EpiShared<FUSED ? BN : 1, D::NEEDLUT, EPI == EPI_PLAIN_GN> sh;
 
     // the wave index in a scalar register (the DMA's LDS addresses must be wave-uniform); waves
     // are WM x WN over the tile, wm the row slot and wn the column slot
@@ -1079,9 +1081,7 @@ __global__ void __launch_bounds__(T::NT, (dma_waves_per_simd<T, EPI>())) gemm_dm
     } else {
         const EpiFlags fl = epi_setup<EPI, SRC, BM, BN, T::NT>(p, pre, L2048, sh);
         fused_epilogue<EPI, SRC, T>(p, acc_h, acc_l, rbase, n0, wn, sh, fl, er);
-        if constexpr (EPI == EPI_PLAIN) {
-            if (p.gnstat) gn_flush(p, sh);
-        }
+        if constexpr (EPI == EPI_PLAIN_GN) gn_flush(p, sh);
     }
 }
 
@@ -1097,7 +1097,7 @@ __global__ void __launch_bounds__(256) gemm_hl_kernel(const GemmParams p) {
     static_assert(SRC == SRC_X32 || SRC == SRC_CONV32, "register path serves the int32 sources");
 
     __shared__ __attribute__((aligned(16))) unsigned char smem[2 * T::STAGE];
-    __shared__ __attribute__((aligned(16))) EpiShared<FUSED ? BN : 1, NEEDLUT> sh;
+    __shared__ __attribute__((aligned(16))) EpiShared<FUSED ? BN : 1, NEEDLUT, EPI == EPI_PLAIN_GN> sh;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave % T::WM, wn = wave / T::WM;
@@ -1263,9 +1263,7 @@ __global__ void __launch_bounds__(256) gemm_hl_kernel(const GemmParams p) {
         qkv_epilogue<T>(p, acc_h, acc_l, rbase, n0, wn, er);
     } else {
         fused_epilogue<EPI, SRC, T>(p, acc_h, acc_l, rbase, n0, wn, sh, fl, er);
-        if constexpr (EPI == EPI_PLAIN) {
-            if (p.gnstat) gn_flush(p, sh);
-        }
+        if constexpr (EPI == EPI_PLAIN_GN) gn_flush(p, sh);
     }
 }
 
@@ -1383,6 +1381,7 @@ hipError_t launch_gemm_epi(int epi, const GemmParams& p, int batch, hipStream_t 
     }()
     switch (epi) {
     case EPI_PLAIN: return VK_LAUNCH(EPI_PLAIN);
+    case EPI_PLAIN_GN: return VK_LAUNCH(EPI_PLAIN_GN);
     case EPI_SPLIT3: return VK_LAUNCH(EPI_SPLIT3);
     case EPI_GEGLU: return VK_LAUNCH(EPI_GEGLU);
     case EPI_GELU: return VK_LAUNCH(EPI_GELU);

@@ -13,7 +13,9 @@ typedef long long i64;
 typedef unsigned long long u64;
 
 enum { SRC_I8 = 0, SRC_X32 = 1, SRC_CONV32 = 2, SRC_I16 = 3, SRC_CONV16 = 4 };
-enum { EPI_PLAIN = 0, EPI_SPLIT3 = 1, EPI_GEGLU = 2, EPI_GELU = 3, EPI_QKV = 4, EPI_PARTIAL = 8, EPI_RAW = 9 };
+// EPI_PLAIN_GN: EPI_PLAIN that also accumulates GroupNorm statistics (a kernel instantiation of its
+// own, so that the plain kernels carry none of its registers or code)
+enum { EPI_PLAIN = 0, EPI_SPLIT3 = 1, EPI_GEGLU = 2, EPI_GELU = 3, EPI_QKV = 4, EPI_PLAIN_GN = 5, EPI_PARTIAL = 8, EPI_RAW = 9 };
 
 // Per-(sample, group) GroupNorm statistics (src/kernels.h:9, same layout): the GEMM epilogue accumulates
 // sum, mn and mx; the other fields belong to the normalisation that follows.
@@ -58,7 +60,7 @@ struct GemmParams {
     int mtiles, ntiles;
     // strided batch (EPI_RAW)
     long long sA, sW, sC;
-    // GroupNorm statistics of the output (EPI_PLAIN): GnStat[sample * 32 + group], gnT rows per sample
+    // GroupNorm statistics of the output (EPI_PLAIN_GN): GnStat[sample * 32 + group], gnT rows per sample
     GnStat* gnstat; int gnT;
     // EPI_QKV (src/gemm_hl.h:23-25): N = 3C, C = 64 heads; q/k head-quantised, v int32 into Y2
     int heads, qT, TpQ, TpK, qC;

@@ -35,24 +35,31 @@ class GemmSet:
     def ops(self) -> int:
         return sum(L.ops for L in self.layers)
 
-    def _enqueue(self):
+    def _enqueue(self, reseed: bool = True):
         for p in self.probs:
-            p.reset()
+            if reseed:
+                p.reset()
+            elif p.rowmax is not None:
+                vg.fill_u32(p.rowmax, 0)
             p.run(stream=self.stream)
 
     def run_eager(self):
         with torch.cuda.stream(self.stream):
             self._enqueue()
 
-    def capture(self):
-        """Capture the whole set (residual re-seeds and rowmax zeroing by kernels, then the GEMM of
-        each layer, in forward order) into one graph."""
+    def capture(self, reseed: bool = True):
+        """Capture the whole set into one graph: for each layer in forward order, rowmax zeroing by a
+        kernel (the engine clears every rowmax buffer it allocates, src/engine.cu:161) and the GEMM.
+        With reseed, residual layers first copy their seeded residual back into Y, so that every
+        replay computes the same bytes (the parity tests); without it, Y accumulates in place from
+        replay to replay as the forward's residual stream does, and the graph holds only the GEMMs and
+        the rowmax fills (the timed C5 set)."""
         self.run_eager()                      # first calls outside capture
         self.stream.synchronize()
         self.graph = vg.Graph(self.stream)
         with torch.cuda.stream(self.stream):
             self.graph.begin()
-            self._enqueue()
+            self._enqueue(reseed)
             self.graph.end()
 
     def replay(self):
