@@ -3,11 +3,13 @@
 // fused hi/lo GEMM against the planar path -- Gemm::run over the stacked [hi; lo] planes plus
 // k_epilogue -- for every tile variant; SRC_X32 against k_quant_rows + SRC_I8; SRC_CONV32 against
 // k_pixmax + k_conv_e + k_im2col3 + SRC_I8), plus an int64 host check of the planar path, a graph
-// capture and replay (src/engine.cu:610-631), and the throwing error paths (src/gemm_hl.cu:351,357).
+// capture and replay (src/engine.cu:610-631), GroupNorm statistics (fused and planar, with
+// k_gn_init), the EPI_QKV head layout, and the throwing error paths (src/gemm_hl.cu:351,357).
 // Needs a GPU; run by tests/test_gpu_dropin.py. Prints one line per check and exits non-zero on the
 // first mismatch.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -221,6 +223,100 @@ void test_graph(hipStream_t st, std::mt19937& rng) {
     HIP_OK(hipGraphDestroy(g));
 }
 
+// GroupNorm statistics (src/engine.cu:170-172, src/kernels.cu:63-95): the fused GEMM with gnstat and
+// the planar Gemm::run + k_epilogue(..., gs, T) fill the same records, equal to a host reduction
+void test_gnstat(hipStream_t st, std::mt19937& rng) {
+    const int T = 64, B = 3, M = B * T, N = 320;
+    Problem p = make(rng, M, N, 320);
+    std::vector<int8_t> planes(p.hi);
+    planes.insert(planes.end(), p.lo.begin(), p.lo.end());
+    Dev<int8_t> A(planes), W(p.w);
+    Dev<int32_t> cst(p.cst), e(p.e), Yf(p.res), Yp(p.res), C(size_t(2) * p.Mp * p.Np);
+    Dev<meow::GnStat> gf(size_t(B) * 32), gp(size_t(B) * 32);
+    meow::k_gn_init(st, gf.p, B * 32);
+    meow::k_gn_init(st, gp.p, B * 32);
+    meow::ASrc a;
+    a.src = meow::SRC_I8; a.hi = A.p; a.lo = A.p + size_t(p.Mp) * p.Kp; a.ld8 = p.Kp; a.e = e.p;
+    meow::AEpi ep;
+    ep.Y = Yf.p; ep.ldy = N; ep.residual = Yf.p; ep.gnstat = gf.p; ep.gnT = T;
+    meow::k_gemm_hl2(st, a, p.Mp, M, W.p, p.Kp, p.Np, N, p.Kp, reinterpret_cast<const int4*>(cst.p), ep);
+    meow::Gemm lt;
+    lt.init(0);
+    lt.run(st, A.p, p.Kp, 0, W.p, p.Kp, 0, C.p, p.Np, 0, 2 * p.Mp, p.Np, p.Kp);
+    meow::k_epilogue(st, C.p, C.p + size_t(p.Mp) * p.Np, M, N, p.Np, reinterpret_cast<const int4*>(cst.p), e.p, Yp.p, N, Yp.p, gp.p, T);
+    HIP_OK(hipStreamSynchronize(st));
+    const std::vector<int32_t> want = host_ref(p, true);
+    expect(Yf.get() == want && Yp.get() == want, "GroupNorm GEMMs: Y == int64 host");
+    const std::vector<meow::GnStat> sf = gf.get(), sp = gp.get();
+    bool ok = true;
+    for (int b = 0; b < B; ++b)
+        for (int g = 0; g < 32; ++g) {
+            int64_t sum = 0;
+            int mn = INT32_MAX, mx = INT32_MIN;
+            for (int r = b * T; r < (b + 1) * T; ++r)
+                for (int n = g * (N / 32); n < (g + 1) * (N / 32); ++n) {
+                    const int v = want[size_t(r) * N + n];
+                    sum += v;
+                    mn = v < mn ? v : mn;
+                    mx = v > mx ? v : mx;
+                }
+            for (const auto* s : {&sf[b * 32 + g], &sp[b * 32 + g]}) ok = ok && s->sum == sum && s->mn == mn && s->mx == mx;
+        }
+    expect(ok, "GroupNorm records: fused gnstat == k_epilogue(gs) == host reduction");
+}
+
+// EPI_QKV (src/engine.cu:318-330): v and the head-quantised q/k against a host restatement of the
+// k_quant_heads layout (src/kernels.cu:611-631) over the plain GEMM output
+void test_qkv(hipStream_t st, std::mt19937& rng) {
+    const int heads = 2, C = 64 * heads, T = 77, B = 2, M = B * T, TpQ = 128, TpK = 128;
+    Problem p = make(rng, M, 3 * C, 320);
+    Dev<int8_t> hi(p.hi), lo(p.lo), W(p.w);
+    Dev<int32_t> cst(p.cst), e(p.e), V(size_t(M) * C);
+    const size_t G = size_t(B) * heads * TpQ;
+    Dev<int8_t> qhi(G * 64), qlo(G * 64), khi(G * 64), klo(G * 64);
+    Dev<int32_t> qe(G), ke(G);
+    Dev<int64_t> qhs(G), qls(G), qts(G), khs(G), kls(G), kts(G);
+    meow::ASrc a;
+    a.src = meow::SRC_I8; a.hi = hi.p; a.lo = lo.p; a.ld8 = p.Kp; a.e = e.p;
+    meow::AEpi ep;
+    ep.epi = meow::EPI_QKV; ep.Y2 = V.p; ep.heads = heads; ep.T = T; ep.TpQ = TpQ; ep.TpK = TpK; ep.C = C;
+    ep.qhi = qhi.p; ep.qlo = qlo.p; ep.khi = khi.p; ep.klo = klo.p; ep.qe = qe.p; ep.ke = ke.p;
+    ep.qhs = qhs.p; ep.qls = qls.p; ep.qts = qts.p; ep.khs = khs.p; ep.kls = kls.p; ep.kts = kts.p;
+    meow::k_gemm_hl2(st, a, p.Mp, M, W.p, p.Kp, p.Np, 3 * C, p.Kp, reinterpret_cast<const int4*>(cst.p), ep);
+    HIP_OK(hipStreamSynchronize(st));
+    const std::vector<int32_t> y = host_ref(p, false);
+    bool vok = true;
+    const std::vector<int32_t> vg = V.get();
+    for (int r = 0; r < M; ++r)
+        for (int c = 0; c < C; ++c) vok = vok && vg[size_t(r) * C + c] == y[size_t(r) * 3 * C + 2 * C + c];
+    expect(vok, "EPI_QKV v == plain GEMM columns [2C, 3C)");
+    bool qok = true;
+    for (int part = 0; part < 2; ++part) {
+        const std::vector<int8_t> H = (part ? khi : qhi).get(), L = (part ? klo : qlo).get();
+        const std::vector<int32_t> E = (part ? ke : qe).get();
+        const std::vector<int64_t> HS = (part ? khs : qhs).get(), LS = (part ? kls : qls).get(), TS = (part ? kts : qts).get();
+        for (int r = 0; r < M; ++r)
+            for (int h = 0; h < heads; ++h) {
+                const int32_t* v = &y[size_t(r) * 3 * C + part * C + 64 * h];
+                int64_t m = 0;
+                for (int d = 0; d < 64; ++d) m = std::max<int64_t>(m, v[d] < 0 ? -int64_t(v[d]) : v[d]);
+                int ee = 0;
+                for (int k = 15; k < 32; ++k) ee += m >= (int64_t(1) << k);
+                const size_t gt = size_t((r / T) * heads + h) * (part ? TpK : TpQ) + r % T;
+                int64_t hs = 0, ls = 0, ts = 0;
+                for (int d = 0; d < 64; ++d) {
+                    int q = ee ? (v[d] >> ee) + ((v[d] >> (ee - 1)) & 1) : v[d];
+                    q = q < -32767 ? -32767 : (q > 32767 ? 32767 : q);
+                    const int hb = q >> 8, lb = (q & 255) - 128;
+                    qok = qok && H[gt * 64 + d] == hb && L[gt * 64 + d] == lb;
+                    hs += hb; ls += lb; ts += q;
+                }
+                qok = qok && E[gt] == ee && HS[gt] == hs && LS[gt] == ls && TS[gt] == ts;
+            }
+    }
+    expect(qok, "EPI_QKV q/k planes, e and sums == host k_quant_heads restatement");
+}
+
 void test_errors(hipStream_t st) {
     expect(!meow::gemm_hl_supported(100, 64, 16) && meow::gemm_hl_supported(128, 64, 16), "gemm_hl_supported");
     bool threw = false;
@@ -255,6 +351,8 @@ int main() {
         test_x32(st, rng);
         test_conv32(st, rng);
         test_graph(st, rng);
+        test_gnstat(st, rng);
+        test_qkv(st, rng);
         test_errors(st);
     } catch (const std::exception& ex) {
         std::printf("FAIL exception: %s\n", ex.what());
