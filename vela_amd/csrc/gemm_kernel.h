@@ -1267,31 +1267,35 @@ __global__ void __launch_bounds__(256) gemm_hl_kernel(const GemmParams p) {
     }
 }
 
-// Split-K reduction and epilogue: one thread per row and group of four output columns; sums the
-// int32 partials of all K ranges and applies the exact int64 epilogue.
+// Split-K reduction and epilogue: one thread per (row, group of four output columns), numbered row by
+// row over a flat grid so that every thread has work whatever the column count; sums the int32
+// partials of all K ranges and applies the exact int64 epilogue.
 template <int EPI>
 __global__ void __launch_bounds__(256) splitk_epilogue_kernel(const GemmParams p) {
-    // grid: x = groups of 1024 output columns (4 per thread), y = rows (strided when M > gridDim.y)
     const int nout = EPI == EPI_GEGLU ? (p.Nreal >> 1) : p.Nreal;
-    const int c0 = (blockIdx.x * 256 + threadIdx.x) * 4;
+    const int tpr = (nout + 3) >> 2;   // threads per row
+    const unsigned total = unsigned(p.Mreal) * unsigned(tpr);
     const size_t plane = size_t(p.ws_rows) * p.ws_ld;
-    const bool in = c0 < nout;
-    const bool full = c0 + 3 < nout;
-    for (int r = blockIdx.y; r < p.Mreal; r += gridDim.y) {
-        const int er = p.xrowmax ? rowexp_u32(p.xrowmax[r]) : (p.e ? p.e[r] : 0);
-        // plane sums of ws columns [wc, wc + 4) over the K splits (16-byte loads: ws_ld % 4 == 0)
-        auto sum4 = [&](int wc, v4i& h, v4i& l) {
-            h = v4i{0, 0, 0, 0};
-            l = v4i{0, 0, 0, 0};
-            for (int s = 0; s < p.ksplit; ++s) {
-                const int32_t* b = p.ws + (size_t(s * 2) * p.ws_rows + r) * p.ws_ld + wc;
-                h += *reinterpret_cast<const v4i*>(b);
-                l += *reinterpret_cast<const v4i*>(b + plane);
-            }
-        };
-        int y[4] = {0, 0, 0, 0};
+    for (unsigned idx = blockIdx.x * 256u + threadIdx.x; idx - threadIdx.x < total; idx += gridDim.x * 256u) {
+        const bool live = idx < total;
+        const int r = live ? int(idx / unsigned(tpr)) : 0;
+        const int c0 = live ? int(idx - unsigned(r) * unsigned(tpr)) * 4 : 0;
+        const bool full = c0 + 3 < nout;
         uint32_t mx = 0;
-        if (in) {
+        if (live) {
+            const int er = p.xrowmax ? rowexp_u32(p.xrowmax[r]) : (p.e ? p.e[r] : 0);
+            // plane sums of ws columns [wc, wc + 4) over the K splits (16-byte loads: ws_ld % 4 == 0)
+            auto sum4 = [&](int wc, v4i& h, v4i& l) {
+                h = v4i{0, 0, 0, 0};
+                l = v4i{0, 0, 0, 0};
+#pragma unroll 4
+                for (int s = 0; s < p.ksplit; ++s) {
+                    const int32_t* b = p.ws + (size_t(s * 2) * p.ws_rows + r) * p.ws_ld + wc;
+                    h += *reinterpret_cast<const v4i*>(b);
+                    l += *reinterpret_cast<const v4i*>(b + plane);
+                }
+            };
+            int y[4] = {0, 0, 0, 0};
             if constexpr (EPI == EPI_GEGLU) {
                 v4i h0, l0, h1, l1;
                 sum4(2 * c0, h0, l0);       // columns a0 g0 a1 g1
@@ -1348,10 +1352,15 @@ __global__ void __launch_bounds__(256) splitk_epilogue_kernel(const GemmParams p
             }
         }
         if (EPI != EPI_SPLIT3 && p.rowmax) {
-            // every lane of the wave is on row r: one atomic per wave
+            // one atomic per wave when the wave's lanes share a row, else one per lane
+            const int r0 = __shfl(r, 0), r63 = __shfl(r, 63);
+            if (r0 == r63) {
 #pragma unroll
-            for (int o = 32; o; o >>= 1) mx = max(mx, uint32_t(__shfl_xor(int(mx), o)));
-            if ((threadIdx.x & 63) == 0 && mx) atomicMax(p.rowmax + r, mx);
+                for (int o = 32; o; o >>= 1) mx = max(mx, uint32_t(__shfl_xor(int(mx), o)));
+                if ((threadIdx.x & 63) == 0 && mx) atomicMax(p.rowmax + r, mx);
+            } else if (live && mx) {
+                atomicMax(p.rowmax + r, mx);
+            }
         }
     }
 }

@@ -1,4 +1,6 @@
 // Single-plane int8 x int8 -> int32 GEMM (the Gemm::run replacement) and the split-K epilogue.
+#include <algorithm>
+
 #include "gemm_kernel.h"
 
 namespace vk {
@@ -13,7 +15,9 @@ hipError_t launch_gemm_raw(int variant, const GemmParams& p, int batch, hipStrea
 
 hipError_t launch_splitk_epilogue(int epi, const GemmParams& p, hipStream_t st) {
     const int nout = epi == EPI_GEGLU ? (p.Nreal >> 1) : p.Nreal;
-    const dim3 grid(unsigned((nout + 1023) / 1024), unsigned(p.Mreal < 65535 ? p.Mreal : 65535));
+    // one thread per (row, 4 columns), at most 16 blocks of 256 per CU (the kernel strides beyond)
+    const long long threads = (long long)p.Mreal * ((nout + 3) / 4);
+    const dim3 grid(unsigned(std::min<long long>((threads + 255) / 256, 4096)));
     switch (epi) {
     case EPI_PLAIN: hipLaunchKernelGGL(splitk_epilogue_kernel<EPI_PLAIN>, grid, dim3(256), 0, st, p); break;
     case EPI_SPLIT3: hipLaunchKernelGGL(splitk_epilogue_kernel<EPI_SPLIT3>, grid, dim3(256), 0, st, p); break;
