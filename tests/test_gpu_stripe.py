@@ -81,3 +81,10 @@ def test_stripe_c2_rows():
     c.q[1, :] = 32767
     c.q[2, ::2] = -32768
     c.check(what="stripe C2 rows")
+
+
+def test_stripe_gelu_residual():
+    """GELU with a residual (the reference adds it after the GELU, src/gemm_hl.cu:280-284) under the
+    forced variant: the row-stationary kernel adds residuals to PLAIN outputs only, so the call runs
+    on the tile kernels."""
+    Case(vg.SRC_I16, 384, 256, 320, epi=vg.EPI_GELU, seed=92, residual=True, rowmax=True, s_range=(16, 24)).check(what="stripe gelu residual")

@@ -78,8 +78,9 @@ constexpr int NCU = 256;   // MI355X compute units
 int cdiv(long long a, long long b) { return int((a + b - 1) / b); }
 
 // Variant 4 forces the row-stationary kernel (stripe_kernel.h) where it applies: int16 rows or int8
-// planes, epilogue PLAIN / GEGLU / GELU, Kp <= 320, output columns in whole groups of four and
-// 16-byte aligned output, Y extent below 2^31. Blocks of 128 rows stream 64-row W chunks.
+// planes, epilogue PLAIN (with or without a residual) / GEGLU / GELU, Kp <= 320, output columns in
+// whole groups of four and 16-byte aligned output, Y extent below 2^31. Blocks of 128 rows stream
+// 64-row W chunks.
 constexpr int VARIANT_STRIPE = 4;
 constexpr int STRIPE_BM = 128, STRIPE_CH = 64;
 constexpr int STRIPE_NCOLS = 1280;   // W rows per block, at most
@@ -87,6 +88,7 @@ constexpr int STRIPE_NCOLS = 1280;   // W rows per block, at most
 bool stripe_applies(int src, int epi, const vk::GemmParams& p) {
     if (src != VGEMM_SRC_I16 && src != VGEMM_SRC_I8) return false;
     if (epi != VGEMM_EPI_PLAIN && epi != VGEMM_EPI_GEGLU && epi != VGEMM_EPI_GELU) return false;
+    if (p.R && epi != VGEMM_EPI_PLAIN) return false;   // the kernel adds a residual to PLAIN outputs only
     if (p.Kp > 320 || !p.vec_store) return false;
     const int nout = epi == VGEMM_EPI_GEGLU ? p.Nreal / 2 : p.Nreal;
     if (nout % 4) return false;
