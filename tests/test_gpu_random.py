@@ -64,3 +64,67 @@ def test_random_case(seed):
         Case(src, M, N, K, epi=epi, seed=seed, conv=conv, **kw).check(what=what)
     finally:
         vg.set_variant(-1)
+
+
+def draw_qkv(seed):
+    r = np.random.default_rng(20_000 + seed)
+    src = int(r.choice([vg.SRC_I8, vg.SRC_I16, vg.SRC_X32]))
+    heads, T, B = int(r.integers(1, 7)), int(r.integers(1, 300)), int(r.integers(1, 4))
+    K = int(r.integers(1, 40)) * 8 * int(r.choice([1, 4]))
+    kw = dict(s_range=S_RANGES[int(r.integers(len(S_RANGES)))], m_range=M_RANGES[int(r.integers(len(M_RANGES)))])
+    if src != vg.SRC_X32 and int(r.integers(2)):
+        kw["e_max"] = int(r.integers(1, 12))
+    return src, heads, T, B, K, int(r.choice([-1, 0, 1, 2, 3, 4])), kw
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_qkv(seed):
+    from tests.test_gpu_qkv_gn import check_qkv
+
+    src, heads, T, B, K, variant, kw = draw_qkv(seed)
+    print(f"[random qkv] seed {seed}: src {src} heads {heads} T {T} B {B} K {K} variant {variant} {kw}", flush=True)
+    try:
+        check_qkv(src, heads, T, B=B, K=K, seed=seed, variant=variant, **kw)
+    finally:
+        vg.set_variant(-1)
+
+
+# (B, H, W, C, stride) with Ho * Wo a multiple of 64, for the GroupNorm sample length
+GN_CONV = [(2, 8, 8, 16, 1), (1, 16, 16, 32, 2), (3, 8, 16, 64, 1), (1, 16, 16, 64, 1), (2, 32, 8, 16, 1)]
+
+
+def draw_gn(seed):
+    r = np.random.default_rng(30_000 + seed)
+    src = int(r.choice([vg.SRC_I8, vg.SRC_I16, vg.SRC_X32, vg.SRC_CONV16, vg.SRC_CONV32]))
+    N = int(r.integers(1, 20)) * 32
+    kw = dict(s_range=S_RANGES[int(r.integers(len(S_RANGES)))], m_range=M_RANGES[int(r.integers(len(M_RANGES)))],
+              residual=bool(r.integers(2)), rowmax=bool(r.integers(2)))
+    conv = None
+    if src in (vg.SRC_CONV16, vg.SRC_CONV32):
+        conv = GN_CONV[int(r.integers(len(GN_CONV)))]
+        if src == vg.SRC_CONV32 and conv[3] % 16:
+            conv = conv[:3] + (32,) + conv[4:]
+        B, H, W, C, stride = conv
+        T = ((H - 1) // stride + 1) * ((W - 1) // stride + 1)
+        M, K = B * T, 9 * C
+    else:
+        T = 64 * int(r.integers(1, 6))
+        M = T * int(r.integers(1, 4))
+        K = int(r.integers(1, 40)) * 8 * int(r.choice([1, 4]))
+        if src != vg.SRC_X32 and int(r.integers(2)):
+            kw["e_max"] = int(r.integers(1, 12))
+    return src, M, N, K, T, conv, int(r.choice([-1, 0, 1, 2, 3, 4])), kw
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_gnstat(seed):
+    from tests.test_gpu_qkv_gn import check_gn
+
+    src, M, N, K, T, conv, variant, kw = draw_gn(seed)
+    what = f"seed {seed}: src {src} M {M} N {N} K {K} T {T} conv {conv} variant {variant} {kw}"
+    print(f"[random gn] {what}", flush=True)
+    vg.set_variant(variant)
+    try:
+        check_gn(Case(src, M, N, K, seed=seed, conv=conv, **kw), T, what)
+    finally:
+        vg.set_variant(-1)
