@@ -94,7 +94,7 @@ def roofline(ops, nbytes, seconds):
             "frac": round(achieved / PEAK_INT8_TOPS, 4)}
 
 
-def vendor_planar_us(L, stream, steps=10):
+def vendor_planar_us(L, stream, steps=10, warmup=3):
     """hipBLASLt (torch._int_mm) on the int8 GEMM of the reference's planar route for this layer:
     the stacked [hi; lo] planes [2M x K] times W^T [K x N] -> int32 (src/engine.cu:155, 195, 212,
     276), without the separate epilogue or im2col passes that route also needs. A comparison point
@@ -106,7 +106,7 @@ def vendor_planar_us(L, stream, steps=10):
         W = torch.randint(-128, 128, (L.Np, L.Kp), dtype=torch.int8, device="cuda")
         Wt = W.t()
         with torch.cuda.stream(stream):
-            return round(time_launches(lambda: torch._int_mm(A, Wt), stream, steps, 3) * 1e3, 2)
+            return round(time_launches(lambda: torch._int_mm(A, Wt), stream, steps, warmup) * 1e3, 2)
     except RuntimeError:
         return None
 
@@ -174,8 +174,10 @@ def _cpu_model():
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    # a long window: the GPU's clocks settle only after some milliseconds of sustained load, and a
+    # window of a few launches catches a transient (C2: 88 us at 20 launches, 81.5 us sustained)
+    ap.add_argument("--steps", type=int, default=1000)
+    ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--no-unet", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-configs", action="store_true")
@@ -245,7 +247,7 @@ def main():
     log(f"[bench] {L.name}: {ms * 1e3:.1f} us/launch, {tops:.1f} TOPS ({100 * tops / PEAK_INT8_TOPS:.1f}% of int8 peak)")
     traffic, traffic_src = pmc_traffic()
 
-    vendor_c2 = vendor_planar_us(L, stream)
+    vendor_c2 = vendor_planar_us(L, stream, args.steps, args.warmup)
     roof = roofline(L.ops, L.hbm_bytes, ms * 1e-3)
     roof["traffic"] = traffic
     roof.update({"traffic_source": traffic_src, "kernel": "vk::stripe_kernel<SRC_I16, EPI_GEGLU>",
@@ -279,12 +281,12 @@ def main():
             p = cf.DeviceProblem(Lc)
             p.reset()
             torch.cuda.synchronize()
-            t = time_launches(lambda: p.run(stream=stream), stream, max(5, args.steps), 3)
+            t = time_launches(lambda: p.run(stream=stream), stream, max(5, args.steps), args.warmup)
             table[Lc.name] = {"us": round(t * 1e3, 2), "tops": round(Lc.ops / (t * 1e-3) / 1e12, 2),
                               "pct_int8_peak": round(100 * Lc.ops / (t * 1e-3) / 1e12 / PEAK_INT8_TOPS, 2),
                               "gbs_algorithmic": round(Lc.hbm_bytes / (t * 1e-3) / 1e9, 1),
                               "roofline": roofline(Lc.ops, Lc.hbm_bytes, t * 1e-3)}
-            table[Lc.name]["hipblaslt_planar_gemm_us"] = vendor_planar_us(Lc, stream)
+            table[Lc.name]["hipblaslt_planar_gemm_us"] = vendor_planar_us(Lc, stream, max(5, args.steps), args.warmup)
             if not args.no_cpu:
                 table[Lc.name]["cpu_ms"] = round(cpu_time(Lc, p.h, 3) * 1e3, 2)
             log(f"[bench] {Lc.name}: {table[Lc.name]}")
@@ -298,7 +300,7 @@ def main():
         log("[bench] C5: building the 194-GEMM UNet set")
         gs = GemmSet()
         gs.capture(reseed=False)   # GEMMs + rowmax fills only: no residual re-seeding copies
-        t = time_launches(gs.replay, gs.stream, max(5, args.steps // 2), 2)
+        t = time_launches(gs.replay, gs.stream, max(5, min(100, args.steps // 2)), max(2, min(10, args.warmup // 20)))
         out["unet_gemm_set_ms"] = round(t, 4)
         out["unet_gemm_set"] = {"gemms": len(gs.layers), "ms": round(t, 4), "tops": round(gs.ops / (t * 1e-3) / 1e12, 2),
                                 "pct_int8_peak": round(100 * gs.ops / (t * 1e-3) / 1e12 / PEAK_INT8_TOPS, 2),
