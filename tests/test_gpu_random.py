@@ -51,19 +51,24 @@ def draw(seed):
         kw["residual"] = epi != vg.EPI_GEGLU and bool(r.integers(2))
     if src in (vg.SRC_I8, vg.SRC_I16) and int(r.integers(2)):
         kw["e_max"] = int(r.integers(1, 12))
-    return src, epi, variant, M, N, K, conv, kw
+    splitk = int(r.choice([0, 0, 0, 2, 3, 5]))   # forced K splits (with a workspace), 0: none
+    return src, epi, variant, M, N, K, conv, kw, splitk
 
 
 @pytest.mark.parametrize("seed", range(128))
 def test_random_case(seed):
-    src, epi, variant, M, N, K, conv, kw = draw(seed)
-    what = f"seed {seed}: src {src} epi {epi} variant {variant} M {M} N {N} K {K} conv {conv} {kw}"
+    src, epi, variant, M, N, K, conv, kw, splitk = draw(seed)
+    what = f"seed {seed}: src {src} epi {epi} variant {variant} splitk {splitk} M {M} N {N} K {K} conv {conv} {kw}"
     print(f"[random] {what}", flush=True)
     vg.set_variant(variant)
+    vg.set_splitk(splitk)
     try:
-        Case(src, M, N, K, epi=epi, seed=seed, conv=conv, **kw).check(what=what)
+        c = Case(src, M, N, K, epi=epi, seed=seed, conv=conv, **kw)
+        ws = vg.workspace_bytes(c.Mp, M, c.Np, N, c.Kp, epi) if splitk else 0
+        c.check(ws_bytes=ws, what=what)
     finally:
         vg.set_variant(-1)
+        vg.set_splitk(0)
 
 
 def draw_qkv(seed):
