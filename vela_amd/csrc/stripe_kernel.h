@@ -67,6 +67,10 @@ constexpr unsigned STRIPE_LUT_RAW = 8192;
 
 enum { FORM_INT = 0, FORM_EXACT = 1 };
 
+#ifndef EB_GEGLU
+#define EB_GEGLU 4
+#endif
+
 template <int SRC, int EPI>
 __global__ void __launch_bounds__(256, 2) stripe_kernel(const GemmParams p) {
     using S = StripeCfg;
@@ -75,6 +79,7 @@ __global__ void __launch_bounds__(256, 2) stripe_kernel(const GemmParams p) {
     constexpr bool GEGLU = EPI == EPI_GEGLU;
     constexpr int NOUT = GEGLU ? 1 : S::NSUB;  // output subtiles per chunk
     constexpr int STORES = NOUT * 16;          // output stores per lane per chunk
+    constexpr int EB = GEGLU ? EB_GEGLU : 16;  // epilogue elements computed together
     static_assert(SRC == SRC_I16 || SRC == SRC_I8, "stripe sources");
     static_assert(EPI == EPI_PLAIN || EPI == EPI_GEGLU || EPI == EPI_GELU, "stripe epilogues");
 
@@ -374,37 +379,63 @@ __global__ void __launch_bounds__(256, 2) stripe_kernel(const GemmParams p) {
             if (form == FORM_INT) {
                 const int4 ka = sh.tab[tb + 32 * u + lc];
                 const int4 kg = sh.tab[tb + (GEGLU ? 32 : 32 * u) + lc];
+                // GEGLU of element i; hi = the high word of the 64-bit product a ge + 2^15
+                auto geglu = [&](int i, unsigned& hi) -> int {
+                    const int ya = req((acc_h[0][i] << 8) + acc_l[0][i], ka);
+                    const int yg = req((acc_h[1][i] << 8) + acc_l[1][i], kg);
+                    unsigned h0;
+                    const int ge = mulsh16(yg, phi(yg), h0);
+                    return mulsh16(ya, ge, hi);
+                };
                 auto run = [&](auto hasr, auto rmax) {
                     constexpr bool HASR = decltype(hasr)::value, RMAX = decltype(rmax)::value;
+                    // EB elements at a time: their values first, with no branch between them, so
+                    // that their dependency chains (64-bit products, table lookups) interleave; then
+                    // their stores
 #pragma unroll
-                    for (int i = 0; i < 16; ++i) {
-                        const unsigned voff = vbase + unsigned(8 * (i >> 2) + (i & 3)) * ldy4;
-                        const int ya = req((acc_h[u][i] << 8) + acc_l[u][i], ka);
-                        int y;
-                        if constexpr (GEGLU) {
-                            const int yg = req((acc_h[1][i] << 8) + acc_l[1][i], kg);
-                            unsigned h0, hi;
-                            const int ge = mulsh16(yg, phi(yg), h0);
-                            y = mulsh16(ya, ge, hi);
-                            // |a ge| >= 2^47: the result saturates. A wave-uniform branch, rarely taken;
-                            // the empty asm keeps the test on the high word and the branch a branch.
-                            asm volatile("" : "+v"(hi));
-                            const bool ovf = hi + 32768u > 65535u;
-                            if (__builtin_amdgcn_ballot_w64(ovf)) {
-                                asm volatile("; saturating GEGLU product");
-                                y = ovf ? (int(hi) >> 31) ^ 0x7fffffff : y;
+                    for (int i0 = 0; i0 < 16; i0 += EB) {
+                        int yv[EB];
+                        unsigned hv[GEGLU ? EB : 1];
+                        unsigned ov = 0;   // OR of hi + 2^15 over the elements: > 65535 iff one overflows
+#pragma unroll
+                        for (int j = 0; j < EB; ++j) {
+                            const int i = i0 + j;
+                            if constexpr (GEGLU) {
+                                yv[j] = geglu(i, hv[j]);
+                                // opaque to the compiler, so that the tests below stay on the 32-bit
+                                // high word (not on a 64-bit product kept alive for them)
+                                asm volatile("" : "+v"(hv[j]));
+                                ov |= hv[j] + 32768u;
+                            } else if constexpr (EPI == EPI_GELU) {
+                                const int ya = req((acc_h[u][i] << 8) + acc_l[u][i], ka);
+                                unsigned h0;
+                                yv[j] = mulsh16(ya, phi(ya), h0);
+                            } else {
+                                yv[j] = req((acc_h[u][i] << 8) + acc_l[u][i], ka);
                             }
-                        } else if constexpr (EPI == EPI_GELU) {
-                            unsigned h0;
-                            y = mulsh16(ya, phi(ya), h0);
-                        } else {
-                            y = ya;
                         }
-                        if constexpr (HASR) y = add_sat(y, int(__builtin_amdgcn_raw_buffer_load_b32(rR, int(voff), 0, 0)));
-                        __builtin_amdgcn_raw_buffer_store_b32(y, rY, int(voff), 0, 0);
-                        // max(y, -y) is |y| as an unsigned value, also for INT_MIN. Columns past the
-                        // output have m = s = C = 0 in the table and zero W rows, so their y is 0.
-                        if constexpr (RMAX) yabs[i] = int(max(unsigned(yabs[i]), unsigned(max(y, int(0u - unsigned(y))))));
+                        if constexpr (GEGLU) {
+                            // |a ge| >= 2^47 for an element of the wave: that result saturates. Rarely
+                            // taken; the overflowing elements are replaced.
+                            if (__builtin_amdgcn_ballot_w64(ov > 65535u)) {
+                                asm volatile("; saturating GEGLU product");
+#pragma unroll
+                                for (int j = 0; j < EB; ++j)
+                                    if (hv[j] + 32768u > 65535u) yv[j] = (int(hv[j]) >> 31) ^ 0x7fffffff;
+                            }
+                        }
+#pragma unroll
+                        for (int j = 0; j < EB; ++j) {
+                            const int i = i0 + j;
+                            const unsigned voff = vbase + unsigned(8 * (i >> 2) + (i & 3)) * ldy4;
+                            int y = yv[j];
+                            if constexpr (HASR) y = add_sat(y, int(__builtin_amdgcn_raw_buffer_load_b32(rR, int(voff), 0, 0)));
+                            __builtin_amdgcn_raw_buffer_store_b32(y, rY, int(voff), 0, 0);
+                            // max(y, -y) is |y| as an unsigned value, also for INT_MIN. Columns past the
+                            // output have m = s = C = 0 in the table and zero W rows, so their y is 0.
+                            if constexpr (RMAX) yabs[i] = int(max(unsigned(yabs[i]), unsigned(max(y, int(0u - unsigned(y))))));
+                        }
+                        __builtin_amdgcn_sched_barrier(0);   // batches do not mix (register pressure)
                     }
                 };
                 if (EPI == EPI_PLAIN && p.R) {
