@@ -49,6 +49,7 @@ struct StripeCfg {
     static constexpr int NCOLS = 1280;              // W rows (table columns) per block, at most
     static constexpr int CPT = NCOLS / 256;         // table columns per thread
     static constexpr int DMA_INS = STAGE / 1024 / 4;// DMA instructions per wave per chunk
+    static constexpr int EB_GEGLU = 4;              // GEGLU outputs computed together (8: spills)
     static_assert(STAGE % 4096 == 0, "stripe geometry");
 };
 
@@ -67,10 +68,6 @@ constexpr unsigned STRIPE_LUT_RAW = 8192;
 
 enum { FORM_INT = 0, FORM_EXACT = 1 };
 
-#ifndef EB_GEGLU
-#define EB_GEGLU 4
-#endif
-
 template <int SRC, int EPI>
 __global__ void __launch_bounds__(256, 2) stripe_kernel(const GemmParams p) {
     using S = StripeCfg;
@@ -79,7 +76,7 @@ __global__ void __launch_bounds__(256, 2) stripe_kernel(const GemmParams p) {
     constexpr bool GEGLU = EPI == EPI_GEGLU;
     constexpr int NOUT = GEGLU ? 1 : S::NSUB;  // output subtiles per chunk
     constexpr int STORES = NOUT * 16;          // output stores per lane per chunk
-    constexpr int EB = GEGLU ? EB_GEGLU : 16;  // epilogue elements computed together
+    constexpr int EB = GEGLU ? S::EB_GEGLU : 16;  // epilogue elements computed together
     static_assert(SRC == SRC_I16 || SRC == SRC_I8, "stripe sources");
     static_assert(EPI == EPI_PLAIN || EPI == EPI_GEGLU || EPI == EPI_GELU, "stripe epilogues");
 
