@@ -310,6 +310,13 @@ __global__ void __launch_bounds__(256, 2) stripe_kernel(const GemmParams p) {
         hi = unsigned(u64(t) >> 32);
         return int(__builtin_amdgcn_alignbit(hi, unsigned(u64(t)), 16));
     };
+    // the same with 2^47 added to the rounding constant: returns y ^ 2^31 (y biased to unsigned order)
+    // and hi = (high word of a b + 2^15) + 2^15, which is <= 65535 exactly when y fits in int32
+    auto mulsh16b = [&](int a, int b, unsigned& hi) -> unsigned {
+        const i64 t = i64(a) * i64(b) + (32768 + (1LL << 47));
+        hi = unsigned(u64(t) >> 32);
+        return __builtin_amdgcn_alignbit(hi, unsigned(u64(t)), 16);
+    };
     // the integer requantisation (A m + C) >> s of an element, exact when it fits in int32
     auto req = [&](int A, const int4& k) -> int {
         const i64 t = i64(A) * i64(k.x) + i64((u64(unsigned(k.w)) << 32) | unsigned(k.z));
@@ -376,33 +383,39 @@ __global__ void __launch_bounds__(256, 2) stripe_kernel(const GemmParams p) {
             if (form == FORM_INT) {
                 const int4 ka = sh.tab[tb + 32 * u + lc];
                 const int4 kg = sh.tab[tb + (GEGLU ? 32 : 32 * u) + lc];
-                // GEGLU of element i; hi = the high word of the 64-bit product a ge + 2^15
-                auto geglu = [&](int i, unsigned& hi) -> int {
+                // GEGLU of element i, biased (y ^ 2^31); hi = the high word of a ge + 2^15, plus 2^15
+                auto geglu = [&](int i, unsigned& hi) -> unsigned {
                     const int ya = req((acc_h[0][i] << 8) + acc_l[0][i], ka);
                     const int yg = req((acc_h[1][i] << 8) + acc_l[1][i], kg);
                     unsigned h0;
                     const int ge = mulsh16(yg, phi(yg), h0);
-                    return mulsh16(ya, ge, hi);
+                    return mulsh16b(ya, ge, hi);
                 };
-                auto run = [&](auto hasr, auto rmax) {
+                // FULL: every row of the block is below Mreal. Then a store's row offset (uniform)
+                // goes in the instruction's scalar offset and its vector offset is the lane's base:
+                // in range exactly when the column is (OOB otherwise), whether or not the hardware
+                // range check counts the scalar offset. Otherwise each element's full offset is in
+                // the vector offset, so that rows at or past Mreal fall outside the buffer.
+                auto run = [&](auto hasr, auto rmax, auto full) {
                     constexpr bool HASR = decltype(hasr)::value, RMAX = decltype(rmax)::value;
+                    constexpr bool FULL = decltype(full)::value;
                     // EB elements at a time: their values first, with no branch between them, so
                     // that their dependency chains (64-bit products, table lookups) interleave; then
                     // their stores
 #pragma unroll
                     for (int i0 = 0; i0 < 16; i0 += EB) {
-                        int yv[EB];
+                        int yv[EB];        // GEGLU: biased, y ^ 2^31
                         unsigned hv[GEGLU ? EB : 1];
-                        unsigned ov = 0;   // OR of hi + 2^15 over the elements: > 65535 iff one overflows
+                        unsigned ov = 0;   // OR of the biased high words: > 65535 iff one overflows
 #pragma unroll
                         for (int j = 0; j < EB; ++j) {
                             const int i = i0 + j;
                             if constexpr (GEGLU) {
-                                yv[j] = geglu(i, hv[j]);
+                                yv[j] = int(geglu(i, hv[j]));
                                 // opaque to the compiler, so that the tests below stay on the 32-bit
                                 // high word (not on a 64-bit product kept alive for them)
                                 asm volatile("" : "+v"(hv[j]));
-                                ov |= hv[j] + 32768u;
+                                ov |= hv[j];
                             } else if constexpr (EPI == EPI_GELU) {
                                 const int ya = req((acc_h[u][i] << 8) + acc_l[u][i], ka);
                                 unsigned h0;
@@ -416,31 +429,49 @@ __global__ void __launch_bounds__(256, 2) stripe_kernel(const GemmParams p) {
                             // taken; the overflowing elements are replaced.
                             if (__builtin_amdgcn_ballot_w64(ov > 65535u)) {
                                 asm volatile("; saturating GEGLU product");
+                                // the sign of the product is the sign bit of the biased high word;
+                                // the biased saturated value is ~0 (INT_MAX) or 0 (INT_MIN)
 #pragma unroll
                                 for (int j = 0; j < EB; ++j)
-                                    if (hv[j] + 32768u > 65535u) yv[j] = (int(hv[j]) >> 31) ^ 0x7fffffff;
+                                    if (hv[j] > 65535u) yv[j] = ~(int(hv[j]) >> 31);
                             }
                         }
 #pragma unroll
                         for (int j = 0; j < EB; ++j) {
                             const int i = i0 + j;
-                            const unsigned voff = vbase + unsigned(8 * (i >> 2) + (i & 3)) * ldy4;
-                            int y = yv[j];
-                            if constexpr (HASR) y = add_sat(y, int(__builtin_amdgcn_raw_buffer_load_b32(rR, int(voff), 0, 0)));
-                            __builtin_amdgcn_raw_buffer_store_b32(y, rY, int(voff), 0, 0);
-                            // max(y, -y) is |y| as an unsigned value, also for INT_MIN. Columns past the
-                            // output have m = s = C = 0 in the table and zero W rows, so their y is 0.
-                            if constexpr (RMAX) yabs[i] = int(max(unsigned(yabs[i]), unsigned(max(y, int(0u - unsigned(y))))));
+                            const unsigned soff = unsigned(8 * (i >> 2) + (i & 3)) * ldy4;
+                            const unsigned voff = FULL ? vbase : vbase + soff;
+                            const int sgo = FULL ? int(soff) : 0;
+                            int y = GEGLU ? int(unsigned(yv[j]) ^ 0x80000000u) : yv[j];
+                            if constexpr (HASR) y = add_sat(y, int(__builtin_amdgcn_raw_buffer_load_b32(rR, int(voff), sgo, 0)));
+                            __builtin_amdgcn_raw_buffer_store_b32(y, rY, int(voff), sgo, 0);
+                            // Columns past the output have m = s = C = 0 in the table and zero W rows,
+                            // so their y is 0.
+                            if constexpr (RMAX) {
+                                unsigned ay;
+                                if constexpr (GEGLU) {
+                                    // |y| = |(y ^ 2^31) - 2^31| as an unsigned difference, also for INT_MIN
+                                    asm("v_sad_u32 %0, %1, %2, 0" : "=v"(ay) : "v"(yv[j]), "s"(0x80000000u));
+                                } else {
+                                    // max(y, -y) is |y| as an unsigned value, also for INT_MIN
+                                    ay = unsigned(max(y, int(0u - unsigned(y))));
+                                }
+                                yabs[i] = int(max(unsigned(yabs[i]), ay));
+                            }
                         }
                         __builtin_amdgcn_sched_barrier(0);   // batches do not mix (register pressure)
                     }
                 };
+                auto run_rows = [&](auto hasr, auto rmax) {
+                    if (m0 + BM <= p.Mreal) run(hasr, rmax, std::true_type{});
+                    else run(hasr, rmax, std::false_type{});
+                };
                 if (EPI == EPI_PLAIN && p.R) {
-                    if (p.rowmax) run(std::true_type{}, std::true_type{});
-                    else run(std::true_type{}, std::false_type{});
+                    if (p.rowmax) run_rows(std::true_type{}, std::true_type{});
+                    else run_rows(std::true_type{}, std::false_type{});
                 } else {
-                    if (p.rowmax) run(std::false_type{}, std::true_type{});
-                    else run(std::false_type{}, std::false_type{});
+                    if (p.rowmax) run_rows(std::false_type{}, std::true_type{});
+                    else run_rows(std::false_type{}, std::false_type{});
                 }
             } else {
                 // the reference's int64 formula, one element per iteration (its row maximum goes
