@@ -88,3 +88,25 @@ def test_stripe_gelu_residual():
     forced variant: the row-stationary kernel adds residuals to PLAIN outputs only, so the call runs
     on the tile kernels."""
     Case(vg.SRC_I16, 384, 256, 320, epi=vg.EPI_GELU, seed=92, residual=True, rowmax=True, s_range=(16, 24)).check(what="stripe gelu residual")
+
+
+@pytest.mark.parametrize("src", [vg.SRC_I16, vg.SRC_I8])
+def test_stripe_geglu_saturating_integer_form(src):
+    """The integer form's saturating GEGLU products (|a ge| >= 2^47 while a and g themselves fit in
+    int32, so the block keeps the integer form), both signs, in full and partial row stripes (M = 300:
+    two full stripes of 128 rows and one of 44), with the row maximum."""
+    c = Case(src, 300, 256, 64, epi=vg.EPI_GEGLU, seed=93, rowmax=True, s_range=(16, 16),
+             m_range=(1 << 17, 1 << 18), b_range=(-1000, 1000))
+    if src == vg.SRC_I16:
+        c.q[::7, :] = 32767
+        c.q[3::7, :] = -32768
+    else:
+        c.hi[:300:7, :] = 127
+        c.lo[:300:7, :] = 127
+        c.hi[3:300:7, :] = -128
+        c.lo[3:300:7, :] = -128
+    want, _ = c.reference()
+    imax, imin = np.iinfo(np.int32).max, np.iinfo(np.int32).min
+    for rows in (slice(0, 256), slice(256, 300)):
+        assert (want[rows] == imax).any() and (want[rows] == imin).any(), "the case must saturate both ways"
+    c.check(what=f"stripe saturating GEGLU {src}")
