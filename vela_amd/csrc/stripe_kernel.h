@@ -28,8 +28,9 @@
 // only vector-memory instructions after it in chunk c are that chunk's output stores, a fixed
 // number per lane (every lane stores unconditionally; rows and columns outside the output go to
 // an out-of-range buffer offset, which the hardware drops). So waiting for at most that many
-// outstanding operations completes the DMA. Blocks whose epilogue loads from memory (residual, the
-// int64 form) wait for all of them instead.
+// outstanding operations completes the DMA. Residual loads (integer form) are consumed before the
+// chunk's last stores, so they do not change that count; blocks of the int64 form, whose epilogue
+// loads from memory element by element, wait for all operations instead.
 #pragma once
 #include <type_traits>
 
@@ -68,7 +69,9 @@ constexpr unsigned STRIPE_LUT_RAW = 8192;
 
 enum { FORM_INT = 0, FORM_EXACT = 1 };
 
-template <int SRC, int EPI>
+// RES: the PLAIN instantiation for calls with a residual (its own kernel, so that the residual
+// loads do not shape the code of the others)
+template <int SRC, int EPI, bool RES = false>
 __global__ void __launch_bounds__(256, 2) stripe_kernel(const GemmParams p) {
     using S = StripeCfg;
     constexpr int CH = S::CH, NKS = S::NKS, BM = S::BM;
@@ -79,6 +82,7 @@ __global__ void __launch_bounds__(256, 2) stripe_kernel(const GemmParams p) {
     constexpr int EB = GEGLU ? S::EB_GEGLU : 16;  // epilogue elements computed together
     static_assert(SRC == SRC_I16 || SRC == SRC_I8, "stripe sources");
     static_assert(EPI == EPI_PLAIN || EPI == EPI_GEGLU || EPI == EPI_GELU, "stripe epilogues");
+    static_assert(!RES || EPI == EPI_PLAIN, "residual: PLAIN only");
 
     __shared__ __attribute__((aligned(16))) StripeShared<NEEDLUT> sh;
 
@@ -295,7 +299,9 @@ __global__ void __launch_bounds__(256, 2) stripe_kernel(const GemmParams p) {
     v16i yabs;
 #pragma unroll
     for (int i = 0; i < 16; ++i) yabs[i] = 0;
-    const bool lean = form == FORM_INT && !p.R;   // the epilogue issues stores only
+    // the integer form's epilogue issues a fixed number of stores per chunk, and residual loads that
+    // it consumes before the chunk's last stores
+    const bool lean = form == FORM_INT && (RES || !p.R);
     const bool lut_lds = NEEDLUT && !sh.flag[5];  // the expanded table in LDS is valid (0 <= L <= 65536)
 
     // phi(x) for tables with 0 <= L <= 65536: x clamped to [-2^20 - 1, 2^20], entry (x >> 10) + 1025
@@ -405,6 +411,16 @@ __global__ void __launch_bounds__(256, 2) stripe_kernel(const GemmParams p) {
 #pragma unroll
                     for (int i0 = 0; i0 < 16; i0 += EB) {
                         int yv[EB];        // GEGLU: biased, y ^ 2^31
+                        int rv[HASR ? EB : 1];
+                        if constexpr (HASR) {
+                            // the batch's residuals first, so that their latency hides behind its arithmetic
+#pragma unroll
+                            for (int j = 0; j < EB; ++j) {
+                                const int i = i0 + j;
+                                const unsigned soff = unsigned(8 * (i >> 2) + (i & 3)) * ldy4;
+                                rv[j] = int(__builtin_amdgcn_raw_buffer_load_b32(rR, int(FULL ? vbase : vbase + soff), FULL ? int(soff) : 0, 0));
+                            }
+                        }
                         unsigned hv[GEGLU ? EB : 1];
                         unsigned ov = 0;   // OR of the biased high words: > 65535 iff one overflows
 #pragma unroll
@@ -443,7 +459,7 @@ __global__ void __launch_bounds__(256, 2) stripe_kernel(const GemmParams p) {
                             const unsigned voff = FULL ? vbase : vbase + soff;
                             const int sgo = FULL ? int(soff) : 0;
                             int y = GEGLU ? int(unsigned(yv[j]) ^ 0x80000000u) : yv[j];
-                            if constexpr (HASR) y = add_sat(y, int(__builtin_amdgcn_raw_buffer_load_b32(rR, int(voff), sgo, 0)));
+                            if constexpr (HASR) y = add_sat(y, rv[j]);
                             __builtin_amdgcn_raw_buffer_store_b32(y, rY, int(voff), sgo, 0);
                             // Columns past the output have m = s = C = 0 in the table and zero W rows,
                             // so their y is 0.
@@ -466,7 +482,7 @@ __global__ void __launch_bounds__(256, 2) stripe_kernel(const GemmParams p) {
                     if (m0 + BM <= p.Mreal) run(hasr, rmax, std::true_type{});
                     else run(hasr, rmax, std::false_type{});
                 };
-                if (EPI == EPI_PLAIN && p.R) {
+                if constexpr (RES) {
                     if (p.rowmax) run_rows(std::true_type{}, std::true_type{});
                     else run_rows(std::true_type{}, std::false_type{});
                 } else {
@@ -523,7 +539,10 @@ template <int SRC>
 hipError_t launch_stripe_t(int epi, const GemmParams& p, hipStream_t st) {
     const dim3 grid(unsigned(p.mtiles * p.ntiles));
     switch (epi) {
-    case EPI_PLAIN: hipLaunchKernelGGL((stripe_kernel<SRC, EPI_PLAIN>), grid, dim3(256), 0, st, p); break;
+    case EPI_PLAIN:
+        if (p.R) hipLaunchKernelGGL((stripe_kernel<SRC, EPI_PLAIN, true>), grid, dim3(256), 0, st, p);
+        else hipLaunchKernelGGL((stripe_kernel<SRC, EPI_PLAIN>), grid, dim3(256), 0, st, p);
+        break;
     case EPI_GEGLU: hipLaunchKernelGGL((stripe_kernel<SRC, EPI_GEGLU>), grid, dim3(256), 0, st, p); break;
     case EPI_GELU: hipLaunchKernelGGL((stripe_kernel<SRC, EPI_GELU>), grid, dim3(256), 0, st, p); break;
     default: return hipErrorInvalidValue;
