@@ -151,8 +151,6 @@ def cpu_baseline(L, h, unet_fraction=4):
         t_all = time.perf_counter()
         for Lu in cf.unet_layers():
             hu = cf.make_host(Lu)
-            if Lu.meta.get("conv_in"):
-                hu = cf.unet_conv_in_operand(Lu, hu)
             r1 = max(1, -(-Lu.M // unet_fraction))
             total += cpu_time(Lu, hu, 1, rows=(0, r1)) * Lu.M / r1
         out["unet_gemm_set_ms"] = round(total * 1e3, 1)

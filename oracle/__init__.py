@@ -71,6 +71,9 @@ _SIGS = {
     "orc_prep_weight": (None, [P, I, I, I, P, P, P, I, I, P, P]),
     "orc_interleave2": (None, [P, P, P, P, I, I, P, P]),
     "orc_gn_accumulate": (None, [P, I, I, I, I, P, P, P]),
+    "orc_gn_ref_tile": (None, [I, I, I, I, P, P]),
+    "orc_gn_tiles": (None, [P, I, I, I, I, I, I, P, P, P]),
+    "orc_gn_blocks": (None, [P, I, I, I, I, P, P, P]),
     "orc_qkv_heads": (None, [P, I, I, I, I, I, I, I] + [P] * 13),
 }
 
@@ -297,6 +300,40 @@ def gn_stats(Y, M, N, T, ldy=None):
     return {"sum": s, "mn": mn.astype(np.int64), "mx": mx.astype(np.int64)}
 
 
+def _gn_records(M, T):
+    cnt = (M + T - 1) // T * 32
+    return np.zeros(cnt, np.int64), np.full(cnt, 2**31 - 1, np.int32), np.full(cnt, -(2**31), np.int32)
+
+
+def gn_ref_tile(Mp, Np, Kp, src):
+    """(BMr, BNr): the reference's fused-GEMM tile for these padded sizes (src/gemm_hl.cu:352-358);
+    src is a GemmSrc code (SRC_I8 = 0 and the int16 rows SRC_I16 = 3 count as int8 planes)."""
+    bm, bn = ctypes.c_int(), ctypes.c_int()
+    lib().orc_gn_ref_tile(Mp, Np, Kp, 1 if src in (0, 3) else 0, ctypes.addressof(bm), ctypes.addressof(bn))
+    return bm.value, bn.value
+
+
+def gn_stats_fused(Y, M, N, T, Mp, Np, Kp, src, ldy=None, tile=None):
+    """GroupNorm records of a fused GEMM's EPI_PLAIN output by the reference's per-tile flush rule
+    (fresh records): dict of int64 arrays [ceil(M / T) * 32]."""
+    Y = np.ascontiguousarray(Y, np.int32)
+    ldy = ldy or Y.shape[1]
+    bm, bn = tile or gn_ref_tile(Mp, Np, Kp, src)
+    s, mn, mx = _gn_records(M, T)
+    lib().orc_gn_tiles(a(Y), M, N, ldy, T, bm, bn, a(s), a(mn), a(mx))
+    return {"sum": s, "mn": mn.astype(np.int64), "mx": mx.astype(np.int64)}
+
+
+def gn_stats_planar(Y, M, N, T, ldy=None):
+    """GroupNorm records of k_epilogue's output by the reference's per-1024-element flush rule
+    (fresh records): dict of int64 arrays [ceil(M / T) * 32]."""
+    Y = np.ascontiguousarray(Y, np.int32)
+    ldy = ldy or Y.shape[1]
+    s, mn, mx = _gn_records(M, T)
+    lib().orc_gn_blocks(a(Y), M, N, ldy, T, a(s), a(mn), a(mx))
+    return {"sum": s, "mn": mn.astype(np.int64), "mx": mx.astype(np.int64)}
+
+
 def qkv_heads(Y, M, C, heads, T, TpQ, TpK, fill=0x5A):
     """EPI_QKV outputs from the plain output Y [M x 3C]. Buffers start filled with `fill` bytes (rows
     t >= T are left so). Returns dict: q/k -> (hi, lo [B*heads*Tp x 64], e, hs, ls, ts), v -> [M x C]."""
@@ -347,6 +384,12 @@ def layer_reference(L, h, rows=None, seed_y=None):
               Y=Y, ldy=nout, residual=Y if L.residual else None, rowmax=rowmax, rows=rows)
     if L.src == SRC_CONV16:
         gemm(SRC_CONV16, img=h["img"], H=L.H, W=L.W, C=L.C, stride=L.stride, **kw)
+    elif L.kind == "conv_in":
+        # k_pixmax + k_im2col3, then the GEMM on the planes (src/engine.cu:254-280)
+        pm = pixmax(h["img32"].reshape(-1, L.C), L.B * L.H * L.W, L.C)
+        hi, lo, e = im2col3(h["img32"], pm, L.B, L.H, L.W, L.C, L.stride, L.Kp)
+        kw["e"] = e
+        gemm(SRC_I8, hi=hi, lo=lo, **kw)
     else:
         gemm(SRC_I16, q16=h["a"], K=h["a"].shape[1], **kw)
     return Y, rowmax

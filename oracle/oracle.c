@@ -256,10 +256,10 @@ void orc_epilogue_geglu_q(const int32_t* Chi, const int32_t* Clo, int M, int F, 
     }
 }
 
-/* GroupNorm statistics of an epilogue's output (EPI_PLAIN): src/gemm_hl.cu:285-287, 306-309 and
- * src/kernels.cu:63-95. Every y[r][n] of the (post-residual) output is added to record
+/* Exact GroupNorm statistics of an output (no flush rule): every y[r][n] is added to record
  * (r / T) * 32 + n / (N / 32): sum += y, mn = min(mn, y), mx = max(mx, y). The records are
- * accumulated into, as the reference's atomics do after k_gn_init. */
+ * accumulated into, as the reference's atomics do after k_gn_init. This is what the reference's
+ * statistics reduce to when no tile's group is saturated through (see orc_gn_tiles). */
 void orc_gn_accumulate(const int32_t* Y, int M, int N, int ldy, int T, int64_t* sum, int32_t* mn, int32_t* mx) {
     const int cg = N / 32;
     for (int r = 0; r < M; ++r) {
@@ -271,6 +271,83 @@ void orc_gn_accumulate(const int32_t* Y, int M, int N, int ldy, int T, int64_t* 
             if (y < mn[k]) mn[k] = y;
             if (y > mx[k]) mx[k] = y;
         }
+    }
+}
+
+/* Fold the statistics of one region (a tile or a block) into a record by the reference's flush
+ * rule: the region's (sum, min, max) of a group are added only when its min is not INT_MAX, so a
+ * region whose values of that group are all INT_MAX (or that holds none) adds nothing
+ * (src/gemm_hl.cu:306-309, src/kernels.cu:67-68). */
+static void gn_flush_region(int64_t rsum, int32_t rmn, int32_t rmx, int64_t* sum, int32_t* mn, int32_t* mx) {
+    if (rmn == INT32_MAX) return;
+    *sum += rsum;
+    if (rmn < *mn) *mn = rmn;
+    if (rmx > *mx) *mx = rmx;
+}
+
+/* The tile the reference's fused GEMM runs for these padded sizes, which is the region its
+ * GroupNorm statistics are flushed by (src/gemm_hl.cu:352-358 with g_gemm_hl_variant = -1): for
+ * Kp >= 2048 the 64x128 tile when Np % 128 == 0, else the 128x64 tile when Mp % 128 == 0 and the
+ * source is the int8 planes; otherwise 64x64. src8 = 1 for int8-plane sources (SRC_I8, and the int16
+ * rows that hold the same bytes), 0 for the sources quantised on load (SRC_X32, SRC_CONV32). */
+void orc_gn_ref_tile(int Mp, int Np, int Kp, int src8, int* BMr, int* BNr) {
+    int v = 0;
+    if (Kp >= 2048) v = Np % 128 == 0 ? 2 : (Mp % 128 == 0 ? 1 : 0);
+    if (v == 1 && Mp % 128) v = 0;
+    if (v == 2 && Np % 128) v = 0;
+    if (!src8 && v == 1) v = 0;
+    *BMr = v == 1 ? 128 : 64;
+    *BNr = v == 2 ? 128 : 64;
+}
+
+/* GroupNorm statistics of the fused GEMM's EPI_PLAIN output (src/gemm_hl.cu:175-177, 285-287,
+ * 306-309): each BMr x BNr tile (rows m0 = i*BMr, columns n0 = j*BNr) gathers, per group
+ * n / (N / 32), the sum, min and max of its outputs with r < M, n < N, and flushes them into record
+ * (m0 / T) * 32 + group by the rule above. The whole tile goes to the sample of its first row, as
+ * in the reference. */
+void orc_gn_tiles(const int32_t* Y, int M, int N, int ldy, int T, int BMr, int BNr, int64_t* sum, int32_t* mn, int32_t* mx) {
+    const int cg = N / 32;
+    for (int m0 = 0; m0 < M; m0 += BMr) {
+        const int b = m0 / T;
+        for (int n0 = 0; n0 < N; n0 += BNr) {
+            int64_t s[32];
+            int32_t lo[32], hi[32];
+            for (int g = 0; g < 32; ++g) { s[g] = 0; lo[g] = INT32_MAX; hi[g] = INT32_MIN; }
+            for (int r = m0; r < m0 + BMr && r < M; ++r)
+                for (int n = n0; n < n0 + BNr && n < N; ++n) {
+                    const int32_t y = Y[(size_t)r * ldy + n];
+                    const int g = n / cg;
+                    s[g] += y;
+                    if (y < lo[g]) lo[g] = y;
+                    if (y > hi[g]) hi[g] = y;
+                }
+            for (int g = 0; g < 32; ++g) gn_flush_region(s[g], lo[g], hi[g], sum + b * 32 + g, mn + b * 32 + g, mx + b * 32 + g);
+        }
+    }
+}
+
+/* GroupNorm statistics of the planar epilogue k_epilogue (src/kernels.cu:70-95, 732-736): the output
+ * [M x N] (N % 4 == 0) is cut into blocks of 1024 consecutive elements in row-major order (element
+ * r * N + n); each block gathers per group n / (N / 32) the sum, min and max of its elements and
+ * flushes them by the rule above into record (first row of the block / T) * 32 + group. With
+ * (T * N) % 1024 == 0 no block holds two samples. */
+void orc_gn_blocks(const int32_t* Y, int M, int N, int ldy, int T, int64_t* sum, int32_t* mn, int32_t* mx) {
+    const int cg = N / 32;
+    const int64_t total = (int64_t)M * N;
+    for (int64_t e0 = 0; e0 < total; e0 += 1024) {
+        const int b = (int)((e0 / N) / T);
+        int64_t s[32];
+        int32_t lo[32], hi[32];
+        for (int g = 0; g < 32; ++g) { s[g] = 0; lo[g] = INT32_MAX; hi[g] = INT32_MIN; }
+        for (int64_t i = e0; i < e0 + 1024 && i < total; ++i) {
+            const int r = (int)(i / N), n = (int)(i % N);
+            const int32_t y = Y[(size_t)r * ldy + n];
+            const int g = n / cg;
+            s[g] += y;
+            if (y < lo[g]) lo[g] = y;
+            if (y > hi[g]) hi[g] = y;
+        }
+        for (int g = 0; g < 32; ++g) gn_flush_region(s[g], lo[g], hi[g], sum + b * 32 + g, mn + b * 32 + g, mx + b * 32 + g);
     }
 }
 

@@ -82,6 +82,9 @@ void orc_epilogue_geglu_q(const int32_t* Chi, const int32_t* Clo, int M, int F, 
 
 /* GroupNorm statistics (EPI_PLAIN, k_epilogue with gs): accumulate into sum/mn/mx [(M / T) * 32] */
 void orc_gn_accumulate(const int32_t* Y, int M, int N, int ldy, int T, int64_t* sum, int32_t* mn, int32_t* mx);
+void orc_gn_ref_tile(int Mp, int Np, int Kp, int src8, int* BMr, int* BNr);
+void orc_gn_tiles(const int32_t* Y, int M, int N, int ldy, int T, int BMr, int BNr, int64_t* sum, int32_t* mn, int32_t* mx);
+void orc_gn_blocks(const int32_t* Y, int M, int N, int ldy, int T, int64_t* sum, int32_t* mn, int32_t* mx);
 /* EPI_QKV outputs from the plain output Y [M x 3C]: head-quantised q/k planes and V [M x C] */
 void orc_qkv_heads(const int32_t* Y, int M, int ldy, int C, int heads, int T, int TpQ, int TpK,
                    int8_t* qhi, int8_t* qlo, int32_t* qe, int64_t* qhs, int64_t* qls, int64_t* qts,

@@ -18,6 +18,9 @@ Definitions (reference file:line of the statement each one encodes):
   y             sat32(rshr((q . w) * m, s - e) + b), (+ residual, saturated) src/gemm_hl.h:1-3
   GEGLU         sat32(rshr(a * sat32(rshr(g * lut(g), 16)), 16))             src/gemm_hl.cu:292-293
   GELU          sat32(rshr(y * lut(y), 16))                                  src/gemm_hl.cu:280
+The *_dev forms restate what the reference's fixed-width code computes where its int64 product
+acc * m or its int32 table interpolation overflows: two's-complement wrapping, as the GPU executing
+it does (rshr_dev, epi1_dev, lut_dev, geglu_dev, gelu_dev).
 """
 from __future__ import annotations
 
@@ -43,6 +46,59 @@ def rshr(v: int, s: int) -> int:
     if s >= 0:
         return sat32(round_half_up(Fraction(v, 2 ** min(s, 62))))
     return sat32(v * 2 ** min(-s, 31))
+
+
+def wrap64(x: int) -> int:
+    """x reduced to a two's-complement int64 (what the device's 64-bit arithmetic keeps)."""
+    x = int(x) & (2**64 - 1)
+    return x - 2**64 if x >= 2**63 else x
+
+
+def wrap32(x: int) -> int:
+    x = int(x) & (2**32 - 1)
+    return x - 2**32 if x >= 2**31 else x
+
+
+def rshr_dev(v: int, s: int) -> int:
+    """rshr as the reference's int64 code evaluates it for any int64 v: the product v arrives
+    wrapped to 64 bits and the rounding add v + 2^(p-1) wraps too (src/intops.cuh:11-13); equal to
+    rshr() wherever neither wraps."""
+    v, s = wrap64(v), int(s)
+    if s >= 0:
+        p = min(s, 62)
+        t = wrap64(v + ((1 << p) >> 1))
+        return sat32(t >> p)          # Python's >> on ints is the arithmetic (floor) shift
+    neg = min(-s, 31)
+    lim = 1 << (62 - neg)
+    return sat32(min(max(v, -lim), lim) << neg)
+
+
+def epi1_dev(acc: int, m: int, s: int, e: int, b: int) -> int:
+    """y = sat32(rshr(acc * m, s - e) + b) with the int64 product acc * m wrapping
+    (src/gemm_hl.cu:40-43: `acc * c.x` on int64)."""
+    return sat32(rshr_dev(wrap64(int(acc) * int(m)), int(s) - int(e)) + int(b))
+
+
+def lut_dev(x: int, L) -> int:
+    """lut16i as its int32 code evaluates it for any table: b - a, (b - a) * f and a + (.. >> 10)
+    all wrap to 32 bits (src/intops.cuh:42-50); equal to lut() when nothing wraps."""
+    z = int(x) + (16 << 16)
+    if z < 0:
+        return 0
+    if z >= (32 << 16):
+        return 65536
+    i, f = z >> 10, z & 1023
+    a, b = int(L[i]), int(L[i + 1])
+    prod = wrap32(wrap32(b - a) * f)
+    return wrap32(a + (prod >> 10))
+
+
+def geglu_dev(a: int, g: int, L) -> int:
+    return sat32(rshr_dev(int(a) * sat32(rshr_dev(int(g) * lut_dev(g, L), 16)), 16))
+
+
+def gelu_dev(y: int, L) -> int:
+    return sat32(rshr_dev(int(y) * lut_dev(y, L), 16))
 
 
 def row_exp(m: int) -> int:

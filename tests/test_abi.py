@@ -161,7 +161,10 @@ def test_epilogue_and_gn_init_errors():
     lib = _lib.load()
     base = [None, FAKE, FAKE, 64, 128, 128, FAKE, FAKE, FAKE, 128, None]
     assert lib.vgemm_epilogue(*base, FAKE, 0) == -1
-    assert "GroupNorm" in lib.vgemm_last_error().decode()
+    assert "GN stats: shape" in lib.vgemm_last_error().decode()
+    # ldy != N with statistics: the reference throws "epilogue GN stats: shape" (src/kernels.cu:734)
+    assert lib.vgemm_epilogue(*base[:9], 132, None, FAKE, 64) == -1
+    assert "GN stats: shape" in lib.vgemm_last_error().decode()
     assert lib.vgemm_epilogue(*base[:4], 96, 96, *base[6:9], 96, None, FAKE, 48) == -1   # 96 * 48 % 1024 != 0
     assert lib.vgemm_epilogue(*base[:4], 100, 100, *base[6:9], 100, None, FAKE, 64) == -1  # N % 4
     assert lib.vgemm_gn_init(None, None, 4) == -1

@@ -138,9 +138,10 @@ def check_gn(c: Case, T, what, ws_bytes=0):
     assert_equal(Yg, Y, f"{what} Y")
     if rm is not None:
         assert_equal(rmg, rm, f"{what} rowmax")
-    want = oracle.gn_stats(Y, c.M, c.N, T)
+    want = oracle.gn_stats_fused(Y, c.M, c.N, T, c.Mp, c.Np, c.Kp, c.src)
     for k in ("sum", "mn", "mx"):
         assert_equal(st[k], want[k], f"{what} gn.{k}")
+    return Y, want
 
 
 @pytest.mark.parametrize("T", [64, 192, 256])
@@ -184,15 +185,34 @@ def test_gn_ignores_workspace():
     check_gn(c, 64, "gn ws", ws_bytes=256 << 20)
 
 
-@pytest.mark.parametrize("variant", [-1, 0, 1])
+@pytest.mark.parametrize("variant", [-1, 0, 1, 2, 3])
 def test_gn_saturated_groups(variant):
-    """Outputs that saturate to INT_MAX over whole groups of a tile (y > 0 plus a residual of INT_MAX)
-    still count: sum, min and max include them."""
+    """Outputs that saturate to INT_MAX through whole groups of one of the reference's 64 x 64 tiles
+    (y > 0 plus a residual of INT_MAX): that tile adds nothing for those groups, as the reference's
+    flush test (min != INT_MAX, src/gemm_hl.cu:306-309) skips it; a tile with one value below INT_MAX
+    in the group counts in full. Every forced tile shape gives the same records."""
     vg.set_variant(variant)
     c = Case(vg.SRC_I16, 256, 320, 320, seed=95, residual=True, s_range=(30, 30), m_range=(1, 2), b_range=(1000, 2000))
-    c.res[:64, :40] = 2**31 - 1
-    c.res[64:128, 100:] = 2**31 - 1
-    check_gn(c, 128, f"gn saturated v{variant}")
+    c.res[:64, :40] = 2**31 - 1        # tile (0, 0), groups 0..3 saturated through
+    c.res[64:128, 100:] = 2**31 - 1    # tiles (1, 1..4): groups 10..31 saturated through
+    c.res[127, 200] = -5               # ... except one value of group 20 in tile (1, 3)
+    Y, want = check_gn(c, 128, f"gn saturated v{variant}")
+    exact = oracle.gn_stats(Y, c.M, c.N, 128)
+    assert (want["sum"] != exact["sum"]).any() and (want["mx"] != exact["mx"]).any(), "the case must exercise the flush rule"
+
+
+@pytest.mark.parametrize("variant", [-1, 0, 1, 2])
+def test_gn_saturated_deep_tiles(variant):
+    """Deep K (Kp >= 2048) with Np % 128 == 0: the reference's tile is 64 x 128, so the statistics
+    regions are 64 x 128 whatever tile shape runs here."""
+    vg.set_variant(variant)
+    c = Case(vg.SRC_I16, 256, 256, 2048, seed=96, residual=True, s_range=(34, 34), m_range=(1, 2), b_range=(1000, 2000))
+    assert oracle.gn_ref_tile(c.Mp, c.Np, c.Kp, c.src) == (64, 128)
+    c.res[:64, :128] = 2**31 - 1       # one whole 64 x 128 tile
+    c.res[64:128, :64] = 2**31 - 1     # half of the next: not a whole tile, counts
+    Y, want = check_gn(c, 128, f"gn saturated deep v{variant}")
+    exact = oracle.gn_stats(Y, c.M, c.N, 128)
+    assert (want["sum"] != exact["sum"]).any()
 
 
 def test_gn_accumulates_over_calls():
@@ -225,6 +245,35 @@ def test_planar_epilogue_gn(M, N, T):
     torch.cuda.synchronize()
     assert_equal(to_np(Y), want, "planar Y")
     st = vg.gn_stats_read(gs, Mb * 32)
-    ref = oracle.gn_stats(want, M, N, T)
+    ref = oracle.gn_stats_planar(want, M, N, T)
     for k in ("sum", "mn", "mx"):
         assert_equal(st[k], ref[k], f"planar gn.{k}")
+
+
+@pytest.mark.parametrize("M,N,T", [(256, 320, 64), (64, 1024, 16)])
+def test_planar_epilogue_gn_saturated(M, N, T):
+    """k_epilogue statistics by the reference's rule (src/kernels.cu:67-68): a 1024-element block whose
+    outputs of a group all saturate to INT_MAX (residual INT_MAX, y >= 0) adds nothing for it."""
+    r = np.random.default_rng(M * 3 + N)
+    ldc = N
+    Chi = r.integers(0, 1 << 12, (M, ldc)).astype(np.int32)
+    Clo = r.integers(0, 1 << 12, (M, ldc)).astype(np.int32)
+    cst = np.stack([r.integers(1, 4, N), np.full(N, 20), r.integers(0, 1000, N), r.integers(0, 100, N)], 1).astype(np.int32)
+    e = np.zeros(M, np.int32)
+    R = r.integers(-(1 << 20), 1 << 20, (M, N)).astype(np.int32)
+    flat = R.reshape(-1)
+    flat[1024:2048] = 2**31 - 1            # the whole second block
+    flat[3 * 1024:3 * 1024 + 300] = 2**31 - 1
+    want = oracle.epilogue(Chi, Clo, M, N, ldc, cst, e, N, R)
+    Mb = -(-M // T)
+    gs = vg.gn_stats_alloc(Mb * 32)
+    vg.k_gn_init(gs, Mb * 32)
+    Y = dev(R)
+    vg.k_epilogue(dev(Chi), dev(Clo), M, N, ldc, dev(cst), dev(e), Y, N, residual=Y, gs=gs, T=T)
+    torch.cuda.synchronize()
+    assert_equal(to_np(Y), want, "planar Y")
+    st = vg.gn_stats_read(gs, Mb * 32)
+    ref = oracle.gn_stats_planar(want, M, N, T)
+    assert (ref["sum"] != oracle.gn_stats(want, M, N, T)["sum"]).any(), "the case must exercise the flush rule"
+    for k in ("sum", "mn", "mx"):
+        assert_equal(st[k], ref[k], f"planar saturated gn.{k}")

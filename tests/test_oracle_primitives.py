@@ -156,6 +156,82 @@ def test_geglu_gelu_against_definition():
         assert L.orc_gelu(int(a), tp) == rm.gelu(int(a), tab)
 
 
+def test_dev_forms_equal_definitions_without_wrap():
+    """The wrap-aware restatements reduce to the exact-rational definitions wherever no fixed-width
+    operation overflows."""
+    r = np.random.default_rng(21)
+    for _ in range(3000):
+        v = int(r.integers(-(2**61), 2**61))
+        s = int(r.integers(-40, 70))
+        assert rm.rshr_dev(v, s) == rm.rshr(v, s)
+    tab = r.integers(0, 65537, 2049)
+    for x in r.integers(-(1 << 21), 1 << 21, 2000):
+        assert rm.lut_dev(int(x), tab) == rm.lut(int(x), tab)
+
+
+def test_dev_forms_known_wraps():
+    """Worked values where the reference's fixed-width arithmetic wraps."""
+    # rounding add: 2^63 - 1 + 2^0 wraps to -2^63, so rshr(2^63 - 1, 1) = sat32(-2^62) = INT_MIN
+    assert rm.rshr_dev(2**63 - 1, 1) == -(2**31)
+    # product: 2^40 * 2^24 = 2^64 wraps to 0; (2^40 + 1) * 2^24 wraps to 2^24
+    assert rm.epi1_dev(2**40, 2**24, 20, 0, 7) == 7
+    assert rm.epi1_dev(2**40 + 1, 2**24, 10, 0, 7) == 2**14 + 7
+    # product 3 * 2^62 wraps to -2^62: rshr(-2^62, 40) = -2^22
+    assert rm.epi1_dev(3 * 2**31, 2**31, 40, 0, 0) == -(2**22)
+    # table: a = -2^31 + 1, b = 2^31 - 1, f = 512: b - a wraps to -2, the product to -1024, and
+    # a + (-1024 >> 10) = -2^31 (the unwrapped interpolation would give 0)
+    L = np.zeros(2049, np.int64)
+    L[5], L[6] = -(2**31) + 1, 2**31 - 1
+    x = 5 * 1024 + 512 - (1 << 20)
+    assert rm.lut(x, L) == 0 and rm.lut_dev(x, L) == -(2**31)
+    # (b - a) * f wraps without b - a wrapping: a = 0, b = 2^22, f = 1023 -> 2^22 * 1023 mod 2^32
+    L[5], L[6] = 0, 2**22
+    x = 5 * 1024 + 1023 - (1 << 20)
+    assert rm.lut_dev(x, L) == rm.wrap32(2**22 * 1023) >> 10 and rm.lut(x, L) == (2**22 * 1023) >> 10
+
+
+def test_epi1_wraps_like_the_reference():
+    """|acc * m| >= 2^63: the int64 product of src/gemm_hl.cu:41 wraps; the oracle's epi1 agrees
+    with the wrap-aware restatement on the K = 11520 extremes (|acc| up to 11520 * 32767 * 127)."""
+    r = np.random.default_rng(22)
+    n = 4000
+    acc_target = r.integers(-(11520 * 32767 * 127), 11520 * 32767 * 127, n, dtype=np.int64)
+    wsum = r.integers(-127 * 11520, 127 * 11520, n)
+    # split acc = 256 chi + clo + 128 wsum into plane sums of the sizes K = 11520 produces
+    rest = acc_target - 128 * wsum
+    chi = (rest // 256).astype(np.int64)
+    clo = rest - 256 * chi
+    m = r.integers((1 << 31) - (1 << 20), 1 << 31, n, dtype=np.int64)
+    s = r.integers(0, 63, n)
+    b = r.integers(-(2**31), 2**31, n, dtype=np.int64)
+    er = np.zeros(n, np.int32)
+    cst = np.stack([m, s, b, wsum], 1).astype(np.int32)
+    got = oracle.epi1(chi.astype(np.int32), clo.astype(np.int32), cst, er)
+    wraps = 0
+    for i in range(n):
+        acc = 256 * int(chi[i]) + int(clo[i]) + 128 * int(wsum[i])
+        wraps += abs(acc * int(m[i])) >= 2**63
+        assert got[i] == rm.epi1_dev(acc, int(m[i]), int(s[i]), 0, int(b[i])), i
+    assert wraps > n // 4
+
+
+def test_lut16i_wraps_like_the_reference():
+    """Tables whose entries differ by 2^21 or more: (b - a) * f (and b - a itself) wrap in int32."""
+    r = np.random.default_rng(23)
+    tab = r.integers(-(2**31), 2**31, 2049, dtype=np.int64).astype(np.int32)
+    xs = r.integers(-(1 << 20), 1 << 20, 4000)
+    got = oracle.lut16i(xs, tab)
+    np.testing.assert_array_equal(got, [rm.lut_dev(int(x), tab) for x in xs])
+    assert sum(rm.lut_dev(int(x), tab) != rm.lut(int(x), tab) for x in xs) > 1000
+    L = oracle.lib()
+    tp = tab.ctypes.data_as(ctypes.c_void_p)
+    vals = list(r.integers(-(1 << 21), 1 << 21, 1500))
+    for i, a in enumerate(vals):
+        g = vals[(i * 5 + 1) % len(vals)]
+        assert L.orc_geglu(int(a), int(g), tp) == rm.geglu_dev(int(a), int(g), tab)
+        assert L.orc_gelu(int(a), tp) == rm.gelu_dev(int(a), tab)
+
+
 @pytest.mark.parametrize("seed", [0, 1])
 def test_attn_score_split_identity(seed):
     """src/test_attn_score.cu:14-24: on the reference's edge list and random quantised operands,

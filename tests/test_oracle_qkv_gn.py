@@ -61,6 +61,138 @@ def test_gn_stats_accumulate_across_calls():
     np.testing.assert_array_equal(mx, np.maximum(a["mx"], b["mx"]))
 
 
+INT_MAX, INT_MIN = 2**31 - 1, -(2**31)
+
+
+@pytest.mark.parametrize("Mp,Np,Kp,src,want", [
+    # src/gemm_hl.cu:352-358 with g_gemm_hl_variant = -1, case by case
+    (32768, 320, 320, 0, (64, 64)),      # Kp < 2048: the small tile
+    (32768, 1280, 2047, 3, (64, 64)),
+    (8192, 640, 5760, 0, (64, 128)),     # deep K, Np % 128 == 0: the wide tile
+    (512, 1280, 11520, 2, (64, 128)),    # ... for any source
+    (32768, 320, 2880, 0, (128, 64)),    # deep K, Np % 128 != 0, Mp % 128 == 0: the tall tile (int8 planes)
+    (32768, 320, 2880, 3, (128, 64)),    # int16 rows hold the same planes
+    (32768, 320, 2880, 1, (64, 64)),     # register-path sources have no tall tile
+    (32768, 320, 2880, 2, (64, 64)),
+    (32704, 320, 2880, 0, (64, 64)),     # Mp % 128 != 0: the small tile
+])
+def test_gn_ref_tile(Mp, Np, Kp, src, want):
+    assert oracle.gn_ref_tile(Mp, Np, Kp, src) == want
+
+
+def _gn_regions(Y, M, N, T, regions):
+    """Records by the flush rule, from an explicit list of regions: (sample, rows, cols) with rows
+    and cols index arrays. Straight numpy, one region at a time."""
+    B = -(-M // T)
+    s = np.zeros(B * 32, np.int64)
+    mn = np.full(B * 32, INT_MAX, np.int64)
+    mx = np.full(B * 32, INT_MIN, np.int64)
+    grp = np.arange(N) // (N // 32)
+    for b, rows, cols in regions:
+        sub = Y[np.ix_(rows, cols)].astype(np.int64)
+        for g in np.unique(grp[cols]):
+            v = sub[:, grp[cols] == g]
+            if v.size == 0 or v.min() == INT_MAX:
+                continue
+            s[b * 32 + g] += v.sum()
+            mn[b * 32 + g] = min(mn[b * 32 + g], v.min())
+            mx[b * 32 + g] = max(mx[b * 32 + g], v.max())
+    return {"sum": s, "mn": mn, "mx": mx}
+
+
+def _tile_regions(M, N, T, bm, bn):
+    return [(m0 // T, np.arange(m0, min(m0 + bm, M)), np.arange(n0, min(n0 + bn, N)))
+            for m0 in range(0, M, bm) for n0 in range(0, N, bn)]
+
+
+def _block_regions(M, N, T):
+    out = []
+    for e0 in range(0, M * N, 1024):
+        idx = np.arange(e0, min(e0 + 1024, M * N))
+        r, n = idx // N, idx % N
+        for rr in np.unique(r):   # a block is a run of whole and partial rows
+            out.append(((e0 // N) // T, np.array([rr]), n[r == rr]))
+    return out
+
+
+def _check(got, want):
+    for k in ("sum", "mn", "mx"):
+        np.testing.assert_array_equal(got[k], want[k], err_msg=k)
+
+
+@pytest.mark.parametrize("M,N,T,tile", [(256, 320, 128, (64, 64)), (256, 320, 64, (128, 64)),
+                                        (200, 1280, 64, (64, 128)), (384, 96, 192, (64, 64))])
+def test_gn_tiles_without_saturation_equal_exact(M, N, T, tile):
+    """No output is INT_MAX: the flush rule never fires and the statistics are the exact ones
+    (when every tile lies in one sample)."""
+    r = np.random.default_rng(M * N)
+    Y = _y(r, M, N, 30)
+    Y[0, 0] = INT_MIN
+    got = oracle.gn_stats_fused(Y, M, N, T, 0, 0, 0, 0, tile=tile)
+    if T % tile[0] == 0:
+        _check(got, oracle.gn_stats(Y, M, N, T))
+    _check(got, _gn_regions(Y, M, N, T, _tile_regions(M, N, T, *tile)))
+
+
+@pytest.mark.parametrize("tile", [(64, 64), (128, 64), (64, 128)])
+def test_gn_tiles_drop_saturated_tile_groups(tile):
+    """A tile whose outputs of a group are all INT_MAX adds neither their sum nor their max; one
+    more element below INT_MAX in that tile and group brings the whole tile-group back."""
+    M, N, T = 256, 320, 128       # groups of 10 columns
+    r = np.random.default_rng(7)
+    Y = _y(r, M, N, 20)
+    bm, bn = tile
+    Y[:bm, :bn] = INT_MAX                  # tile (0, 0): groups 0..bn/10 saturated through
+    Y[128:128 + bm, 0:10] = INT_MAX        # a tile of sample 1, group 0 only
+    Y[128 + bm - 1, 5] = 17                # ... but one element of it is not: that tile-group counts
+    Y[:, 300:310] = INT_MIN                # group 30 at INT_MIN everywhere: always counts
+    got = oracle.gn_stats_fused(Y, M, N, T, 0, 0, 0, 0, tile=tile)
+    _check(got, _gn_regions(Y, M, N, T, _tile_regions(M, N, T, bm, bn)))
+    exact = oracle.gn_stats(Y, M, N, T)
+    # group 0 of sample 0: the saturated tile (0, 0) is dropped
+    assert got["sum"][0] == exact["sum"][0] - bm * 10 * INT_MAX
+    assert got["sum"][32] == exact["sum"][32] and got["mx"][32] == INT_MAX
+    assert got["mx"][0] < INT_MAX and exact["mx"][0] == INT_MAX
+    assert got["mn"][0] == exact["mn"][0]
+    assert got["mn"][30] == INT_MIN and got["sum"][30] == exact["sum"][30]
+
+
+def test_gn_tiles_whole_tile_to_first_rows_sample():
+    """A 128-row tile over samples of 64 rows credits all its rows to the sample of its first row."""
+    M, N, T = 256, 64, 64
+    Y = np.ones((M, N), np.int32)
+    got = oracle.gn_stats_fused(Y, M, N, T, 0, 0, 0, 0, tile=(128, 64))
+    per_group = 2     # 64 columns / 32 groups
+    np.testing.assert_array_equal(got["sum"].reshape(4, 32)[:, 0], [128 * per_group, 0, 128 * per_group, 0])
+    np.testing.assert_array_equal(got["mn"].reshape(4, 32)[:, 0], [1, INT_MAX, 1, INT_MAX])
+
+
+@pytest.mark.parametrize("M,N,T", [(192, 128, 64), (300, 1280, 100), (512, 320, 256), (64, 32, 32)])
+def test_gn_blocks_against_regions(M, N, T):
+    """k_epilogue's per-1024-element blocks, with saturated groups planted inside one block."""
+    r = np.random.default_rng(M + 3 * N)
+    Y = _y(r, M, N, 24)
+    flat = Y.reshape(-1)
+    cg = N // 32
+    for e in range(1024, min(2048, M * N)):      # block 1: group 0 elements saturated
+        if (e % N) // cg == 0:
+            flat[e] = INT_MAX
+    got = oracle.gn_stats_planar(Y, M, N, T)
+    _check(got, _gn_regions(Y, M, N, T, _block_regions(M, N, T)))
+
+
+def test_gn_blocks_drop_saturated_block():
+    """N = 1024: each block is one row. Row 1 all INT_MAX adds nothing; row 0 adds everything."""
+    M, N, T = 4, 1024, 4
+    Y = np.zeros((M, N), np.int32)
+    Y[1] = INT_MAX
+    Y[2, :] = 5
+    got = oracle.gn_stats_planar(Y, M, N, T)
+    np.testing.assert_array_equal(got["sum"], np.full(32, 5 * 32))
+    np.testing.assert_array_equal(got["mn"], np.zeros(32))
+    np.testing.assert_array_equal(got["mx"], np.full(32, 5))
+
+
 def _round_half_up(y, e):
     """floor(y / 2^e + 1/2) exactly, by integer floor division."""
     y = y.astype(np.int64)

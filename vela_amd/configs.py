@@ -37,7 +37,7 @@ def phi_lut() -> np.ndarray:
 @dataclass
 class Layer:
     name: str
-    kind: str                      # "linear" | "conv"
+    kind: str                      # "linear" | "conv" | "conv_in" (3x3 conv of an int32 image through im2col3)
     M: int                         # output rows (B*Ho*Wo for a conv)
     K: int                         # real reduction length (9C for a conv)
     N: int                         # real output columns of W (2F for GEGLU)
@@ -59,7 +59,7 @@ class Layer:
 
     def __post_init__(self):
         if self.src < 0:
-            self.src = SRC_CONV16 if self.kind == "conv" else SRC_I16
+            self.src = {"conv": SRC_CONV16, "conv_in": SRC_I8}.get(self.kind, SRC_I16)
 
     @property
     def Kp(self) -> int:
@@ -94,6 +94,8 @@ class Layer:
     def a_bytes(self) -> int:
         if self.kind == "conv":
             return 2 * self.B * self.H * self.W * self.C   # the NHWC image, counted once
+        if self.kind == "conv_in":
+            return 4 * self.B * self.H * self.W * self.C   # the int32 NHWC image, counted once
         return 2 * self.M * self.K
 
     @property
@@ -135,6 +137,12 @@ def make_host(L: Layer) -> dict:
     h = {}
     if L.kind == "conv":
         h["img"] = _act((L.B, L.H, L.W, L.C), s + 1, L.a_dist)
+    elif L.kind == "conv_in":
+        # int32 pixels: 16-bit Gaussian values times 2^k, k in [0, 6] per pixel, so that the
+        # per-row shifts e of the im2col quantisation vary over the image
+        base = _act((L.B, L.H, L.W, L.C), s + 1, L.a_dist).astype(np.int32)
+        k = dg.i32_uniform((L.B, L.H, L.W, 1), s + 8, 0, 6)
+        h["img32"] = np.ascontiguousarray(base << k)
     else:
         h["a"] = _act((L.M, L.K), s + 1, L.a_dist)
     w = np.zeros((L.Np, L.Kp), dtype=np.int8)
@@ -187,7 +195,9 @@ def unet_layers(B: int = 8) -> list[Layer]:
     (src/engine.cu:455-490 with resnet :389-405 and transformer :406-454; widths 320/640/1280/1280,
     64x64 latent). QKV is one PLAIN GEMM with N = 3C; ff.net.0.proj is the interleaved GEGLU GEMM
     (+ rowmax, as gegluX at :447); ff.net.2 writes rowmax; residual adds as at :400-401, :431, :440,
-    :447, :451. conv_in (C = 4) runs on a materialised im2col operand (K = 36 padded to 48)."""
+    :447, :451. conv_in (C = 4, an int32 image) runs as the reference runs it (src/engine.cu:458 ->
+    :254-280): pixel maxima, a materialised im2col3 operand (K = 36 padded to 48, e per row), then the
+    GEMM on those int8 planes."""
     L: list[Layer] = []
     seed = SEED0 + 5
 
@@ -221,7 +231,7 @@ def unet_layers(B: int = 8) -> list[Layer]:
 
     ch = [320, 640, 1280, 1280]
     H = 64
-    add(Layer("conv_in", "linear", B * H * H, 36, 320, a_dist=("gauss", 3000.0), meta={"conv_in": True}))
+    add(Layer("conv_in", "conv_in", B * H * H, 36, 320, B=B, H=H, W=H, C=4, a_dist=("gauss", 3000.0)))
     skips = [320]
     cin = 320
     for i in range(4):
@@ -253,22 +263,6 @@ def unet_layers(B: int = 8) -> list[Layer]:
     return L
 
 
-def unet_conv_in_operand(L: Layer, h: dict) -> dict:
-    """conv_in's A operand: a tap-major 3x3 im2col of a [B,64,64,4] int16 image, K = 36 zero-padded
-    to 48 (the value 0 contributes nothing: its W columns are zero)."""
-    B, H = 8, 64
-    img = _act((B, H, H, 4), L.seed * 16 + 1, L.a_dist)
-    pad = np.zeros((B, H + 2, H + 2, 4), np.int16)
-    pad[:, 1:-1, 1:-1] = img
-    cols = np.zeros((B, H, H, 48), np.int16)
-    for tap in range(9):
-        ky, kx = divmod(tap, 3)
-        cols[..., tap * 4:(tap + 1) * 4] = pad[:, ky:ky + H, kx:kx + H]
-    h = dict(h)
-    h["a"] = cols.reshape(B * H * H, 48)
-    return h
-
-
 # ---------------------------------------------------------------- device problem
 
 class DeviceProblem:
@@ -281,9 +275,14 @@ class DeviceProblem:
 
         self.L = L
         self.h = h if h is not None else make_host(L)
-        if L.meta.get("conv_in") and "a" not in (h or {}):
-            self.h = unet_conv_in_operand(L, self.h)
         t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(device)   # noqa: E731
+        if L.kind == "conv_in":
+            # k_pixmax + k_im2col3 outputs: pixel maxima, int8 planes [Mp x Kp] and row shifts
+            self.img32 = t(self.h["img32"])
+            self.pm = torch.zeros(L.B * L.H * L.W, dtype=torch.int32, device=device)
+            self.hi = torch.zeros((L.Mp, L.Kp), dtype=torch.int8, device=device)
+            self.lo = torch.zeros((L.Mp, L.Kp), dtype=torch.int8, device=device)
+            self.e_in = torch.zeros(L.Mp, dtype=torch.int32, device=device)
         self.w = t(self.h["w"])
         self.cst = t(self.h["cst"])
         self.e = t(self.h["e"]) if self.h.get("e") is not None else None
@@ -313,6 +312,8 @@ class DeviceProblem:
             A.q16 = vg.ptr(self.a)
             A.ld16 = self.a.shape[1]
             A.K = self.a.shape[1]
+        elif L.kind == "conv_in":
+            A.hi, A.lo, A.ld8, A.e = vg.ptr(self.hi), vg.ptr(self.lo), L.Kp, vg.ptr(self.e_in)
         else:
             raise ValueError("DeviceProblem drives the int16 sources")
         E = vg.AEpi(epi=L.epi, Y=vg.ptr(self.y), ldy=L.Nout)
@@ -337,4 +338,7 @@ class DeviceProblem:
         from . import gemm as vg
 
         L = self.L
+        if L.kind == "conv_in":
+            vg.k_pixmax(self.img32, L.B * L.H * L.W, L.C, self.pm, stream=stream)
+            vg.k_im2col3(self.img32, self.pm, L.B, L.H, L.W, L.C, L.stride, self.hi, self.lo, self.e_in, L.Kp, stream=stream)
         vg.k_gemm_hl2(self.A, L.Mp, L.M, self.w, self.w.shape[1], L.Np, L.N, L.Kp, self.cst, self.E, stream=stream)

@@ -92,7 +92,11 @@ bool stripe_applies(int src, int epi, const vk::GemmParams& p) {
     if (p.Kp > 320 || !p.vec_store) return false;
     const int nout = epi == VGEMM_EPI_GEGLU ? p.Nreal / 2 : p.Nreal;
     if (nout % 4) return false;
-    const long long yext = ((long long)(p.Mreal - 1) * p.ldy + nout) * 4;
+    // the kernel forms 32-bit byte offsets for every row of a 128-row stripe, pad rows included:
+    // all of them must stay below 2^31, so that rows at or past Mreal fail the buffer range check
+    // instead of wrapping back into Y
+    const long long rows = (long long)cdiv(p.Mreal, STRIPE_BM) * STRIPE_BM;
+    const long long yext = ((rows - 1) * p.ldy + nout) * 4;
     return yext <= MAX_EXTENT;
 }
 
@@ -163,6 +167,18 @@ size_t ws_bytes_for(int variant, int M, int N, int splits) {
     const size_t rows = size_t(cdiv(M, TILES[variant].BM)) * TILES[variant].BM;
     const size_t cols = size_t(cdiv(N, TILES[variant].BN)) * TILES[variant].BN;
     return size_t(splits) * 2 * rows * cols * 4;
+}
+
+// The tile the reference's fused GEMM runs for these padded sizes (src/gemm_hl.cu:352-358, automatic
+// choice), which is the region its GroupNorm statistics are gathered and flushed over: for
+// Kp >= 2048, 64 x 128 when Np % 128 == 0, else 128 x 64 when Mp % 128 == 0 and the A operand is int8
+// planes (the int16 rows hold the same planes), else 64 x 64.
+Tiles gn_ref_tile(int Mp, int Np, int Kp, int src) {
+    int v = 0;
+    if (Kp >= 2048) v = Np % 128 == 0 ? 2 : (Mp % 128 == 0 ? 1 : 0);
+    const bool planes = src == VGEMM_SRC_I8 || src == VGEMM_SRC_I16;
+    if (v == 1 && !planes) v = 0;
+    return Tiles{v == 1 ? 128 : 64, v == 2 ? 128 : 64};
 }
 
 int launch_src(int src, int variant, int epi, const vk::GemmParams& p, hipStream_t st) {
@@ -340,6 +356,14 @@ int vgemm_hl2(void* stream, const VgemmASrc* A, int Mp, int Mreal, const int8_t*
     int variant = halo_bm ? (halo_bm == 128 ? 0 : 1) : g_variant >= 0 && g_variant < NVARIANT ? g_variant : pick_variant(Mreal, Nreal, Kp);
     if (variant >= 3 && (A->src == VGEMM_SRC_X32 || A->src == VGEMM_SRC_CONV32)) variant = 0;
     if (epi == VGEMM_EPI_QKV) variant = 0;   // whole heads per wave (the reference forces its 64 x 64 tile, src/gemm_hl.cu:358)
+    if (p.gnstat) {
+        // statistics regions = the reference's tile; the block must hold whole regions (128 x 128
+        // holds any of them, as does the halo kernel's 128 x 128)
+        const Tiles rt = gn_ref_tile(Mp, Np, Kp, A->src);
+        p.gnBM = rt.BM;
+        p.gnBN = rt.BN;
+        if (!halo_bm && (TILES[variant].BM % rt.BM || TILES[variant].BN % rt.BN)) variant = 0;
+    }
     const int BM = TILES[variant].BM, BN = TILES[variant].BN;
     p.mtiles = cdiv(Mreal, BM);
     p.ntiles = cdiv(Nreal, BN);
@@ -438,7 +462,7 @@ int vgemm_epilogue(void* stream, const int32_t* Chi, const int32_t* Clo, int M, 
     if (!Chi || !Clo || !cst || !e || !Y || M <= 0 || N <= 0) return fail(VGEMM_ERR_ARG, "epilogue: bad arguments");
     if (!aligned16(Chi) || !aligned16(Clo) || !aligned16(Y) || (residual && !aligned16(residual))) return fail(VGEMM_ERR_ARG, "epilogue: pointers must be 16-byte aligned");
     // src/kernels.h:16: 32 groups of whole columns, a block's 1024 elements in one sample
-    if (gs && (N % 32 || T <= 0 || ((long long)T * N) % 1024)) return fail(VGEMM_ERR_ARG, "epilogue: GroupNorm statistics need N %% 32 == 0 and (T*N) %% 1024 == 0");
+    if (gs && (N % 32 || T <= 0 || ((long long)T * N) % 1024 || ldy != N)) return fail(VGEMM_ERR_ARG, "epilogue GN stats: shape (N %% 32 == 0, (T*N) %% 1024 == 0 and ldy == N required)");
     return hip_status(vk::launch_epilogue(static_cast<hipStream_t>(stream), Chi, Clo, M, N, ldc, reinterpret_cast<const int4*>(cst), e, Y, ldy, residual,
                                           static_cast<vk::GnStat*>(gs), T),
                       "epilogue launch");

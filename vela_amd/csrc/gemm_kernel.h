@@ -133,14 +133,17 @@ __device__ __forceinline__ void quant16_pairs(unsigned* d, int e) {
 
 // ---------------------------------------------------------------- epilogue shared state
 
-// GroupNorm accumulators of a block (EPI_PLAIN_GN only): [sample slot][group], slot 0 = sample gsb0
+// GroupNorm accumulators of a block (EPI_PLAIN_GN only): [region][group]. A region is one
+// gnBM x gnBN tile of the reference's GEMM (the granularity its statistics are flushed at); a
+// block of at most 128 x 256 outputs holds at most 2 x 4 of them, region (tr, tc) at slot 4 tr + tc.
+constexpr int GN_REGIONS = 8;
 template <bool GN>
 struct GnShared {};
 template <>
 struct GnShared<true> {
-    long long gsum[2][32];
-    int gmin[2][32], gmax[2][32];
-    int gsb0;
+    long long gsum[GN_REGIONS][32];
+    int gmin[GN_REGIONS][32], gmax[GN_REGIONS][32];
+    int gm0;   // first output row of the block
 };
 
 // Per-block epilogue constants, GELU table and exactness flags, in LDS.
@@ -154,32 +157,33 @@ struct EpiShared : GnShared<GN> {
     int flag[8];        // emin, emax, smin, smax, column bound failed, table range failed, max |b|, b not foldable
 };
 
-// GroupNorm accumulators of a block (src/gemm_hl.cu:175-177, 285-287, 306-309): cleared before the
-// epilogue (by threads 0..63, before a barrier), one LDS atomic per group and value, then flushed
-// to GnStat[sample * 32 + group] by one global atomic each. A block spans at most two samples
-// (gnT % 64 == 0, at most 128 rows), a wave's rows lie in one. A slot is empty when its min and max
-// both keep their initial values; the reference tests min != INT_MAX alone, which also skips a
-// (tile, group) whose every output saturated to INT_MAX (its 64 x 64 tiles differ from these, so
-// that corner case cannot be reproduced tile for tile: the statistics here are the exact ones).
+// GroupNorm statistics of a block (src/gemm_hl.cu:175-177, 285-287, 306-309). The reference gathers
+// the sum, min and max of its tile's outputs per group and flushes them to
+// GnStat[(tile row 0 / gnT) * 32 + group] only when the min is not INT_MAX, so a tile whose outputs
+// of a group all saturated to INT_MAX adds nothing for that group. The statistics here are gathered
+// per region = one such tile (the host picks a block shape made of whole regions and passes the
+// reference's tile as gnBM x gnBN), cleared before the epilogue, fed by one LDS atomic per group and
+// lane, and flushed by the same rule with one global atomic each.
 template <class S>
 __device__ __forceinline__ void gn_clear(const GemmParams& p, int m0, S& sh) {
     const int tid = threadIdx.x;
-    if (tid < 64) {
+    if (tid < GN_REGIONS * 32) {
         sh.gsum[tid >> 5][tid & 31] = 0;
         sh.gmin[tid >> 5][tid & 31] = INT_MAX;
         sh.gmax[tid >> 5][tid & 31] = INT_MIN;
     }
-    if (tid == 0) sh.gsb0 = p.gnT > 0 ? m0 / p.gnT : 0;
+    if (tid == 0) sh.gm0 = m0;
 }
 
 template <class S>
 __device__ __forceinline__ void gn_flush(const GemmParams& p, S& sh) {
     __syncthreads();
     const int tid = threadIdx.x;
-    if (tid < 64) {
+    if (tid < GN_REGIONS * 32) {
         const int slot = tid >> 5, g = tid & 31;
-        if (sh.gmin[slot][g] != INT_MAX || sh.gmax[slot][g] != INT_MIN) {   // the slot holds values
-            GnStat* gs = p.gnstat + (sh.gsb0 + slot) * 32 + g;
+        if (sh.gmin[slot][g] != INT_MAX) {   // the reference's test: a region of INT_MAX values (or none) adds nothing
+            const int r0 = sh.gm0 + (slot >> 2) * p.gnBM;   // the region's first row gives its sample
+            GnStat* gs = p.gnstat + (r0 / p.gnT) * 32 + g;
             atomicAdd(reinterpret_cast<unsigned long long*>(&gs->sum), static_cast<unsigned long long>(sh.gsum[slot][g]));
             atomicMin(&gs->mn, sh.gmin[slot][g]);
             atomicMax(&gs->mx, sh.gmax[slot][g]);
@@ -611,15 +615,14 @@ __device__ __forceinline__ void fused_epilogue_t(const GemmParams& p, const v4i 
             }
         }
         if constexpr (gn) {
-            // group of column c: c / (Nreal / 32); the wave's rows lie in one sample (gnT % 64 == 0)
+            // group of column c: c / (Nreal / 32); region of the lane's rows and four columns: the
+            // block's rows and columns start at multiples of its shape, which holds whole regions
             S& shw = const_cast<S&>(sh);
             const int cg = p.Nreal >> 5;
-            const int slot = rbase / p.gnT - shw.gsb0;
+            const int slot = ((rbase % T::BM) / p.gnBM) * 4 + (ncol % T::BN) / p.gnBN;
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
-                // a lane holds values unless min and max are both still at their initial values
-                // (min == INT_MAX alone would drop columns whose values all saturated to INT_MAX)
-                if (ncol + v < nlim && (gmn[v] != INT_MAX || gmx[v] != INT_MIN)) {
+                if (ncol + v < nlim) {
                     const int g = (ncol + v) / cg;
                     atomicAdd(reinterpret_cast<unsigned long long*>(&shw.gsum[slot][g]), static_cast<unsigned long long>(gsum[v]));
                     atomicMin(&shw.gmin[slot][g], gmn[v]);

@@ -59,114 +59,157 @@ __global__ void __launch_bounds__(256) pixmax_kernel(const int32_t* __restrict__
     if (lane == 0) pm[r] = m;
 }
 
-__device__ __forceinline__ uint32_t window_max(const uint32_t* __restrict__ pm, int b, int H, int W, int stride, int oy, int ox) {
-    uint32_t m = 0;
-    for (int ky = 0; ky < 3; ++ky)
-        for (int kx = 0; kx < 3; ++kx) {
-            const int iy = oy * stride - 1 + ky, ix = ox * stride - 1 + kx;
-            if (iy >= 0 && iy < H && ix >= 0 && ix < W) m = max(m, pm[(size_t(b) * H + iy) * W + ix]);
-        }
-    return m;
-}
-
-// k_conv_e (src/gemm_hl.cu:335-349)
-__global__ void __launch_bounds__(256) conv_e_kernel(const uint32_t* __restrict__ pm, int B, int H, int W, int stride, int Ho, int Wo,
+// k_conv_e (src/gemm_hl.cu:335-349): e[r] = row_exp of the maximum of pm over the 3x3 window of
+// output pixel r (pad 1, image border excluded). Separable: a block takes one output row (b, oy) and
+// a run of `oc` output columns; it first reduces the (at most three) input rows of the windows column
+// by column into LDS, with 0 outside the image (pm >= 0, so 0 is the identity of the maximum), then
+// each output column takes the maximum of three neighbouring column values. oc = min(256, 1024 /
+// stride), so the (oc - 1) * stride + 3 input columns of a run fit the LDS row.
+constexpr int CONVE_LDS = 1027;
+__host__ __device__ inline int conv_e_run(int stride) { return stride >= 1024 ? 1 : min(256, 1024 / stride); }
+__global__ void __launch_bounds__(256) conv_e_kernel(const uint32_t* __restrict__ pm, int H, int W, int stride, int Ho, int Wo, int runs,
                                                      int32_t* __restrict__ e) {
-    const int r = blockIdx.x * 256 + threadIdx.x;
-    if (r >= B * Ho * Wo) return;
-    const int pp = r % (Ho * Wo), b = r / (Ho * Wo), oy = pp / Wo, ox = pp - oy * Wo;
-    e[r] = rowexp_u32(window_max(pm, b, H, W, stride, oy, ox));
-}
-
-// k_im2col3 (src/kernels.cu:117-170, 740-744): one block per output row (tap-major K, C % 4 == 0);
-// rows [rows, align32(rows)) get hi 0x00 / lo 0x80 (written here by a kernel, not a memset).
-__global__ void __launch_bounds__(256) im2col3_kernel(const int32_t* __restrict__ X, const uint32_t* __restrict__ pm, int B, int H, int W,
-                                                      int C, int stride, int Ho, int Wo, int rows, int8_t* __restrict__ hi,
-                                                      int8_t* __restrict__ lo, int32_t* __restrict__ e, int Kp) {
-    __shared__ int she;
-    const int r = blockIdx.x;
-    unsigned* h = reinterpret_cast<unsigned*>(hi + size_t(r) * Kp);
-    unsigned* l = reinterpret_cast<unsigned*>(lo + size_t(r) * Kp);
-    const int K4 = Kp >> 2;
-    if (r >= rows) {
-        for (int k = threadIdx.x; k < K4; k += 256) { h[k] = PAD_HI4; l[k] = PAD_LO4; }
-        return;
-    }
-    const int b = r / (Ho * Wo), p = r % (Ho * Wo), oy = p / Wo, ox = p % Wo;
-    if (threadIdx.x == 0) {
-        she = rowexp_u32(window_max(pm, b, H, W, stride, oy, ox));
-        e[r] = she;
+    __shared__ uint32_t colmax[CONVE_LDS];
+    const int oc = conv_e_run(stride);
+    const int row = blockIdx.x / runs, run = blockIdx.x - row * runs;   // row = b * Ho + oy
+    const int oy = row % Ho, b = row / Ho;
+    const int ox0 = run * oc;
+    const int ix0 = ox0 * stride - 1;                  // first input column of the run's windows
+    const int nx = min(oc, Wo - ox0);
+    const int ncols = (nx - 1) * stride + 3;           // input columns its windows cover
+    const int iy0 = oy * stride - 1;
+    const uint32_t* img = pm + size_t(b) * H * W;
+    for (int j = threadIdx.x; j < ncols; j += 256) {
+        const int ix = ix0 + j;
+        uint32_t m = 0;
+        if (ix >= 0 && ix < W) {
+#pragma unroll
+            for (int ky = 0; ky < 3; ++ky) {
+                const int iy = iy0 + ky;
+                if (iy >= 0 && iy < H) m = max(m, img[size_t(iy) * W + ix]);
+            }
+        }
+        colmax[j] = m;
     }
     __syncthreads();
-    const int ee = she, C4 = C >> 2, K4r = 9 * C4;
-    for (int idx = threadIdx.x; idx < K4; idx += 256) {
-        if (idx >= K4r) { h[idx] = PAD_HI4; l[idx] = PAD_LO4; continue; }
-        const int tap = idx / C4, c = (idx - tap * C4) * 4;
-        const int iy = oy * stride - 1 + tap / 3, ix = ox * stride - 1 + tap % 3;
-        int q[4] = {0, 0, 0, 0};
-        if (iy >= 0 && iy < H && ix >= 0 && ix < W) {
-            const int4 v = *reinterpret_cast<const int4*>(X + ((size_t(b) * H + iy) * W + ix) * C + c);
-            q[0] = quant16_32(v.x, ee); q[1] = quant16_32(v.y, ee); q[2] = quant16_32(v.z, ee); q[3] = quant16_32(v.w, ee);
-        }
-        h[idx] = pack_hi4(q[0], q[1], q[2], q[3]);
-        l[idx] = pack_lo4(q[0], q[1], q[2], q[3]);
+    const int t = threadIdx.x;
+    if (t < nx) {
+        const int j = t * stride;
+        const uint32_t m = max(max(colmax[j], colmax[j + 1]), colmax[j + 2]);
+        e[size_t(row) * Wo + ox0 + t] = rowexp_u32(m);
     }
 }
 
-// k_epilogue (src/kernels.cu:70-95): four columns per thread. With GN, the per-(sample, group)
-// sum, min and max of the outputs are gathered in LDS and flushed by one global atomic each per
-// block; a block's 1024 elements lie in one sample ((T * N) % 1024 == 0, checked on the host).
-// A group is flushed when it holds values (min or max moved from its initial value); the reference's
-// test of min != INT_MAX alone would skip a block's group whose outputs all saturated to INT_MAX.
+// k_im2col3 (src/kernels.cu:117-170, 740-744): the materialised 3x3 im2col, tap-major K
+// (k = tap*C + c, tap = 3*ky + kx), quantised per output row with e = row_exp(window maximum of pm),
+// pad columns [9C, Kp) and pad rows [rows, align32(rows)) set to the value 0 = (hi 0, lo -128).
+// One wave per output row, four rows per block: lanes 0..8 fetch the window's nine pm values, a
+// wave maximum gives e (no LDS), then the wave walks the nine taps, each lane quantising four
+// consecutive channels per step (C % 4 == 0: 16-byte loads, 4-byte hi/lo stores).
+__global__ void __launch_bounds__(256) im2col3_kernel(const int32_t* __restrict__ X, const uint32_t* __restrict__ pm, int H, int W,
+                                                      int C, int stride, int Ho, int Wo, int rows, int rows_pad,
+                                                      int8_t* __restrict__ hi, int8_t* __restrict__ lo, int32_t* __restrict__ e, int Kp) {
+    const int r = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (r >= rows_pad) return;
+    unsigned* h = reinterpret_cast<unsigned*>(hi + size_t(r) * Kp);
+    unsigned* l = reinterpret_cast<unsigned*>(lo + size_t(r) * Kp);
+    const int K4 = Kp >> 2, C4 = C >> 2;
+    if (r >= rows) {
+        for (int k = lane; k < K4; k += 64) { h[k] = PAD_HI4; l[k] = PAD_LO4; }
+        return;
+    }
+    const int ox = r % Wo, oy = (r / Wo) % Ho, b = r / (Wo * Ho);
+    const int iy0 = oy * stride - 1, ix0 = ox * stride - 1;
+    // the window maximum: lane t < 9 holds tap t's pixel maximum (0 outside the image)
+    uint32_t m = 0;
+    if (lane < 9) {
+        const int iy = iy0 + lane / 3, ix = ix0 + lane % 3;
+        if (iy >= 0 && iy < H && ix >= 0 && ix < W) m = pm[(size_t(b) * H + iy) * W + ix];
+    }
+#pragma unroll
+    for (int o = 8; o; o >>= 1) m = max(m, uint32_t(__shfl_xor(int(m), o)));   // lanes 0..15 hold all nine
+    const int ee = rowexp_u32(uint32_t(__shfl(int(m), 0)));
+    if (lane == 0) e[r] = ee;
+    for (int tap = 0; tap < 9; ++tap) {
+        const int iy = iy0 + tap / 3, ix = ix0 + tap % 3;
+        const bool inside = iy >= 0 && iy < H && ix >= 0 && ix < W;
+        const int4* src = reinterpret_cast<const int4*>(X + ((size_t(b) * H + (inside ? iy : 0)) * W + (inside ? ix : 0)) * C);
+        for (int c4 = lane; c4 < C4; c4 += 64) {
+            int q0 = 0, q1 = 0, q2 = 0, q3 = 0;
+            if (inside) {
+                const int4 v = src[c4];
+                q0 = quant16_32(v.x, ee); q1 = quant16_32(v.y, ee); q2 = quant16_32(v.z, ee); q3 = quant16_32(v.w, ee);
+            }
+            h[tap * C4 + c4] = pack_hi4(q0, q1, q2, q3);
+            l[tap * C4 + c4] = pack_lo4(q0, q1, q2, q3);
+        }
+    }
+    for (int k = 9 * C4 + lane; k < K4; k += 64) { h[k] = PAD_HI4; l[k] = PAD_LO4; }
+}
+
+// k_epilogue (src/kernels.cu:70-95, 732-736): y = epi1 of the cuBLASLt-path plane sums (+ residual,
+// saturated). The output [M x N] is processed in spans of 1024 consecutive row-major elements, one
+// wave per span; per step lane l takes the four consecutive columns at element span + 256 j + 4 l
+// (N % 4 == 0, so they lie in one row), so each load/store instruction of a wave covers 1 KB.
+// With GN the span is also the region the statistics are gathered over, as in the reference: the
+// wave's sum/min/max per group go to a table of its own in LDS (each lane first merges its four
+// values by group) and are flushed to GnStat[(first row of the span / T) * 32 + group] when the
+// min is not INT_MAX (a span whose outputs of a group are all INT_MAX adds nothing).
+struct GnTable {
+    long long sum[32];
+    int mn[32], mx[32];
+};
+
 template <bool GN>
 __global__ void __launch_bounds__(256) epilogue_kernel(const int32_t* __restrict__ Chi, const int32_t* __restrict__ Clo, int M, int N, int ldc,
                                                        const int4* __restrict__ cst, const int32_t* __restrict__ e, int32_t* Y, int ldy,
                                                        const int32_t* R, GnStat* gs, int T) {
-    __shared__ long long gsum[32];
-    __shared__ int gmin[32], gmax[32];
-    if (GN) {
-        if (threadIdx.x < 32) { gsum[threadIdx.x] = 0; gmin[threadIdx.x] = INT_MAX; gmax[threadIdx.x] = INT_MIN; }
-        __syncthreads();
-    }
-    const int tpr = N >> 2;
-    const size_t idx = size_t(blockIdx.x) * 256 + threadIdx.x;
-    const bool live = idx < size_t(M) * tpr;
-    if (!GN && !live) return;
-    int r = 0, n = 0;
-    int y[4] = {0, 0, 0, 0};
-    if (live) {
-        r = int(idx / tpr);
-        n = int(idx - size_t(r) * tpr) * 4;
+    __shared__ GnTable tab[GN ? 4 : 1];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    GnTable& t = tab[GN ? wave : 0];
+    if (GN && lane < 32) { t.sum[lane] = 0; t.mn[lane] = INT_MAX; t.mx[lane] = INT_MIN; }
+    const unsigned long long total = (unsigned long long)M * unsigned(N);
+    const unsigned long long s0 = ((unsigned long long)blockIdx.x * 4 + wave) * 1024ull;
+    const int cg = N >> 5;
+    if (GN) __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const unsigned long long el = s0 + 256ull * j + 4ull * lane;
+        if (el >= total) break;
+        const int r = int(el / unsigned(N)), n = int(el - (unsigned long long)r * unsigned(N));
         const int er = e[r];
         const int4 hv = *reinterpret_cast<const int4*>(Chi + size_t(r) * ldc + n);
         const int4 lv = *reinterpret_cast<const int4*>(Clo + size_t(r) * ldc + n);
-        const int hh[4] = {hv.x, hv.y, hv.z, hv.w}, ll[4] = {lv.x, lv.y, lv.z, lv.w};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) { const int4 c = cst[n + j]; y[j] = epi1_exact(hh[j], ll[j], c.x, c.y, c.z, c.w, er); }
+        const int4 c0 = cst[n], c1 = cst[n + 1], c2 = cst[n + 2], c3 = cst[n + 3];
+        int y[4] = {epi1_exact(hv.x, lv.x, c0.x, c0.y, c0.z, c0.w, er), epi1_exact(hv.y, lv.y, c1.x, c1.y, c1.z, c1.w, er),
+                    epi1_exact(hv.z, lv.z, c2.x, c2.y, c2.z, c2.w, er), epi1_exact(hv.w, lv.w, c3.x, c3.y, c3.z, c3.w, er)};
         if (R) {
             const int4 rv = *reinterpret_cast<const int4*>(R + size_t(r) * ldy + n);
             y[0] = add_sat(y[0], rv.x); y[1] = add_sat(y[1], rv.y); y[2] = add_sat(y[2], rv.z); y[3] = add_sat(y[3], rv.w);
         }
         *reinterpret_cast<int4*>(Y + size_t(r) * ldy + n) = make_int4(y[0], y[1], y[2], y[3]);
-    }
-    if (GN) {
-        if (live) {
-            const int cg = N >> 5;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int g = (n + j) / cg;
-                atomicAdd(reinterpret_cast<unsigned long long*>(&gsum[g]), static_cast<unsigned long long>(static_cast<long long>(y[j])));
-                atomicMin(&gmin[g], y[j]);
-                atomicMax(&gmax[g], y[j]);
+        if constexpr (GN) {
+            // runs of equal group among the four columns: one atomic triple per run
+            int v = 0;
+            while (v < 4) {
+                const int g = (n + v) / cg;
+                long long sm = 0;
+                int mn = INT_MAX, mx = INT_MIN;
+                for (; v < 4 && (n + v) / cg == g; ++v) { sm += y[v]; mn = min(mn, y[v]); mx = max(mx, y[v]); }
+                atomicAdd(reinterpret_cast<unsigned long long*>(&t.sum[g]), static_cast<unsigned long long>(sm));
+                atomicMin(&t.mn[g], mn);
+                atomicMax(&t.mx[g], mx);
             }
         }
-        __syncthreads();
-        if (threadIdx.x < 32 && (gmin[threadIdx.x] != INT_MAX || gmax[threadIdx.x] != INT_MIN)) {
-            const int b = int(size_t(blockIdx.x) * 256 / size_t(tpr) / size_t(T));
-            GnStat* s = gs + b * 32 + threadIdx.x;
-            atomicAdd(reinterpret_cast<unsigned long long*>(&s->sum), static_cast<unsigned long long>(gsum[threadIdx.x]));
-            atomicMin(&s->mn, gmin[threadIdx.x]);
-            atomicMax(&s->mx, gmax[threadIdx.x]);
+    }
+    if constexpr (GN) {
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        if (s0 < total && lane < 32 && t.mn[lane] != INT_MAX) {
+            GnStat* d = gs + int((s0 / unsigned(N)) / unsigned(T)) * 32 + lane;
+            atomicAdd(reinterpret_cast<unsigned long long*>(&d->sum), static_cast<unsigned long long>(t.sum[lane]));
+            atomicMin(&d->mn, t.mn[lane]);
+            atomicMax(&d->mx, t.mx[lane]);
         }
     }
 }
@@ -236,19 +279,22 @@ hipError_t launch_pixmax(hipStream_t st, const int32_t* X, int rows, int C, uint
     return hipGetLastError();
 }
 hipError_t launch_conv_e(hipStream_t st, const uint32_t* pm, int B, int H, int W, int stride, int32_t* e) {
-    const int Ho = (H - 1) / stride + 1, Wo = (W - 1) / stride + 1, rows = B * Ho * Wo;
-    hipLaunchKernelGGL(conv_e_kernel, dim3(blocks_for(rows, 256)), dim3(256), 0, st, pm, B, H, W, stride, Ho, Wo, e);
+    const int Ho = (H - 1) / stride + 1, Wo = (W - 1) / stride + 1;
+    const int runs = int(blocks_for(Wo, conv_e_run(stride)));
+    const long long nb = (long long)B * Ho * runs;
+    if (nb > 0x7fffffffLL) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(conv_e_kernel, dim3(unsigned(nb)), dim3(256), 0, st, pm, H, W, stride, Ho, Wo, runs, e);
     return hipGetLastError();
 }
 hipError_t launch_im2col3(hipStream_t st, const int32_t* X, const uint32_t* pm, int B, int H, int W, int C, int stride, int8_t* hi, int8_t* lo,
                           int32_t* e, int Kp) {
     const int Ho = (H - 1) / stride + 1, Wo = (W - 1) / stride + 1, rows = B * Ho * Wo, Mp = (rows + 31) / 32 * 32;
-    hipLaunchKernelGGL(im2col3_kernel, dim3(unsigned(Mp)), dim3(256), 0, st, X, pm, B, H, W, C, stride, Ho, Wo, rows, hi, lo, e, Kp);
+    hipLaunchKernelGGL(im2col3_kernel, dim3(blocks_for(Mp, 4)), dim3(256), 0, st, X, pm, H, W, C, stride, Ho, Wo, rows, Mp, hi, lo, e, Kp);
     return hipGetLastError();
 }
 hipError_t launch_epilogue(hipStream_t st, const int32_t* Chi, const int32_t* Clo, int M, int N, int ldc, const int4* cst, const int32_t* e,
                            int32_t* Y, int ldy, const int32_t* R, GnStat* gs, int T) {
-    const dim3 grid(blocks_for(size_t(M) * (N / 4), 256));
+    const dim3 grid(unsigned((size_t(M) * N + 4095) / 4096));   // four 1024-element spans per block
     if (gs) hipLaunchKernelGGL(epilogue_kernel<true>, grid, dim3(256), 0, st, Chi, Clo, M, N, ldc, cst, e, Y, ldy, R, gs, T);
     else hipLaunchKernelGGL(epilogue_kernel<false>, grid, dim3(256), 0, st, Chi, Clo, M, N, ldc, cst, e, Y, ldy, R, gs, T);
     return hipGetLastError();

@@ -60,8 +60,9 @@ struct GemmParams {
     int mtiles, ntiles;
     // strided batch (EPI_RAW)
     long long sA, sW, sC;
-    // GroupNorm statistics of the output (EPI_PLAIN_GN): GnStat[sample * 32 + group], gnT rows per sample
-    GnStat* gnstat; int gnT;
+    // GroupNorm statistics of the output (EPI_PLAIN_GN): GnStat[sample * 32 + group], gnT rows per
+    // sample, gathered and flushed per gnBM x gnBN region (the reference's tile, 64 or 128 each)
+    GnStat* gnstat; int gnT, gnBM, gnBN;
     // EPI_QKV (src/gemm_hl.h:23-25): N = 3C, C = 64 heads; q/k head-quantised, v int32 into Y2
     int heads, qT, TpQ, TpK, qC;
     int8_t *qhi, *qlo, *khi, *klo;

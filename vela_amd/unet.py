@@ -7,7 +7,6 @@ used by two GEMMs at once.
 """
 from __future__ import annotations
 
-import numpy as np
 import torch
 
 from . import configs as cf
@@ -52,8 +51,8 @@ class GemmSet:
         kernel (the engine clears every rowmax buffer it allocates, src/engine.cu:161) and the GEMM.
         With reseed, residual layers first copy their seeded residual back into Y, so that every
         replay computes the same bytes (the parity tests); without it, Y accumulates in place from
-        replay to replay as the forward's residual stream does, and the graph holds only the GEMMs and
-        the rowmax fills (the timed C5 set)."""
+        replay to replay as the forward's residual stream does, and the graph holds only the GEMMs,
+        the rowmax fills and conv_in's pixel-max and im2col3 passes (the timed C5 set)."""
         self.run_eager()                      # first calls outside capture
         self.stream.synchronize()
         self.graph = vg.Graph(self.stream)
@@ -64,28 +63,3 @@ class GemmSet:
 
     def replay(self):
         self.graph.replay()
-
-    def check_layer(self, i: int, rows_per_block: int = 16, seed: int = 0) -> None:
-        """Bit-exact check of layer i on three row blocks (first, last and one seeded block; every
-        output row depends on its own A row only) against the CPU oracle."""
-        import oracle
-
-        p = self.probs[i]
-        L = p.L
-        h = cf.make_host(L)
-        if L.meta.get("conv_in"):
-            h = cf.unet_conv_in_operand(L, h)
-        r = np.random.default_rng(seed + i)
-        starts = sorted({0, max(0, L.M - rows_per_block), int(r.integers(0, max(1, L.M - rows_per_block)))})
-        y = p.y.cpu().numpy()
-        rm = p.rowmax.cpu().numpy().view(np.uint32) if p.rowmax is not None else None
-        for s0 in starts:
-            rows = (s0, min(L.M, s0 + rows_per_block))
-            want, wrm = oracle.layer_reference(L, h, rows=rows)
-            got = y[rows[0]:rows[1]]
-            exp = want[rows[0]:rows[1]]
-            if not np.array_equal(got, exp):
-                bad = np.argwhere(got != exp)[0]
-                raise AssertionError(f"layer {i} {L.name}: rows {rows} mismatch at {tuple(bad)}: {got[tuple(bad)]} != {exp[tuple(bad)]}")
-            if rm is not None and not np.array_equal(rm[rows[0]:rows[1]], wrm[rows[0]:rows[1]]):
-                raise AssertionError(f"layer {i} {L.name}: rowmax mismatch in rows {rows}")
