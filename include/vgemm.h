@@ -89,6 +89,17 @@ void vgemm_aepi_init(VgemmAEpi* e);
 int vgemm_hl2(void* stream, const VgemmASrc* A, int Mp, int Mreal, const int8_t* W, int ldw, int Np, int Nreal,
               int Kp, const int32_t* cst, const VgemmAEpi* E);
 
+/* No counterpart in the reference: vgemm_hl2 for callers that cannot allocate device memory (code
+ * under stream capture, tight serving loops, harnesses that forbid hipMalloc). Same arguments, same
+ * results; AEpi.ws / ws_bytes are ignored and the split-K partials go to a static device workspace
+ * of VGEMM_NOALLOC_WS_BYTES (64 MiB) that each GPU holds until the process ends. A call whose split
+ * would need more returns VGEMM_ERR_UNSUPPORTED (no BASELINE or UNet shape does: the largest needs
+ * 60 MiB). Every call on one GPU shares that GPU's workspace: calls that overlap on one GPU (other
+ * streams, other threads) race. No hipMalloc, hipFree or allocating library call is made. */
+#define VGEMM_NOALLOC_WS_BYTES ((size_t)64 << 20)
+int vgemm_hl2_noalloc(void* stream, const VgemmASrc* A, int Mp, int Mreal, const int8_t* W, int ldw, int Np, int Nreal,
+                      int Kp, const int32_t* cst, const VgemmAEpi* E);
+
 /* meow::k_gemm_hl (src/gemm_hl.h:30-33, src/gemm_hl.cu:371-376): SRC_I8 planes + epilogue. */
 int vgemm_hl(void* stream, const int8_t* Ahi, const int8_t* Alo, int lda, int Mp, int Mreal,
              const int8_t* W, int ldw, int Np, int Nreal, int Kp, const int32_t* cst, const int32_t* e,

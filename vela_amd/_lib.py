@@ -76,6 +76,7 @@ SIGNATURES = [
     ("vgemm_asrc_init", None, [ctypes.POINTER(ASrc)]),
     ("vgemm_aepi_init", None, [ctypes.POINTER(AEpi)]),
     ("vgemm_hl2", I, [P, ctypes.POINTER(ASrc), I, I, P, I, I, I, I, P, ctypes.POINTER(AEpi)]),
+    ("vgemm_hl2_noalloc", I, [P, ctypes.POINTER(ASrc), I, I, P, I, I, I, I, P, ctypes.POINTER(AEpi)]),
     ("vgemm_hl", I, [P, P, P, I, I, I, P, I, I, I, I, P, P, P, I, P, I, I, P, P, P]),
     ("vgemm_conv_e", I, [P, P, I, I, I, I, P]),
     ("vgemm_supported", I, [I, I, I]),

@@ -4,7 +4,9 @@
 #include <cstdarg>
 #include <cstdio>
 #include <algorithm>
+#include <atomic>
 #include <cstring>
+#include <mutex>
 #include <string>
 
 #include "../../include/vgemm.h"
@@ -229,8 +231,21 @@ size_t vgemm_workspace_bytes(int Mp, int Mreal, int Np, int Nreal, int Kp, int e
     return nb;
 }
 
-int vgemm_hl2(void* stream, const VgemmASrc* A, int Mp, int Mreal, const int8_t* W, int ldw, int Np, int Nreal, int Kp,
-              const int32_t* cst, const VgemmAEpi* E) {
+}  // extern "C"
+
+namespace {
+
+// Where the split-K partials of a call go: the caller's workspace (AEpi.ws; a call whose split would
+// not fit runs unsplit), or the library's static scratch (the call is rejected if its split would
+// not fit).
+struct WsPolicy {
+    void* ws;
+    size_t bytes;
+    bool strict;
+};
+
+int hl2_impl(void* stream, const VgemmASrc* A, int Mp, int Mreal, const int8_t* W, int ldw, int Np, int Nreal, int Kp,
+             const int32_t* cst, const VgemmAEpi* E, WsPolicy wsp) {
     if (!A || !E) return fail(VGEMM_ERR_ARG, "gemm_hl: null ASrc/AEpi");
     if (!vgemm_supported(Mp, Np, Kp)) return fail(VGEMM_ERR_ARG, "gemm_hl: unsupported shape (Mp %d, Np %d, Kp %d)", Mp, Np, Kp);
     if (Mreal < 0 || Mreal > Mp || Nreal < 0 || Nreal > Np) return fail(VGEMM_ERR_ARG, "gemm_hl: Mreal/Nreal outside Mp/Np");
@@ -369,8 +384,13 @@ int vgemm_hl2(void* stream, const VgemmASrc* A, int Mp, int Mreal, const int8_t*
     p.ntiles = cdiv(Nreal, BN);
     const int nK = halo_bm ? p.C / 64 : (Kp + 63) / 64;
     // the split-K epilogue pass carries neither the QKV layout nor the GroupNorm statistics
-    int splits = E->ws && epi != VGEMM_EPI_QKV && !E->gnstat ? pick_splitk(variant, Mreal, Nreal, Kp) : 1;
-    if (splits > 1 && ws_bytes_for(variant, Mreal, Nreal, splits) > E->ws_bytes) splits = 1;
+    int splits = wsp.ws && epi != VGEMM_EPI_QKV && !E->gnstat ? pick_splitk(variant, Mreal, Nreal, Kp) : 1;
+    if (splits > 1 && ws_bytes_for(variant, Mreal, Nreal, splits) > wsp.bytes) {
+        if (wsp.strict)
+            return fail(VGEMM_ERR_UNSUPPORTED, "gemm_hl_noalloc: the split-K partials of this call need %zu bytes; the static workspace holds %zu",
+                        ws_bytes_for(variant, Mreal, Nreal, splits), wsp.bytes);
+        splits = 1;
+    }
     if (splits > nK) splits = nK;
     auto run = [&](int e) {
         if (halo_bm) return hip_status(vk::launch_gemm_conv16_halo(halo_bm, e, p, st), "gemm_hl halo conv launch");
@@ -380,16 +400,65 @@ int vgemm_hl2(void* stream, const VgemmASrc* A, int Mp, int Mreal, const int8_t*
         p.ksplit = 1; p.kper = nK;
         return run(p.gnstat ? vk::EPI_PLAIN_GN : epi);
     }
-    if (!aligned16(E->ws)) return fail(VGEMM_ERR_ARG, "gemm_hl: workspace must be 16-byte aligned");
+    if (!aligned16(wsp.ws)) return fail(VGEMM_ERR_ARG, "gemm_hl: workspace must be 16-byte aligned");
     p.ksplit = splits;
     p.kper = (nK + splits - 1) / splits;
     p.ksplit = (nK + p.kper - 1) / p.kper;
-    p.ws = static_cast<int32_t*>(E->ws);
+    p.ws = static_cast<int32_t*>(wsp.ws);
     p.ws_rows = p.mtiles * BM;
     p.ws_ld = p.ntiles * BN;
     const int rc = run(vk::EPI_PARTIAL);
     if (rc) return rc;
     return hip_status(vk::launch_splitk_epilogue(epi, p, st), "gemm_hl split-K epilogue");
+}
+
+// ---- the allocation-free entry point's workspace
+// A file-scope device array serves as the split-K workspace of vgemm_hl2_noalloc. Each GPU the
+// library runs on holds its own copy for the life of the process. In host code the name `scratch`
+// is not a device address: its address on the current device comes from hipGetSymbolAddress, taken
+// once per device (scratch_on_current_device) and used everywhere host code refers to it. The
+// partial pass writes every element of its tiles in every K range before the reduction reads them,
+// so nothing in it has to start at zero; concurrent calls on one GPU share it and race.
+static __device__ __align__(256) unsigned char scratch[VGEMM_NOALLOC_WS_BYTES];
+
+constexpr int SCRATCH_MAX_DEVICES = 64;
+std::atomic<void*> g_scratch_dev[SCRATCH_MAX_DEVICES];
+std::mutex g_scratch_mu;
+
+int scratch_on_current_device(void** out) {
+    int dev = -1;
+    const hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_status(e, "hipGetDevice");
+    if (dev < 0 || dev >= SCRATCH_MAX_DEVICES) return fail(VGEMM_ERR_UNSUPPORTED, "gemm_hl_noalloc: device %d out of range", dev);
+    void* ptr = g_scratch_dev[dev].load(std::memory_order_acquire);
+    if (!ptr) {
+        std::lock_guard<std::mutex> lock(g_scratch_mu);
+        ptr = g_scratch_dev[dev].load(std::memory_order_relaxed);
+        if (!ptr) {
+            const hipError_t ge = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+            if (ge != hipSuccess || !ptr) return fail(VGEMM_ERR_HIP, "gemm_hl_noalloc: hipGetSymbolAddress(scratch): %s", hipGetErrorString(ge));
+            g_scratch_dev[dev].store(ptr, std::memory_order_release);
+        }
+    }
+    *out = ptr;
+    return VGEMM_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int vgemm_hl2(void* stream, const VgemmASrc* A, int Mp, int Mreal, const int8_t* W, int ldw, int Np, int Nreal, int Kp,
+              const int32_t* cst, const VgemmAEpi* E) {
+    return hl2_impl(stream, A, Mp, Mreal, W, ldw, Np, Nreal, Kp, cst, E, WsPolicy{E ? E->ws : nullptr, E ? E->ws_bytes : 0, false});
+}
+
+int vgemm_hl2_noalloc(void* stream, const VgemmASrc* A, int Mp, int Mreal, const int8_t* W, int ldw, int Np, int Nreal, int Kp,
+                      const int32_t* cst, const VgemmAEpi* E) {
+    void* ws = nullptr;
+    const int rc = scratch_on_current_device(&ws);
+    if (rc) return rc;
+    return hl2_impl(stream, A, Mp, Mreal, W, ldw, Np, Nreal, Kp, cst, E, WsPolicy{ws, VGEMM_NOALLOC_WS_BYTES, true});
 }
 
 int vgemm_hl(void* stream, const int8_t* Ahi, const int8_t* Alo, int lda, int Mp, int Mreal, const int8_t* W, int ldw, int Np, int Nreal,

@@ -51,6 +51,16 @@ def k_gemm_hl2(A: ASrc, Mp: int, Mreal: int, W, ldw: int, Np: int, Nreal: int, K
     check(load().vgemm_hl2(stream_ptr(stream), ctypes.byref(A), Mp, Mreal, ptr(W), ldw, Np, Nreal, Kp, ptr(cst), ctypes.byref(E)))
 
 
+NOALLOC_WS_BYTES = 64 << 20
+
+
+def k_gemm_hl2_noalloc(A: ASrc, Mp: int, Mreal: int, W, ldw: int, Np: int, Nreal: int, Kp: int, cst, E: AEpi, stream=None) -> None:
+    """vgemm_hl2 with the split-K partials in the library's static device workspace (no allocation;
+    AEpi.ws is ignored; calls that overlap on one GPU race)."""
+    check(load().vgemm_hl2_noalloc(stream_ptr(stream), ctypes.byref(A), Mp, Mreal, ptr(W), ldw, Np, Nreal, Kp, ptr(cst),
+                                   ctypes.byref(E)))
+
+
 def k_gemm_hl(Ahi, Alo, lda: int, Mp: int, Mreal: int, W, ldw: int, Np: int, Nreal: int, Kp: int, cst, e, Y, ldy: int,
               residual=None, epi: int = EPI_PLAIN, Cs: int = 0, Y1=None, Y2=None, Lphi=None, stream=None) -> None:
     """meow::k_gemm_hl (src/gemm_hl.h:30-33)."""
