@@ -18,11 +18,18 @@
 //    (checked from max |m| 2^-s and max |b|). Then y = (A m + C) >> s with A = 256 Chi + Clo
 //    (int32, Kp <= 496) and C = 128 wsum m + 2^(s-1) + b 2^s, one v_mad_i64_i32 and one funnel
 //    shift; GELU/GEGLU take phi(g) from the table as (1024 L[i] + (L[i+1] - L[i]) f) >> 10, then
-//    ge = (g phi + 2^15) >> 16 (never saturates, phi <= 65536) and y = sat32((a ge + 2^15) >> 16),
-//    the saturation being detected per wave and handled on a separate branch.
+//    ge = (g phi + 2^15) >> 16 (never saturates, phi <= 65536) and y = sat32((a ge + 2^15) >> 16).
 //  * otherwise the reference's int64 formula element by element (one element per loop iteration,
 //    so that this rarely used form adds few registers to the kernel). The host sends calls with
 //    per-row shifts to the tile kernels, whose FP64 form covers them at speed.
+//
+// Chunk loop of the integer form (calls without a residual): software-pipelined. Chunk c's MFMAs run
+// in two halves (one 32-column subtile each), interleaved instruction by instruction with the
+// requantising epilogue of chunk c - 1, whose plane sums were folded into one int32 per element
+// (256 Chi + Clo) when its MFMAs finished; the epilogue has no branch (a saturating GEGLU product is
+// clamped per element), so each half is one scheduling region ordered as one MFMA, a few VALU
+// instructions and one LDS read, repeated. The int64 form and residual calls keep the plain loop:
+// a chunk's MFMAs, then its epilogue.
 //
 // Memory ordering: the W DMA of chunk c + 1 is issued right after the barrier of chunk c, and the
 // only vector-memory instructions after it in chunk c are that chunk's output stores, a fixed
@@ -329,194 +336,351 @@ __global__ void __launch_bounds__(256, 2) stripe_kernel(const GemmParams p) {
         return int(__builtin_amdgcn_alignbit(unsigned(u64(t) >> 32), unsigned(u64(t)), unsigned(k.y)));
     };
 
-    for (int c = cb; c < ce; ++c) {
-        const int stage = (c - cb) & 1;
-        // chunk c's DMA is done once at most the previous chunk's stores are outstanding
-        if (c > cb && lean) vm_wait<STORES>();
-        else vm_wait<0>();
-        block_barrier();
-        if (c + 1 < ce) issue(c + 1, stage ^ 1);
-
-        v16i acc_h[S::NSUB], acc_l[S::NSUB];
+    bool pipelined = false;
+    if constexpr (!RES) {
+        if (form == FORM_INT) {
+            pipelined = true;
+            // ---- software-pipelined chunk loop (integer form). The MFMAs of chunk c run interleaved
+            // with the requantising epilogue of chunk c - 1, so that the matrix core and the VALU work
+            // at the same time inside each wave. When a chunk's MFMAs finish, its two plane sums are
+            // folded into one int32 per element, X = 256 Chi + Clo (exact: Kp <= 320), which frees the
+            // accumulators for the next chunk; the epilogue has no branch (GEGLU products that
+            // saturate are clamped per element), so the whole chunk body is one scheduling region.
+            int X[2][16];
+            v16i acc_h[S::NSUB], acc_l[S::NSUB];
+            const v16i vzero = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+            // the MFMAs of K step t of the chunk in LDS stage `stage`
+            auto mfma_step = [&](const unsigned char* sW, int t) __attribute__((always_inline)) {
 #pragma unroll
-        for (int u = 0; u < S::NSUB; ++u)
+                for (int u = 0; u < S::NSUB; ++u) {
+                    const v4i wf = *reinterpret_cast<const v4i*>(sW + (t >> 1) * S::KSTEP + swz(32 * u + lc, 2 * (t & 1) + lh));
+                    acc_h[u] = __builtin_amdgcn_mfma_i32_32x32x32_i8(hf[t], wf, t ? acc_h[u] : vzero, 0, 0, 0);
+                    acc_l[u] = __builtin_amdgcn_mfma_i32_32x32x32_i8(lf[t], wf, t ? acc_l[u] : vzero, 0, 0, 0);
+                }
+            };
+            auto mfma_chunk = [&](int stage) __attribute__((always_inline)) {
 #pragma unroll
-            for (int i = 0; i < 16; ++i) { acc_h[u][i] = 0; acc_l[u][i] = 0; }
-        const unsigned char* sW = sh.w[stage];
-        // all ten K steps: past Kp both operands hold zeros (A registers cleared, W bytes out of range).
-        // The W fragments of step t + 2 are read from LDS before the MFMAs of step t, so that their
-        // latency hides behind four MFMAs of this wave.
-        auto wfrag = [&](int t, int u) -> v4i {
-            return *reinterpret_cast<const v4i*>(sW + (t >> 1) * S::KSTEP + swz(32 * u + lc, 2 * (t & 1) + lh));
-        };
-        constexpr int PF = 2;
-        v4i wq[PF][S::NSUB];
+                for (int t = 0; t < NKS; ++t) mfma_step(sh.w[stage], t);
+            };
+            auto fold = [&]() __attribute__((always_inline)) {
 #pragma unroll
-        for (int t = 0; t < PF; ++t)
+                for (int u = 0; u < S::NSUB; ++u)
 #pragma unroll
-            for (int u = 0; u < S::NSUB; ++u) wq[t][u] = wfrag(t, u);
-        __builtin_amdgcn_sched_group_barrier(0x100, PF * S::NSUB, 0);
+                    for (int i = 0; i < 16; ++i) X[u][i] = (acc_h[u][i] << 8) + acc_l[u][i];
+            };
+            // per-chunk constants of the epilogue of the chunk held in X: table entries of the lane's
+            // column(s) and the byte offset of its first output (OOB past the output's columns)
+            struct EpiC { int4 ka[NOUT], kg; unsigned vbase[NOUT]; };
+            auto epi_consts = [&](int tb, int ocol0) __attribute__((always_inline)) {
+                EpiC k;
 #pragma unroll
-        for (int t = 0; t < NKS; ++t) {
-            v4i wf[S::NSUB];
-#pragma unroll
-            for (int u = 0; u < S::NSUB; ++u) {
-                wf[u] = wq[t % PF][u];
-                if (t + PF < NKS) wq[t % PF][u] = wfrag(t + PF, u);
-            }
-#pragma unroll
-            for (int u = 0; u < S::NSUB; ++u) {
-                acc_h[u] = __builtin_amdgcn_mfma_i32_32x32x32_i8(hf[t], wf[u], acc_h[u], 0, 0, 0);
-                acc_l[u] = __builtin_amdgcn_mfma_i32_32x32x32_i8(lf[t], wf[u], acc_l[u], 0, 0, 0);
-            }
-            // keep that order in the schedule: the reads of step t + 2, then the MFMAs of step t
-            if (t + PF < NKS) __builtin_amdgcn_sched_group_barrier(0x100, S::NSUB, 0);
-            __builtin_amdgcn_sched_group_barrier(0x008, 2 * S::NSUB, 0);
-        }
-
-        // ---- epilogue of chunk c: output subtile u is table rows tb + 32u + lc (GEGLU: a columns,
-        // g columns 32 further), output column ocol0 + 32u + lc
-        const int tb = (c - cb) * CH;
-        const int ocol0 = GEGLU ? c * (CH / 2) : c * CH;
-#pragma unroll
-        for (int u = 0; u < NOUT; ++u) {
-            const int ncol = ocol0 + 32 * u + lc;
-            const bool cok = ncol < nlim;
-            // byte offset of the lane's row rbase + 4 lh and column; + slot rows below. Rows at or past
-            // Mreal land at or past the end of the Y buffer and columns past the output at OOB, so the
-            // hardware drops those stores (and residual loads read zeros there)
-            const unsigned vbase = cok ? rowoff + unsigned(ncol) * 4u : OOB;
-            if (form == FORM_INT) {
-                const int4 ka = sh.tab[tb + 32 * u + lc];
-                const int4 kg = sh.tab[tb + (GEGLU ? 32 : 32 * u) + lc];
-                // GEGLU of element i, biased (y ^ 2^31); hi = the high word of a ge + 2^15, plus 2^15
-                auto geglu = [&](int i, unsigned& hi) -> unsigned {
-                    const int ya = req((acc_h[0][i] << 8) + acc_l[0][i], ka);
-                    const int yg = req((acc_h[1][i] << 8) + acc_l[1][i], kg);
+                for (int u = 0; u < NOUT; ++u) {
+                    const int ncol = ocol0 + 32 * u + lc;
+                    k.vbase[u] = ncol < nlim ? rowoff + unsigned(ncol) * 4u : OOB;
+                    k.ka[u] = sh.tab[tb + 32 * u + lc];
+                }
+                k.kg = GEGLU ? sh.tab[tb + 32 + lc] : k.ka[0];
+                return k;
+            };
+            // output o = 16 u + i of the chunk held in X: requantise, store, row maximum
+            auto epi_one = [&](const EpiC& k, int o, auto rmax, auto full) __attribute__((always_inline)) {
+                constexpr bool RMAX = decltype(rmax)::value, FULL = decltype(full)::value;
+                const int u = o >> 4, i = o & 15;
+                int y;
+                if constexpr (GEGLU) {
+                    const int yg = req(X[1][i], k.kg);
                     unsigned h0;
                     const int ge = mulsh16(yg, phi(yg), h0);
-                    return mulsh16b(ya, ge, hi);
-                };
-                // FULL: every row of the block is below Mreal. Then a store's row offset (uniform)
-                // goes in the instruction's scalar offset and its vector offset is the lane's base:
-                // in range exactly when the column is (OOB otherwise), whether or not the hardware
-                // range check counts the scalar offset. Otherwise each element's full offset is in
-                // the vector offset, so that rows at or past Mreal fall outside the buffer.
-                auto run = [&](auto hasr, auto rmax, auto full) {
-                    constexpr bool HASR = decltype(hasr)::value, RMAX = decltype(rmax)::value;
-                    constexpr bool FULL = decltype(full)::value;
-                    // EB elements at a time: their values first, with no branch between them, so
-                    // that their dependency chains (64-bit products, table lookups) interleave; then
-                    // their stores
+                    // (ya ge + 2^15) >> 16 with 2^47 added: hb is the high word + 2^15, at most 65535
+                    // exactly when y fits in int32; otherwise y saturates to the product's sign
+                    unsigned hb;
+                    const unsigned yb = mulsh16b(req(X[0][i], k.ka[0]), ge, hb);
+                    asm("" : "+v"(hb));   // keep the tests on the 32-bit high word
+                    const int sat = (int(hb) >> 31) ^ 0x7fffffff;
+                    y = hb > 65535u ? sat : int(yb ^ 0x80000000u);
+                } else if constexpr (EPI == EPI_GELU) {
+                    const int ya = req(X[u][i], k.ka[u]);
+                    unsigned h0;
+                    y = mulsh16(ya, phi(ya), h0);
+                } else {
+                    y = req(X[u][i], k.ka[u]);
+                }
+                const unsigned soff = unsigned(8 * (i >> 2) + (i & 3)) * ldy4;
+                __builtin_amdgcn_raw_buffer_store_b32(y, rY, int(FULL ? k.vbase[u] : k.vbase[u] + soff), FULL ? int(soff) : 0, 0);
+                if constexpr (RMAX) yabs[i] = int(max(unsigned(yabs[i]), unsigned(max(y, int(0u - unsigned(y))))));
+            };
+            auto epilogue = [&](int tb, int ocol0, auto rmax, auto full) __attribute__((always_inline)) {
+                const EpiC k = epi_consts(tb, ocol0);
 #pragma unroll
-                    for (int i0 = 0; i0 < 16; i0 += EB) {
-                        int yv[EB];        // GEGLU: biased, y ^ 2^31
-                        int rv[HASR ? EB : 1];
-                        if constexpr (HASR) {
-                            // the batch's residuals first, so that their latency hides behind its arithmetic
+                for (int o = 0; o < NOUT * 16; ++o) epi_one(k, o, rmax, full);
+            };
+            // One chunk body in two halves, one per 32-column MFMA subtile u: K step t's two MFMAs of
+            // subtile u, then the previous chunk's outputs assigned to that step, each step ordered
+            // as one MFMA, VPM VALU instructions and one LDS read, twice. Half u takes the previous
+            // chunk's outputs that are done with X[.][i] for the elements whose registers the fold
+            // of subtile u then reuses (GEGLU: outputs 8u..8u+7, which read X[0][i] and X[1][i];
+            // otherwise: the 16 outputs of subtile u), so only one subtile's accumulators are live.
+            // W fragments are read PFB steps ahead of their MFMAs.
+            constexpr int NO = NOUT * 16, NOH = NO / 2;
+            constexpr int VPM = GEGLU ? 10 : (EPI == EPI_GELU ? 7 : 4);
+            constexpr int PFB = 2;
+            auto wfrag = [&](const unsigned char* sW, int t, int u) __attribute__((always_inline)) {
+                return *reinterpret_cast<const v4i*>(sW + (t >> 1) * S::KSTEP + swz(32 * u + lc, 2 * (t & 1) + lh));
+            };
+            auto body = [&](int stage, int tbp, int ocp, auto rmax, auto full) __attribute__((always_inline)) {
+                const unsigned char* sW = sh.w[stage];
+                const EpiC k = epi_consts(tbp, ocp);
+                int Xn[S::NSUB][16];
 #pragma unroll
+                for (int u = 0; u < S::NSUB; ++u) {
+                    v4i wq[PFB];
+#pragma unroll
+                    for (int t = 0; t < PFB; ++t) wq[t] = wfrag(sW, t, u);
+                    v16i ah, al;
+#pragma unroll
+                    for (int t = 0; t < NKS; ++t) {
+                        const v4i wf = wq[t % PFB];
+                        if (t + PFB < NKS) wq[t % PFB] = wfrag(sW, t + PFB, u);
+                        ah = __builtin_amdgcn_mfma_i32_32x32x32_i8(hf[t], wf, t ? ah : vzero, 0, 0, 0);
+                        al = __builtin_amdgcn_mfma_i32_32x32x32_i8(lf[t], wf, t ? al : vzero, 0, 0, 0);
+#pragma unroll
+                        for (int o = u * NOH + t * NOH / NKS; o < u * NOH + (t + 1) * NOH / NKS; ++o) {
+                            // GEGLU output o reads X[0][o], X[1][o]; the others X[o >> 4][o & 15]
+                            epi_one(k, o, rmax, full);
+                        }
+#pragma unroll
+                        for (int q = 0; q < 2; ++q) {
+                            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                            __builtin_amdgcn_sched_group_barrier(0x002, VPM, 0);
+                            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                        }
+                    }
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) Xn[u][i] = (ah[i] << 8) + al[i];
+                }
+#pragma unroll
+                for (int u = 0; u < S::NSUB; ++u)
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) X[u][i] = Xn[u][i];
+            };
+            auto run = [&](auto rmax, auto full) __attribute__((always_inline)) {
+                // the first chunk: MFMAs alone
+                vm_wait<0>();
+                block_barrier();
+                if (cb + 1 < ce) issue(cb + 1, 1);
+                mfma_chunk(0);
+                fold();
+                for (int c = cb + 1; c < ce; ++c) {
+                    const int stage = (c - cb) & 1;
+                    // chunk c's DMA is done once at most the previous chunk body's stores are outstanding
+                    if (c == cb + 1) vm_wait<0>();
+                    else vm_wait<STORES>();
+                    block_barrier();
+                    if (c + 1 < ce) issue(c + 1, stage ^ 1);
+                    body(stage, (c - 1 - cb) * CH, GEGLU ? (c - 1) * (CH / 2) : (c - 1) * CH, rmax, full);
+                }
+                epilogue((ce - 1 - cb) * CH, GEGLU ? (ce - 1) * (CH / 2) : (ce - 1) * CH, rmax, full);
+            };
+            const bool full = m0 + BM <= p.Mreal;
+            if (p.rowmax) {
+                if (full) run(std::true_type{}, std::true_type{});
+                else run(std::true_type{}, std::false_type{});
+            } else {
+                if (full) run(std::false_type{}, std::true_type{});
+                else run(std::false_type{}, std::false_type{});
+            }
+        }
+    }
+    if (!pipelined) {
+        for (int c = cb; c < ce; ++c) {
+            const int stage = (c - cb) & 1;
+            // chunk c's DMA is done once at most the previous chunk's stores are outstanding
+            if (c > cb && lean) vm_wait<STORES>();
+            else vm_wait<0>();
+            block_barrier();
+            if (c + 1 < ce) issue(c + 1, stage ^ 1);
+
+            v16i acc_h[S::NSUB], acc_l[S::NSUB];
+    #pragma unroll
+            for (int u = 0; u < S::NSUB; ++u)
+    #pragma unroll
+                for (int i = 0; i < 16; ++i) { acc_h[u][i] = 0; acc_l[u][i] = 0; }
+            const unsigned char* sW = sh.w[stage];
+            // all ten K steps: past Kp both operands hold zeros (A registers cleared, W bytes out of range).
+            // The W fragments of step t + 2 are read from LDS before the MFMAs of step t, so that their
+            // latency hides behind four MFMAs of this wave.
+            auto wfrag = [&](int t, int u) -> v4i {
+                return *reinterpret_cast<const v4i*>(sW + (t >> 1) * S::KSTEP + swz(32 * u + lc, 2 * (t & 1) + lh));
+            };
+            constexpr int PF = 2;
+            v4i wq[PF][S::NSUB];
+    #pragma unroll
+            for (int t = 0; t < PF; ++t)
+    #pragma unroll
+                for (int u = 0; u < S::NSUB; ++u) wq[t][u] = wfrag(t, u);
+            __builtin_amdgcn_sched_group_barrier(0x100, PF * S::NSUB, 0);
+    #pragma unroll
+            for (int t = 0; t < NKS; ++t) {
+                v4i wf[S::NSUB];
+    #pragma unroll
+                for (int u = 0; u < S::NSUB; ++u) {
+                    wf[u] = wq[t % PF][u];
+                    if (t + PF < NKS) wq[t % PF][u] = wfrag(t + PF, u);
+                }
+    #pragma unroll
+                for (int u = 0; u < S::NSUB; ++u) {
+                    acc_h[u] = __builtin_amdgcn_mfma_i32_32x32x32_i8(hf[t], wf[u], acc_h[u], 0, 0, 0);
+                    acc_l[u] = __builtin_amdgcn_mfma_i32_32x32x32_i8(lf[t], wf[u], acc_l[u], 0, 0, 0);
+                }
+                // keep that order in the schedule: the reads of step t + 2, then the MFMAs of step t
+                if (t + PF < NKS) __builtin_amdgcn_sched_group_barrier(0x100, S::NSUB, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, 2 * S::NSUB, 0);
+            }
+
+            // ---- epilogue of chunk c: output subtile u is table rows tb + 32u + lc (GEGLU: a columns,
+            // g columns 32 further), output column ocol0 + 32u + lc
+            const int tb = (c - cb) * CH;
+            const int ocol0 = GEGLU ? c * (CH / 2) : c * CH;
+    #pragma unroll
+            for (int u = 0; u < NOUT; ++u) {
+                const int ncol = ocol0 + 32 * u + lc;
+                const bool cok = ncol < nlim;
+                // byte offset of the lane's row rbase + 4 lh and column; + slot rows below. Rows at or past
+                // Mreal land at or past the end of the Y buffer and columns past the output at OOB, so the
+                // hardware drops those stores (and residual loads read zeros there)
+                const unsigned vbase = cok ? rowoff + unsigned(ncol) * 4u : OOB;
+                if (form == FORM_INT) {
+                    const int4 ka = sh.tab[tb + 32 * u + lc];
+                    const int4 kg = sh.tab[tb + (GEGLU ? 32 : 32 * u) + lc];
+                    // GEGLU of element i, biased (y ^ 2^31); hi = the high word of a ge + 2^15, plus 2^15
+                    auto geglu = [&](int i, unsigned& hi) -> unsigned {
+                        const int ya = req((acc_h[0][i] << 8) + acc_l[0][i], ka);
+                        const int yg = req((acc_h[1][i] << 8) + acc_l[1][i], kg);
+                        unsigned h0;
+                        const int ge = mulsh16(yg, phi(yg), h0);
+                        return mulsh16b(ya, ge, hi);
+                    };
+                    // FULL: every row of the block is below Mreal. Then a store's row offset (uniform)
+                    // goes in the instruction's scalar offset and its vector offset is the lane's base:
+                    // in range exactly when the column is (OOB otherwise), whether or not the hardware
+                    // range check counts the scalar offset. Otherwise each element's full offset is in
+                    // the vector offset, so that rows at or past Mreal fall outside the buffer.
+                    auto run = [&](auto hasr, auto rmax, auto full) {
+                        constexpr bool HASR = decltype(hasr)::value, RMAX = decltype(rmax)::value;
+                        constexpr bool FULL = decltype(full)::value;
+                        // EB elements at a time: their values first, with no branch between them, so
+                        // that their dependency chains (64-bit products, table lookups) interleave; then
+                        // their stores
+    #pragma unroll
+                        for (int i0 = 0; i0 < 16; i0 += EB) {
+                            int yv[EB];        // GEGLU: biased, y ^ 2^31
+                            int rv[HASR ? EB : 1];
+                            if constexpr (HASR) {
+                                // the batch's residuals first, so that their latency hides behind its arithmetic
+    #pragma unroll
+                                for (int j = 0; j < EB; ++j) {
+                                    const int i = i0 + j;
+                                    const unsigned soff = unsigned(8 * (i >> 2) + (i & 3)) * ldy4;
+                                    rv[j] = int(__builtin_amdgcn_raw_buffer_load_b32(rR, int(FULL ? vbase : vbase + soff), FULL ? int(soff) : 0, 0));
+                                }
+                            }
+                            unsigned hv[GEGLU ? EB : 1];
+                            unsigned ov = 0;   // OR of the biased high words: > 65535 iff one overflows
+    #pragma unroll
+                            for (int j = 0; j < EB; ++j) {
+                                const int i = i0 + j;
+                                if constexpr (GEGLU) {
+                                    yv[j] = int(geglu(i, hv[j]));
+                                    // opaque to the compiler, so that the tests below stay on the 32-bit
+                                    // high word (not on a 64-bit product kept alive for them)
+                                    asm volatile("" : "+v"(hv[j]));
+                                    ov |= hv[j];
+                                } else if constexpr (EPI == EPI_GELU) {
+                                    const int ya = req((acc_h[u][i] << 8) + acc_l[u][i], ka);
+                                    unsigned h0;
+                                    yv[j] = mulsh16(ya, phi(ya), h0);
+                                } else {
+                                    yv[j] = req((acc_h[u][i] << 8) + acc_l[u][i], ka);
+                                }
+                            }
+                            if constexpr (GEGLU) {
+                                // |a ge| >= 2^47 for an element of the wave: that result saturates. Rarely
+                                // taken; the overflowing elements are replaced.
+                                if (__builtin_amdgcn_ballot_w64(ov > 65535u)) {
+                                    asm volatile("; saturating GEGLU product");
+                                    // the sign of the product is the sign bit of the biased high word;
+                                    // the biased saturated value is ~0 (INT_MAX) or 0 (INT_MIN)
+    #pragma unroll
+                                    for (int j = 0; j < EB; ++j)
+                                        if (hv[j] > 65535u) yv[j] = ~(int(hv[j]) >> 31);
+                                }
+                            }
+    #pragma unroll
                             for (int j = 0; j < EB; ++j) {
                                 const int i = i0 + j;
                                 const unsigned soff = unsigned(8 * (i >> 2) + (i & 3)) * ldy4;
-                                rv[j] = int(__builtin_amdgcn_raw_buffer_load_b32(rR, int(FULL ? vbase : vbase + soff), FULL ? int(soff) : 0, 0));
-                            }
-                        }
-                        unsigned hv[GEGLU ? EB : 1];
-                        unsigned ov = 0;   // OR of the biased high words: > 65535 iff one overflows
-#pragma unroll
-                        for (int j = 0; j < EB; ++j) {
-                            const int i = i0 + j;
-                            if constexpr (GEGLU) {
-                                yv[j] = int(geglu(i, hv[j]));
-                                // opaque to the compiler, so that the tests below stay on the 32-bit
-                                // high word (not on a 64-bit product kept alive for them)
-                                asm volatile("" : "+v"(hv[j]));
-                                ov |= hv[j];
-                            } else if constexpr (EPI == EPI_GELU) {
-                                const int ya = req((acc_h[u][i] << 8) + acc_l[u][i], ka);
-                                unsigned h0;
-                                yv[j] = mulsh16(ya, phi(ya), h0);
-                            } else {
-                                yv[j] = req((acc_h[u][i] << 8) + acc_l[u][i], ka);
-                            }
-                        }
-                        if constexpr (GEGLU) {
-                            // |a ge| >= 2^47 for an element of the wave: that result saturates. Rarely
-                            // taken; the overflowing elements are replaced.
-                            if (__builtin_amdgcn_ballot_w64(ov > 65535u)) {
-                                asm volatile("; saturating GEGLU product");
-                                // the sign of the product is the sign bit of the biased high word;
-                                // the biased saturated value is ~0 (INT_MAX) or 0 (INT_MIN)
-#pragma unroll
-                                for (int j = 0; j < EB; ++j)
-                                    if (hv[j] > 65535u) yv[j] = ~(int(hv[j]) >> 31);
-                            }
-                        }
-#pragma unroll
-                        for (int j = 0; j < EB; ++j) {
-                            const int i = i0 + j;
-                            const unsigned soff = unsigned(8 * (i >> 2) + (i & 3)) * ldy4;
-                            const unsigned voff = FULL ? vbase : vbase + soff;
-                            const int sgo = FULL ? int(soff) : 0;
-                            int y = GEGLU ? int(unsigned(yv[j]) ^ 0x80000000u) : yv[j];
-                            if constexpr (HASR) y = add_sat(y, rv[j]);
-                            __builtin_amdgcn_raw_buffer_store_b32(y, rY, int(voff), sgo, 0);
-                            // Columns past the output have m = s = C = 0 in the table and zero W rows,
-                            // so their y is 0.
-                            if constexpr (RMAX) {
-                                unsigned ay;
-                                if constexpr (GEGLU) {
-                                    // |y| = |(y ^ 2^31) - 2^31| as an unsigned difference, also for INT_MIN
-                                    asm("v_sad_u32 %0, %1, %2, 0" : "=v"(ay) : "v"(yv[j]), "s"(0x80000000u));
-                                } else {
-                                    // max(y, -y) is |y| as an unsigned value, also for INT_MIN
-                                    ay = unsigned(max(y, int(0u - unsigned(y))));
+                                const unsigned voff = FULL ? vbase : vbase + soff;
+                                const int sgo = FULL ? int(soff) : 0;
+                                int y = GEGLU ? int(unsigned(yv[j]) ^ 0x80000000u) : yv[j];
+                                if constexpr (HASR) y = add_sat(y, rv[j]);
+                                __builtin_amdgcn_raw_buffer_store_b32(y, rY, int(voff), sgo, 0);
+                                // Columns past the output have m = s = C = 0 in the table and zero W rows,
+                                // so their y is 0.
+                                if constexpr (RMAX) {
+                                    unsigned ay;
+                                    if constexpr (GEGLU) {
+                                        // |y| = |(y ^ 2^31) - 2^31| as an unsigned difference, also for INT_MIN
+                                        asm("v_sad_u32 %0, %1, %2, 0" : "=v"(ay) : "v"(yv[j]), "s"(0x80000000u));
+                                    } else {
+                                        // max(y, -y) is |y| as an unsigned value, also for INT_MIN
+                                        ay = unsigned(max(y, int(0u - unsigned(y))));
+                                    }
+                                    yabs[i] = int(max(unsigned(yabs[i]), ay));
                                 }
-                                yabs[i] = int(max(unsigned(yabs[i]), ay));
                             }
+                            __builtin_amdgcn_sched_barrier(0);   // batches do not mix (register pressure)
                         }
-                        __builtin_amdgcn_sched_barrier(0);   // batches do not mix (register pressure)
-                    }
-                };
-                auto run_rows = [&](auto hasr, auto rmax) {
-                    if (m0 + BM <= p.Mreal) run(hasr, rmax, std::true_type{});
-                    else run(hasr, rmax, std::false_type{});
-                };
-                if constexpr (RES) {
-                    if (p.rowmax) run_rows(std::true_type{}, std::true_type{});
-                    else run_rows(std::true_type{}, std::false_type{});
-                } else {
-                    if (p.rowmax) run_rows(std::false_type{}, std::true_type{});
-                    else run_rows(std::false_type{}, std::false_type{});
-                }
-            } else {
-                // the reference's int64 formula, one element per iteration (its row maximum goes
-                // straight to memory)
-                const int col = cok ? ncol : 0;
-                const int4 ca = p.cst[GEGLU ? 2 * col : col];
-                const int4 cg = GEGLU ? p.cst[2 * col + 1] : ca;
-#pragma unroll 1
-                for (int i = 0; i < 16; ++i) {
-                    const int slot = 8 * (i >> 2) + (i & 3);
-                    const unsigned voff = vbase + unsigned(slot) * ldy4;
-                    const int er = sh.erow[wave * 32 + 4 * lh + slot];
-                    const int ya = epi1_exact(acc_h[u][i], acc_l[u][i], ca.x, ca.y, ca.z, ca.w, er);
-                    int y;
-                    if constexpr (GEGLU) {
-                        const int yg = epi1_exact(acc_h[1][i], acc_l[1][i], cg.x, cg.y, cg.z, cg.w, er);
-                        const i64 pg = lut_lds ? phi(yg) : lut16i(yg, p.Lphi);
-                        const i64 ge = sat32(rshr(i64(yg) * pg, 16));
-                        y = int(sat32(rshr(i64(ya) * ge, 16)));
-                    } else if constexpr (EPI == EPI_GELU) {
-                        const i64 pa = lut_lds ? phi(ya) : lut16i(ya, p.Lphi);
-                        y = int(sat32(rshr(i64(ya) * pa, 16)));
+                    };
+                    auto run_rows = [&](auto hasr, auto rmax) {
+                        if (m0 + BM <= p.Mreal) run(hasr, rmax, std::true_type{});
+                        else run(hasr, rmax, std::false_type{});
+                    };
+                    if constexpr (RES) {
+                        if (p.rowmax) run_rows(std::true_type{}, std::true_type{});
+                        else run_rows(std::true_type{}, std::false_type{});
                     } else {
-                        y = ya;
+                        if (p.rowmax) run_rows(std::false_type{}, std::true_type{});
+                        else run_rows(std::false_type{}, std::false_type{});
                     }
-                    if (EPI == EPI_PLAIN && p.R) y = add_sat(y, int(__builtin_amdgcn_raw_buffer_load_b32(rR, int(voff), 0, 0)));
-                    __builtin_amdgcn_raw_buffer_store_b32(y, rY, int(voff), 0, 0);
-                    const int r = rbase + 4 * lh + slot;
-                    if (p.rowmax && cok && r < p.Mreal && y) atomicMax(p.rowmax + r, uabs(y));
+                } else {
+                    // the reference's int64 formula, one element per iteration (its row maximum goes
+                    // straight to memory)
+                    const int col = cok ? ncol : 0;
+                    const int4 ca = p.cst[GEGLU ? 2 * col : col];
+                    const int4 cg = GEGLU ? p.cst[2 * col + 1] : ca;
+    #pragma unroll 1
+                    for (int i = 0; i < 16; ++i) {
+                        const int slot = 8 * (i >> 2) + (i & 3);
+                        const unsigned voff = vbase + unsigned(slot) * ldy4;
+                        const int er = sh.erow[wave * 32 + 4 * lh + slot];
+                        const int ya = epi1_exact(acc_h[u][i], acc_l[u][i], ca.x, ca.y, ca.z, ca.w, er);
+                        int y;
+                        if constexpr (GEGLU) {
+                            const int yg = epi1_exact(acc_h[1][i], acc_l[1][i], cg.x, cg.y, cg.z, cg.w, er);
+                            const i64 pg = lut_lds ? phi(yg) : lut16i(yg, p.Lphi);
+                            const i64 ge = sat32(rshr(i64(yg) * pg, 16));
+                            y = int(sat32(rshr(i64(ya) * ge, 16)));
+                        } else if constexpr (EPI == EPI_GELU) {
+                            const i64 pa = lut_lds ? phi(ya) : lut16i(ya, p.Lphi);
+                            y = int(sat32(rshr(i64(ya) * pa, 16)));
+                        } else {
+                            y = ya;
+                        }
+                        if (EPI == EPI_PLAIN && p.R) y = add_sat(y, int(__builtin_amdgcn_raw_buffer_load_b32(rR, int(voff), 0, 0)));
+                        __builtin_amdgcn_raw_buffer_store_b32(y, rY, int(voff), 0, 0);
+                        const int r = rbase + 4 * lh + slot;
+                        if (p.rowmax && cok && r < p.Mreal && y) atomicMax(p.rowmax + r, uabs(y));
+                    }
                 }
             }
         }
