@@ -111,6 +111,105 @@ def vendor_planar_us(L, stream, steps=10, warmup=3):
         return None
 
 
+def dropin_sources(stream, steps, warmup):
+    """Time the A sources and routes the reference engine actually passes (src/engine.cu), on the
+    BASELINE shapes, with seeded synthetic inputs resident in HBM:
+      * SRC_X32: int32 rows quantised on load from their row maxima (linX, :162-175), C1 shape;
+      * SRC_CONV32: an int32 NHWC image, implicit im2col (conv3's fused loader, :254-270), C3 shape,
+        the GEMM alone and with the k_pixmax + k_conv_e passes before it;
+      * SRC_I8: int8 hi/lo planes + per-row e (linQ, :148-159), C1 shape;
+      * Gemm::run on the stacked [hi; lo] planes [2M x K] (the cuBLASLt route, :271-277), C3 shape,
+        alone and as im2col3 + Gemm::run + k_epilogue;
+      * the C4 512-row convolution through AEpi without a split-K workspace (what a caller of the
+        reference's AEpi, which has none, runs)."""
+    import torch
+
+    from vela_amd import configs as cf
+    from vela_amd import gemm as vg
+
+    g = torch.Generator(device="cuda").manual_seed(0x56454C41)
+    dev = torch.device("cuda")
+
+    def rbits(shape):
+        bits = torch.randint(1, 32, shape, generator=g, device=dev, dtype=torch.int64)
+        v = torch.randint(0, 2**31, shape, generator=g, device=dev, dtype=torch.int64) & ((1 << bits) - 1)
+        return (v - (1 << (bits - 1))).to(torch.int32)
+
+    def wcst(L):
+        h = cf.make_host(L)
+        return torch.from_numpy(h["w"]).to(dev), torch.from_numpy(h["cst"]).to(dev)
+
+    def t_us(fn):
+        with torch.cuda.stream(stream):
+            return round(time_launches(fn, stream, steps, warmup) * 1e3, 2)
+
+    out = {}
+    # SRC_X32, C1 shape, residual (to_out / ff.net.2 add into the residual stream)
+    L = cf.c1()
+    w, cst = wcst(L)
+    x = rbits((L.M, L.K))
+    rm = x.to(torch.int64).abs().amax(1).to(torch.int32)
+    y = torch.zeros((L.M, L.N), dtype=torch.int32, device=dev)
+    A = vg.ASrc(src=vg.SRC_X32, x=vg.ptr(x), ldx=L.K, rowmax=vg.ptr(rm), K=L.K)
+    E = vg.AEpi(epi=vg.EPI_PLAIN, Y=vg.ptr(y), ldy=L.N, residual=vg.ptr(y))
+    us = t_us(lambda: vg.k_gemm_hl2(A, L.Mp, L.M, w, L.Kp, L.Np, L.N, L.Kp, cst, E, stream=stream))
+    out["SRC_X32 linear 4096x320x320 + residual"] = {"us": us, "tops": round(L.ops / (us * 1e-6) / 1e12, 1),
+                                                     "gbs_algorithmic": round((4 * L.M * L.K + L.N * L.K + 8 * L.M * L.N) / (us * 1e-6) / 1e9, 1)}
+    # SRC_I8 planes, C1 shape
+    hi = torch.randint(-128, 128, (L.Mp, L.Kp), generator=g, device=dev, dtype=torch.int8)
+    lo = torch.randint(-128, 128, (L.Mp, L.Kp), generator=g, device=dev, dtype=torch.int8)
+    e = torch.randint(0, 4, (L.Mp,), generator=g, device=dev, dtype=torch.int32)
+    us = t_us(lambda: vg.k_gemm_hl(hi, lo, L.Kp, L.Mp, L.M, w, L.Kp, L.Np, L.N, L.Kp, cst, e, y, L.N, stream=stream))
+    out["SRC_I8 planes linear 4096x320x320"] = {"us": us, "tops": round(L.ops / (us * 1e-6) / 1e12, 1),
+                                                "gbs_algorithmic": round((2 * L.M * L.K + L.N * L.K + 4 * L.M * L.N) / (us * 1e-6) / 1e9, 1)}
+    del x, rm, y, hi, lo, e
+    # SRC_CONV32, C3 shape: GEMM alone, and pixmax + conv_e + GEMM
+    L = cf.c3()
+    w, cst = wcst(L)
+    img = rbits((L.B, L.H, L.W, L.C)) >> 12   # 1..19-bit values: row shifts e from 0 to 4
+    pm = torch.zeros(L.B * L.H * L.W, dtype=torch.int32, device=dev)
+    e = torch.zeros(L.Mp, dtype=torch.int32, device=dev)
+    y = torch.zeros((L.M, L.N), dtype=torch.int32, device=dev)
+    vg.k_pixmax(img, L.B * L.H * L.W, L.C, pm)
+    vg.k_conv_e(pm, L.B, L.H, L.W, 1, e)
+    A = vg.ASrc(src=vg.SRC_CONV32, img=vg.ptr(img), H=L.H, W=L.W, C=L.C, stride=1, Ho=L.Ho, Wo=L.Wo, K=L.K, e=vg.ptr(e))
+    E = vg.AEpi(epi=vg.EPI_PLAIN, Y=vg.ptr(y), ldy=L.N)
+    gemm = lambda: vg.k_gemm_hl2(A, L.Mp, L.M, w, L.Kp, L.Np, L.N, L.Kp, cst, E, stream=stream)   # noqa: E731
+
+    def conv_route():
+        vg.k_pixmax(img, L.B * L.H * L.W, L.C, pm, stream=stream)
+        vg.k_conv_e(pm, L.B, L.H, L.W, 1, e, stream=stream)
+        gemm()
+
+    us, us_all = t_us(gemm), t_us(conv_route)
+    out["SRC_CONV32 conv3x3 [8,32,32,640]->640"] = {"us": us, "tops": round(L.ops / (us * 1e-6) / 1e12, 1),
+                                                    "us_with_pixmax_conv_e": us_all}
+    # the cuBLASLt route: im2col3 planes + Gemm::run on [2M x K] + k_epilogue
+    planes = torch.empty((2, L.Mp, L.Kp), dtype=torch.int8, device=dev)
+    C = torch.empty((2 * L.Mp, L.Np), dtype=torch.int32, device=dev)
+    ge = vg.Gemm()
+    ge.init(0)
+    run = lambda: ge.run(planes, L.Kp, 0, w, L.Kp, 0, C, L.Np, 0, 2 * L.Mp, L.Np, L.Kp, stream=stream)   # noqa: E731
+
+    def planar_route():
+        vg.k_pixmax(img, L.B * L.H * L.W, L.C, pm, stream=stream)
+        vg.k_im2col3(img, pm, L.B, L.H, L.W, L.C, 1, planes[0], planes[1], e, L.Kp, stream=stream)
+        run()
+        vg.k_epilogue(C[:L.Mp], C[L.Mp:], L.M, L.N, L.Np, cst, e, y, L.N, stream=stream)
+
+    us, us_all = t_us(run), t_us(planar_route)
+    out["Gemm::run planar [2x8192 x 5760] x [640 x 5760]^T (C3 via im2col3)"] = {
+        "us": us, "tops": round(L.ops / (us * 1e-6) / 1e12, 1), "us_im2col3_run_epilogue": us_all}
+    del img, pm, e, y, planes, C, ge
+    # C4 512-row conv through AEpi without a workspace
+    L = cf.c4()[1]
+    p = cf.DeviceProblem(L, with_ws=False)
+    p.reset()
+    us = t_us(lambda: p.run(stream=stream))
+    out["C4 conv3x3 [8,8,8,1280]->1280, AEpi without workspace"] = {"us": us, "tops": round(L.ops / (us * 1e-6) / 1e12, 1)}
+    return out
+
+
 def cpu_time(L, h, reps, rows=None):
     import numpy as np
 
@@ -290,6 +389,11 @@ def main():
             log(f"[bench] {Lc.name}: {table[Lc.name]}")
             del p
         out["configs"] = table
+
+    # ---- the A sources and routes a drop-in caller passes
+    if not args.no_configs:
+        out["dropin_sources"] = dropin_sources(stream, max(5, args.steps // 4), max(2, args.warmup // 4))
+        log(f"[bench] drop-in sources: {out['dropin_sources']}")
 
     # ---- C5: the UNet GEMM set as one graph
     if not args.no_unet:

@@ -128,6 +128,10 @@ int vgemm_conv16_halo_rows(int H, int W, int C, int stride, int epi);
 
 /* Split-K: force the number of K partitions for calls that pass a workspace (0 = automatic). */
 void vgemm_set_splitk(int s);
+/* Tile order over the XCDs: -1 automatic, 0 row stripes per XCD, 1 column groups per XCD. The order
+ * changes which blocks share an L2, never a result bit. No counterpart in the reference (its tile
+ * raster is CUDA's block order); a tuning and test knob like vgemm_set_splitk. */
+void vgemm_set_tile_order(int order);
 /* Workspace bytes vgemm_hl2 uses for this shape at the current settings (0 = no split-K). */
 size_t vgemm_workspace_bytes(int Mp, int Mreal, int Np, int Nreal, int Kp, int epi);
 

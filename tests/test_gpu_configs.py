@@ -31,6 +31,28 @@ def test_config_full(gpu, L):
         assert_equal(to_np(p.rowmax).view(np.uint32), wrm, L.name + " rowmax")
 
 
+ORDER_CONFIGS = [cf.c1(), cf.c3(), *cf.c4()]
+
+
+@pytest.mark.parametrize("L", ORDER_CONFIGS, ids=[L.name for L in ORDER_CONFIGS])
+def test_config_tile_orders(gpu, L):
+    """Both tile orders over the XCDs (row stripes per XCD, column groups per XCD) give the oracle's
+    bits: the order only renumbers blocks, with and without split-K."""
+    p = cf.DeviceProblem(L)
+    want = None
+    try:
+        for order in (0, 1):
+            vg.set_tile_order(order)
+            p.reset()
+            p.run()
+            torch.cuda.synchronize()
+            if want is None:
+                want, _ = oracle.layer_reference(L, p.h)
+            assert_equal(to_np(p.y), want, f"{L.name} tile order {order}")
+    finally:
+        vg.set_tile_order(-1)
+
+
 def test_config_e_path(gpu):
     """C1 shape with per-row shifts e in [0, 17] (the int16 view of rows quantised with e > 0)."""
     L = cf.Layer("C1 with e", "linear", 4096, 320, 320, e_bits=17, seed=cf.SEED0 + 11)

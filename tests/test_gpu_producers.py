@@ -165,6 +165,32 @@ def test_i8gemm(gpu, variant, M, N, K, batch):
         vg.set_variant(-1)
 
 
+@pytest.mark.parametrize("order", [0, 1])
+@pytest.mark.parametrize("M,N,K,batch", [(257, 100, 320, 1), (77, 96, 64, 3), (192, 1280, 1024, 2)])
+def test_i8gemm_tile_orders(gpu, order, M, N, K, batch):
+    """Gemm::run under each forced tile order over the XCDs, with strided batches."""
+    vg.set_tile_order(order)
+    try:
+        r = np.random.default_rng(7 * M + N + K)
+        lda, ldw, ldc = K, K + 32, N
+        sA, sW, sC = M * lda + 16, N * ldw, M * ldc + 12
+        A = r.integers(-128, 128, sA * batch).astype(np.int8)
+        W = r.integers(-128, 128, sW * batch).astype(np.int8)
+        want = oracle.i8gemm(A, W, M, N, K, batch, sA, sW, sC, lda, ldw, ldc)
+        C = torch.zeros(max(sC * batch, M * ldc), dtype=torch.int32, device="cuda")
+        g = vg.Gemm()
+        g.init(0)
+        g.run(dev(A), lda, sA, dev(W), ldw, sW, C, ldc, sC, M, N, K, batch)
+        torch.cuda.synchronize()
+        got = to_np(C)
+        for b in range(batch):
+            rows = got[b * sC: b * sC + M * ldc].reshape(M, ldc)[:, :N]
+            wrows = want[b * sC: b * sC + M * ldc].reshape(M, ldc)[:, :N]
+            assert_equal(rows, wrows, f"order {order} batch {b}")
+    finally:
+        vg.set_tile_order(-1)
+
+
 def test_graph_replays_match_eager(gpu):
     """A captured sequence of GEMMs (with kernel-zeroed rowmax buffers) replayed several times, with
     eager work and synchronisations between replays, reproduces the eager results every time."""

@@ -83,6 +83,7 @@ SIGNATURES = [
     ("vgemm_set_variant", None, [I]),
     ("vgemm_get_variant", I, []),
     ("vgemm_set_splitk", None, [I]),
+    ("vgemm_set_tile_order", None, [I]),
     ("vgemm_conv16_halo_rows", I, [I, I, I, I, I]),
     ("vgemm_workspace_bytes", SZ, [I, I, I, I, I, I]),
     ("vgemm_i8_create", I, [SZ, ctypes.POINTER(P)]),

@@ -43,6 +43,7 @@ namespace {
 thread_local std::string g_err;
 int g_variant = -1;   // meow::g_gemm_hl_variant: process-wide, written by tests only
 int g_splitk = 0;
+int g_tile_order = -1;
 
 int fail(int code, const char* fmt, ...) {
     char buf[512];
@@ -164,6 +165,35 @@ int pick_splitk(int variant, int M, int N, int Kp) {
     return s < 1 ? 1 : int(s);
 }
 
+// Tile order over the XCDs (vk::tile_index), from the bytes each order fetches from beyond the L2s:
+// row order reads A once and all of W in every XCD that owns row stripes; column order, with at
+// least one (K range, column tile) group per XCD, reads W once and in every XCD the A columns of the
+// one or two K ranges it covers (about 1/8 + 1/ksplit of A). Column order is taken only when it
+// saves a quarter of the estimate; W-heavy shapes (deep 3x3 convolutions on small images, wide
+// GEGLU projections of few rows) are the ones that gain.
+double a_operand_bytes(const VgemmASrc* A, const vk::GemmParams& p) {
+    switch (A->src) {
+    case VGEMM_SRC_I8: return 2.0 * p.Mreal * p.Kp;
+    case VGEMM_SRC_I16: return 2.0 * p.Mreal * p.Kp;
+    case VGEMM_SRC_X32: return 4.0 * p.Mreal * p.K;
+    case VGEMM_SRC_CONV32:
+    case VGEMM_SRC_CONV16: {
+        const double pix = double(p.Mreal) / (double(p.Ho) * p.Wo) * p.H * p.W;
+        return (A->src == VGEMM_SRC_CONV32 ? 4.0 : 2.0) * pix * p.C;
+    }
+    }
+    return 0.0;
+}
+
+int pick_tile_order(const vk::GemmParams& p, double a_bytes) {
+    if (g_tile_order >= 0) return g_tile_order;
+    if ((long long)p.ntiles * p.ksplit < 8) return 0;
+    const double w_bytes = double(p.Nreal) * p.Kp;
+    const double row = a_bytes + w_bytes * std::min(8, p.mtiles);
+    const double col = w_bytes + a_bytes * std::min(8.0, 1.0 + 8.0 / p.ksplit);
+    return col < 0.75 * row ? 1 : 0;
+}
+
 size_t ws_bytes_for(int variant, int M, int N, int splits) {
     if (splits <= 1) return 0;
     const size_t rows = size_t(cdiv(M, TILES[variant].BM)) * TILES[variant].BM;
@@ -216,6 +246,7 @@ int vgemm_supported(int Mp, int Np, int Kp) { return Mp > 0 && Np > 0 && Kp > 0 
 void vgemm_set_variant(int v) { g_variant = v; }
 int vgemm_get_variant(void) { return g_variant; }
 void vgemm_set_splitk(int s) { g_splitk = s < 0 ? 0 : s; }
+void vgemm_set_tile_order(int order) { g_tile_order = order < 0 ? -1 : (order ? 1 : 0); }
 
 int vgemm_conv16_halo_rows(int H, int W, int C, int stride, int epi) {
     if (H <= 0 || W <= 0 || C <= 0 || stride <= 0) return 0;
@@ -396,14 +427,17 @@ int hl2_impl(void* stream, const VgemmASrc* A, int Mp, int Mreal, const int8_t* 
         if (halo_bm) return hip_status(vk::launch_gemm_conv16_halo(halo_bm, e, p, st), "gemm_hl halo conv launch");
         return launch_src(A->src, variant, e, p, st);
     };
+    const double a_bytes = a_operand_bytes(A, p);
     if (splits <= 1) {
         p.ksplit = 1; p.kper = nK;
+        p.colmajor = pick_tile_order(p, a_bytes);
         return run(p.gnstat ? vk::EPI_PLAIN_GN : epi);
     }
     if (!aligned16(wsp.ws)) return fail(VGEMM_ERR_ARG, "gemm_hl: workspace must be 16-byte aligned");
     p.ksplit = splits;
     p.kper = (nK + splits - 1) / splits;
     p.ksplit = (nK + p.kper - 1) / p.kper;
+    p.colmajor = pick_tile_order(p, a_bytes);
     p.ws = static_cast<int32_t*>(wsp.ws);
     p.ws_rows = p.mtiles * BM;
     p.ws_ld = p.ntiles * BN;
@@ -515,6 +549,7 @@ int vgemm_i8_run(void* handle, void* stream, const int8_t* A, int lda, long long
     p.mtiles = cdiv(M, TILES[variant].BM);
     p.ntiles = cdiv(N, TILES[variant].BN);
     p.ksplit = 1; p.kper = (K + 63) / 64;
+    p.colmajor = pick_tile_order(p, double(M) * K);
     p.stride = 1;
     return hip_status(vk::launch_gemm_raw(variant, p, batch, static_cast<hipStream_t>(stream)), "i8gemm launch");
 }

@@ -792,8 +792,12 @@ __device__ __forceinline__ void store_raw(const GemmParams& p, const v4i (&acc)[
 }
 
 // Tile of this block. Blocks are dispatched round-robin over the 8 XCDs; renumber them so that
-// each XCD receives a contiguous range of tiles (neighbouring column tiles of one row stripe share
-// the A stripe in that XCD's L2).
+// each XCD receives a contiguous range of work units, in one of two orders. Row order (K range
+// fastest, then column tile, then row tile): an XCD owns whole row stripes and its L2 serves their
+// A rows to every column tile, while every XCD reads all of W. Column order (row tile fastest, then
+// column tile, then K range): an XCD owns a run of (K range, column tile) groups, so W is read about
+// once over the chip and A once per XCD for the K ranges it covers; the blocks resident together
+// on an XCD share a few W column tiles. The host picks the order with the smaller estimated fetch.
 struct TileIdx {
     int ks, mt, nt;
 };
@@ -802,10 +806,17 @@ __device__ __forceinline__ TileIdx tile_index(const GemmParams& p) {
     const int q8 = nblk >> 3, r8 = nblk & 7, xcd = bid & 7, slot = bid >> 3;
     const int lin = (xcd < r8 ? xcd * (q8 + 1) : r8 * (q8 + 1) + (xcd - r8) * q8) + slot;
     TileIdx t;
-    t.ks = lin % p.ksplit;
-    const int tl = lin / p.ksplit;
-    t.mt = tl / p.ntiles;
-    t.nt = tl - t.mt * p.ntiles;
+    if (p.colmajor) {
+        t.mt = lin % p.mtiles;
+        const int g = lin / p.mtiles;
+        t.ks = g / p.ntiles;
+        t.nt = g - t.ks * p.ntiles;
+    } else {
+        t.ks = lin % p.ksplit;
+        const int tl = lin / p.ksplit;
+        t.mt = tl / p.ntiles;
+        t.nt = tl - t.mt * p.ntiles;
+    }
     return t;
 }
 

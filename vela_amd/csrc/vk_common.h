@@ -56,8 +56,9 @@ struct GemmParams {
     // split-K partials: ws[(split * 2 + plane) * ws_rows + row][col], row stride ws_ld
     int ksplit, kper;
     int32_t* ws; int ws_rows, ws_ld;
-    // tiling
-    int mtiles, ntiles;
+    // tiling; colmajor: tile order over the XCDs (0: each XCD takes whole row stripes, every column
+    // tile and K range of them; 1: each XCD takes (K range, column tile) groups, every row tile of them)
+    int mtiles, ntiles, colmajor;
     // strided batch (EPI_RAW)
     long long sA, sW, sC;
     // GroupNorm statistics of the output (EPI_PLAIN_GN): GnStat[sample * 32 + group], gnT rows per

@@ -19,7 +19,7 @@ SRC_I8, SRC_X32, SRC_CONV32, SRC_I16, SRC_CONV16 = 0, 1, 2, 3, 4
 __all__ = [
     "ASrc", "AEpi", "VgemmError", "EPI_PLAIN", "EPI_SPLIT3", "EPI_GEGLU", "EPI_GELU", "EPI_QKV",
     "SRC_I8", "SRC_X32", "SRC_CONV32", "SRC_I16", "SRC_CONV16", "k_gemm_hl2", "k_gemm_hl", "k_conv_e",
-    "gemm_hl_supported", "set_variant", "get_variant", "set_splitk", "conv16_halo_rows", "workspace_bytes", "Gemm",
+    "gemm_hl_supported", "set_variant", "get_variant", "set_splitk", "set_tile_order", "conv16_halo_rows", "workspace_bytes", "Gemm",
     "k_quant_rows", "k_epilogue", "k_pixmax", "k_im2col3", "k_epilogue_split", "k_epilogue_geglu_q",
     "fill_u32", "Graph", "ptr", "stream_ptr", "GNSTAT_BYTES", "gn_stats_alloc", "k_gn_init", "gn_stats_read",
 ]
@@ -90,6 +90,11 @@ def get_variant() -> int:
 def set_splitk(s: int) -> None:
     """Force the split-K partition count for calls with a workspace (0 = automatic)."""
     load().vgemm_set_splitk(s)
+
+
+def set_tile_order(order: int) -> None:
+    """Tile order over the XCDs: -1 automatic, 0 row stripes per XCD, 1 column groups per XCD."""
+    load().vgemm_set_tile_order(order)
 
 
 def conv16_halo_rows(H: int, W: int, C: int, stride: int, epi: int = EPI_PLAIN) -> int:
