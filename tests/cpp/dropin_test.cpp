@@ -5,7 +5,9 @@
 // k_pixmax + k_conv_e + k_im2col3 + SRC_I8), plus an int64 host check of the planar path, a graph
 // capture and replay (src/engine.cu:610-631), GroupNorm statistics (fused and planar, with
 // k_gn_init), the EPI_QKV head layout, and the throwing error paths (src/gemm_hl.cu:351,357).
-// Needs a GPU; run by tests/test_gpu_dropin.py. Prints one line per check and exits non-zero on the
+// With a model file as argv[1] (tests/golden/tiny_model.poisd), also meow::Poisd + meow::DevModel
+// (src/poisd.h, src/engine.h) and GEMMs on the loaded linears. Needs a GPU; run by
+// tests/test_gpu_dropin.py. Prints one line per check and exits non-zero on the
 // first mismatch.
 #include <hip/hip_runtime.h>
 
@@ -21,6 +23,8 @@
 #include "vela/gemm.h"
 #include "vela/gemm_hl.h"
 #include "vela/kernels.h"
+#include "vela/model.h"
+#include "vela/poisd.h"
 
 #define HIP_OK(x)                                                                          \
     do {                                                                                   \
@@ -339,9 +343,66 @@ void test_errors(hipStream_t st) {
     expect(threw, "Gemm::run throws on a bad call");
 }
 
+// A model file through meow::Poisd / meow::DevModel, and GEMMs on its prepared linears: the merged
+// to_qkv against to_q, to_k and to_v run alone, and a linear off the padding grid against an int64
+// host restatement computed from the file's own tensors.
+void test_model(hipStream_t st, std::mt19937& rng, const char* path) {
+    meow::Poisd bad;
+    std::string err;
+    expect(!bad.load(std::string(path) + ".missing", err) && err.find("cannot open") == 0, "Poisd::load reports a missing file");
+    meow::Poisd model;
+    expect(model.load(path, err), "Poisd::load " + std::string(path) + (err.empty() ? "" : ": " + err));
+    expect(model.has("lut.phi") && model.get("lut.phi").count == 2049 && model.i32s("c.cin") == -77, "Poisd accessors");
+    meow::DevModel dm;
+    dm.load(0, model);
+    expect(dm.bytes > 0 && dm.lutPhi32 != nullptr && dm.hasLin("unet.conv_in") && !dm.hasLin("te.tok"), "DevModel::load");
+    const std::string blk = "unet.down_blocks.0.attentions.0.transformer_blocks.0.attn1.";
+    const meow::Lin& qkv = dm.lin(blk + "to_qkv");
+    expect(qkv.N == 192 && qkv.K == 64 && qkv.Np == 192 && qkv.Kp == 64 && !qkv.conv3, "merged to_qkv geometry");
+    const int M = 150, Mp = 192;
+    std::vector<int16_t> q(size_t(Mp) * 64);
+    for (auto& v : q) v = int16_t(int(rng() % 65535) - 32767);
+    Dev<int16_t> dq(q);
+    auto run = [&](const meow::Lin& L, int ld16) {
+        Dev<int32_t> Y(size_t(M) * L.N);
+        meow::ASrc a;
+        a.src = meow::SRC_I16; a.q16 = dq.p; a.ld16 = ld16; a.K = L.K;
+        meow::AEpi ep;
+        ep.Y = Y.p; ep.ldy = L.N;
+        meow::k_gemm_hl2(st, a, Mp, M, L.w, L.Kp, L.Np, L.N, L.Kp, L.cst, ep);
+        HIP_OK(hipStreamSynchronize(st));
+        return Y.get();
+    };
+    const std::vector<int32_t> all = run(qkv, 64);
+    bool same = true;
+    int part = 0;
+    for (const char* p : {"to_q", "to_k", "to_v"}) {
+        const std::vector<int32_t> one = run(dm.lin(blk + p), 64);
+        for (int r = 0; r < M; ++r)
+            for (int n = 0; n < 64; ++n) same = same && all[size_t(r) * 192 + 64 * part + n] == one[size_t(r) * 64 + n];
+        ++part;
+    }
+    expect(same, "merged to_qkv product == to_q | to_k | to_v products");
+    // 70 x 40 linear (Np 128, Kp 48): the int16 rows are read at ld16 = 64 with K = 40 real columns
+    const std::string te = "unet.time_embedding.linear_1";
+    const meow::Lin& L = dm.lin(te);
+    const std::vector<int32_t> y = run(L, 64);
+    const int8_t* w = model.i8(te + ".w");
+    const std::vector<int64_t> m = model.i32v(te + ".m"), s = model.i32v(te + ".s"), b = model.i32v(te + ".b");
+    bool ok = L.Np == 128 && L.Kp == 48;
+    for (int r = 0; r < M; ++r)
+        for (int n = 0; n < 70; ++n) {
+            int64_t acc = 0;
+            for (int k = 0; k < 40; ++k) acc += int64_t(q[size_t(r) * 64 + k]) * w[n * 40 + k];
+            const int64_t want = sat32(rshr(int64_t(uint64_t(acc) * uint64_t(m[n])), s[n]) + b[n]);
+            ok = ok && y[size_t(r) * 70 + n] == want;
+        }
+    expect(ok, "loaded 70x40 linear == int64 host restatement from the file's tensors");
+}
+
 }  // namespace
 
-int main() {
+int main(int argc, char** argv) {
     hipStream_t st;
     HIP_OK(hipStreamCreate(&st));
     std::mt19937 rng(1);
@@ -354,6 +415,7 @@ int main() {
         test_gnstat(st, rng);
         test_qkv(st, rng);
         test_errors(st);
+        if (argc > 1) test_model(st, rng, argv[1]);
     } catch (const std::exception& ex) {
         std::printf("FAIL exception: %s\n", ex.what());
         return 2;

@@ -1,5 +1,5 @@
 """The C ABI of libvgemm.so without a GPU: the library loads, exports every entry point that
-include/vgemm.h declares, the ctypes mirror of VgemmASrc / VgemmAEpi / VgemmGnStat has the C layout (checked
+include/vgemm.h and include/vgemm_model.h declare, the ctypes mirror of VgemmASrc / VgemmAEpi / VgemmGnStat has the C layout (checked
 against a gcc-compiled probe of the header), and argument checks fail the way the reference throws
 (src/gemm_hl.cu:351,357; src/gemm.cu:41) before any device work."""
 import ctypes
@@ -12,11 +12,11 @@ import pytest
 from vela_amd import _lib
 
 ROOT = Path(__file__).resolve().parent.parent
-HEADER = ROOT / "include" / "vgemm.h"
+HEADERS = [ROOT / "include" / "vgemm.h", ROOT / "include" / "vgemm_model.h"]
 
 
 def declared():
-    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    text = re.sub(r"/\*.*?\*/", "", "\n".join(h.read_text() for h in HEADERS), flags=re.S)
     out = {}
     for m in re.finditer(r"^[A-Za-z_][\w \*]*?\b(vgemm_\w+)\s*\(([^)]*)\)\s*;", text, flags=re.M):
         args = m.group(2).strip()
@@ -40,19 +40,26 @@ PROBE = r"""
 #include <stdio.h>
 #include <stddef.h>
 #include "vgemm.h"
+#include "vgemm_model.h"
 #define F(T, f) printf(#T " " #f " %zu\n", offsetof(T, f));
 int main(void) {
     printf("VgemmASrc sizeof %zu\nVgemmAEpi sizeof %zu\nVgemmGnStat sizeof %zu\n", sizeof(VgemmASrc), sizeof(VgemmAEpi),
            sizeof(VgemmGnStat));
+    printf("VgemmTensor sizeof %zu\nVgemmLin sizeof %zu\nVgemmNorm sizeof %zu\n", sizeof(VgemmTensor), sizeof(VgemmLin),
+           sizeof(VgemmNorm));
     %FIELDS%
     return 0;
 }
 """
 
 
+STRUCTS = (("VgemmASrc", _lib.ASrc), ("VgemmAEpi", _lib.AEpi), ("VgemmGnStat", _lib.GnStat), ("VgemmTensor", _lib.Tensor),
+           ("VgemmLin", _lib.Lin), ("VgemmNorm", _lib.Norm))
+
+
 def test_struct_layout_matches_c(tmp_path):
     lines = []
-    for T, cls in (("VgemmASrc", _lib.ASrc), ("VgemmAEpi", _lib.AEpi), ("VgemmGnStat", _lib.GnStat)):
+    for T, cls in STRUCTS:
         for f, _ in cls._fields_:
             lines.append(f"F({T}, {f})")
     src = tmp_path / "probe.c"
@@ -63,7 +70,7 @@ def test_struct_layout_matches_c(tmp_path):
     for line in subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.splitlines():
         T, f, v = line.split()
         got[(T, f)] = int(v)
-    for T, cls in (("VgemmASrc", _lib.ASrc), ("VgemmAEpi", _lib.AEpi), ("VgemmGnStat", _lib.GnStat)):
+    for T, cls in STRUCTS:
         assert got[(T, "sizeof")] == ctypes.sizeof(cls), T
         for f, _ in cls._fields_:
             assert got[(T, f)] == getattr(cls, f).offset, f"{T}.{f}"

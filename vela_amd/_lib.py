@@ -71,7 +71,26 @@ class AEpi(ctypes.Structure):
             setattr(self, k, v)
 
 
-# (name, restype, argtypes) of every entry point declared in include/vgemm.h
+class Tensor(ctypes.Structure):
+    """VgemmTensor (include/vgemm_model.h) == meow::PoisdTensor (src/poisd.h:10-16) plus a host pointer."""
+
+    _fields_ = [("dtype", I), ("rank", I), ("dims", ctypes.c_uint32 * 8), ("count", SZ), ("offset", SZ), ("bytes", SZ),
+                ("data", P)]
+
+
+class Lin(ctypes.Structure):
+    """VgemmLin (include/vgemm_model.h) == meow::Lin (src/engine.h:12)."""
+
+    _fields_ = [("N", I), ("K", I), ("Np", I), ("Kp", I), ("conv3", I), ("w_host", P), ("cst_host", P), ("w", P), ("cst", P)]
+
+
+class Norm(ctypes.Structure):
+    """VgemmNorm (include/vgemm_model.h) == meow::Norm (src/engine.h:13)."""
+
+    _fields_ = [("C", I), ("den", LL), ("g_host", P), ("beta_host", P), ("g", P), ("beta", P)]
+
+
+# (name, restype, argtypes) of every entry point declared in include/vgemm.h and include/vgemm_model.h
 SIGNATURES = [
     ("vgemm_asrc_init", None, [ctypes.POINTER(ASrc)]),
     ("vgemm_aepi_init", None, [ctypes.POINTER(AEpi)]),
@@ -101,6 +120,19 @@ SIGNATURES = [
     ("vgemm_graph_destroy", I, [P]),
     ("vgemm_fill_u32", I, [P, P, SZ, U32]),
     ("vgemm_gn_init", I, [P, P, I]),
+    ("vgemm_model_open", I, [ctypes.c_char_p, ctypes.POINTER(P)]),
+    ("vgemm_model_close", None, [P]),
+    ("vgemm_model_count", I, [P]),
+    ("vgemm_model_name", ctypes.c_char_p, [P, I]),
+    ("vgemm_model_tensor", I, [P, ctypes.c_char_p, ctypes.POINTER(Tensor)]),
+    ("vgemm_model_prepare", I, [P]),
+    ("vgemm_model_upload", I, [P, I]),
+    ("vgemm_model_device_bytes", SZ, [P]),
+    ("vgemm_model_lin", I, [P, ctypes.c_char_p, ctypes.POINTER(Lin)]),
+    ("vgemm_model_lin_count", I, [P]),
+    ("vgemm_model_lin_name", ctypes.c_char_p, [P, I]),
+    ("vgemm_model_norm", I, [P, ctypes.c_char_p, ctypes.POINTER(Norm)]),
+    ("vgemm_model_table", I, [P, ctypes.c_char_p, ctypes.POINTER(P), ctypes.POINTER(I)]),
     ("vgemm_last_error", ctypes.c_char_p, []),
     ("vgemm_version", ctypes.c_char_p, []),
 ]

@@ -67,6 +67,19 @@ int hip_status(hipError_t e, const char* what) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
+}  // namespace
+
+// the thread-local message of vgemm_last_error, for the other translation units of the library
+namespace vk {
+int set_error(int code, const std::string& msg) {
+    g_err = msg;
+    return code;
+}
+void clear_error() { g_err.clear(); }
+}  // namespace vk
+
+namespace {
+
 // Byte extent a buffer load may touch; the kernels address operands with 32-bit offsets and use
 // offset 2^31 as the "outside" marker, so every extent must stay below 2^31.
 constexpr long long MAX_EXTENT = (1LL << 31) - 64;
