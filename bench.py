@@ -116,7 +116,8 @@ def dropin_sources(stream, steps, warmup):
     BASELINE shapes, with seeded synthetic inputs resident in HBM:
       * SRC_X32: int32 rows quantised on load from their row maxima (linX, :162-175), C1 shape;
       * SRC_CONV32: an int32 NHWC image, implicit im2col (conv3's fused loader, :254-270), C3 shape,
-        the GEMM alone and with the k_pixmax + k_conv_e passes before it;
+        the GEMM alone, with the k_pixmax + k_conv_e passes before it, and given the pixel maxima
+        (ASrc.rowmax) so that the GEMM derives the shifts itself;
       * SRC_I8: int8 hi/lo planes + per-row e (linQ, :148-159), C1 shape;
       * Gemm::run on the stacked [hi; lo] planes [2M x K] (the cuBLASLt route, :271-277), C3 shape,
         alone and as im2col3 + Gemm::run + k_epilogue;
@@ -181,9 +182,13 @@ def dropin_sources(stream, steps, warmup):
         vg.k_conv_e(pm, L.B, L.H, L.W, 1, e, stream=stream)
         gemm()
 
-    us, us_all = t_us(gemm), t_us(conv_route)
+    # the pixel maxima from the producer (its AEpi.rowmax), the shifts derived inside the GEMM
+    Apm = vg.ASrc(src=vg.SRC_CONV32, img=vg.ptr(img), H=L.H, W=L.W, C=L.C, stride=1, Ho=L.Ho, Wo=L.Wo, K=L.K, rowmax=vg.ptr(pm))
+    gemm_pm = lambda: vg.k_gemm_hl2(Apm, L.Mp, L.M, w, L.Kp, L.Np, L.N, L.Kp, cst, E, stream=stream)   # noqa: E731
+
+    us, us_all, us_pm = t_us(gemm), t_us(conv_route), t_us(gemm_pm)
     out["SRC_CONV32 conv3x3 [8,32,32,640]->640"] = {"us": us, "tops": round(L.ops / (us * 1e-6) / 1e12, 1),
-                                                    "us_with_pixmax_conv_e": us_all}
+                                                    "us_with_pixmax_conv_e": us_all, "us_shift_from_pixel_maxima": us_pm}
     # the cuBLASLt route: im2col3 planes + Gemm::run on [2M x K] + k_epilogue
     planes = torch.empty((2, L.Mp, L.Kp), dtype=torch.int8, device=dev)
     C = torch.empty((2 * L.Mp, L.Np), dtype=torch.int32, device=dev)

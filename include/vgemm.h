@@ -45,6 +45,10 @@ typedef struct VgemmASrc {
     const int8_t* hi; const int8_t* lo; int ld8; const int32_t* e;         /* SRC_I8 (e may be NULL = 0) */
     const int32_t* x; int ldx; const uint32_t* rowmax; int K;              /* SRC_X32 (K = real columns) */
     const int32_t* img; int H, W, C, stride, Ho, Wo;                       /* SRC_CONV32 (K = 9C, C % 16 == 0) */
+    /* Convolution sources (SRC_CONV32, SRC_CONV16) with e == NULL and rowmax != NULL: rowmax holds the
+     * image's per-pixel maximum |x| ([B*H*W], as k_pixmax writes it, or the AEpi.rowmax of the GEMM
+     * that produced the image) and each output row's shift is derived in the kernel by k_conv_e's
+     * rule (src/gemm_hl.cu:335-341), so no k_conv_e launch or e buffer is needed. */
     const int16_t* q16; int ld16;                                          /* SRC_I16 (K % 8, ld16 % 8) */
     const int16_t* img16;                                                  /* SRC_CONV16 (C % 8 == 0, C <= 16384) */
 } VgemmASrc;

@@ -75,6 +75,7 @@ class Case:
             else:
                 self.img = r.integers(-32768, 32768, (B, H, W, C)).astype(np.int16)
             pm = oracle.pixmax(self.img.astype(np.int32).reshape(-1, C), B * H * W, C)
+            self.pm = pm
             self.e = oracle.conv_e(pm, B, H, W, stride)
             self.kw = dict(img=self.img, H=H, W=W, C=C, stride=stride)
         self.lut = lut if lut is not None else cf.phi_lut()
@@ -83,6 +84,7 @@ class Case:
         self.nout = nout
         self.res = r.integers(-(2**31), 2**31, (M, nout), dtype=np.int64).astype(np.int32) if residual else None
         self.rowmax = rowmax
+        self.pm_in_kernel = False   # convolution sources: pass the per-pixel maxima instead of e
 
     def reference(self):
         kw = dict(self.kw)
@@ -100,8 +102,12 @@ class Case:
     def asrc(self, keep):
         """The device A operand of this case; device buffers are kept alive in `keep`."""
         A = vg.ASrc(src=self.src)
-        keep["e"] = dev(self.e)
-        A.e = vg.ptr(keep["e"])
+        if self.pm_in_kernel:
+            keep["pm"] = dev(self.pm.view(np.int32))
+            A.rowmax = vg.ptr(keep["pm"])
+        else:
+            keep["e"] = dev(self.e)
+            A.e = vg.ptr(keep["e"])
         if self.src == vg.SRC_I8:
             keep["hi"], keep["lo"] = dev(self.hi), dev(self.lo)
             A.hi, A.lo, A.ld8 = vg.ptr(keep["hi"]), vg.ptr(keep["lo"]), self.Kp
@@ -221,6 +227,28 @@ def test_conv_sources(src, geom, variant):
     B, H, W, C, stride = geom
     Ho, Wo = (H - 1) // stride + 1, (W - 1) // stride + 1
     Case(src, B * Ho * Wo, 96, 9 * C, seed=14, conv=geom, residual=True).check(what=f"conv {src} {geom}")
+
+
+@pytest.mark.parametrize("src", [vg.SRC_CONV32, vg.SRC_CONV16])
+@pytest.mark.parametrize("geom,variant,split", [((2, 8, 8, 32, 1), -1, 0), ((1, 7, 5, 64, 2), 3, 0), ((2, 6, 6, 320, 1), 0, 0),
+                                                ((1, 9, 11, 16, 2), 1, 0), ((8, 8, 8, 256, 1), -1, 0), ((2, 8, 8, 512, 1), 1, 3),
+                                                ((2, 16, 16, 64, 1), -1, 0)])
+def test_conv_shift_from_pixel_maxima(src, geom, variant, split):
+    """A convolution given the image's per-pixel maxima (ASrc.rowmax, e = NULL) derives each row's
+    shift in the kernel by k_conv_e's rule: the same bytes as with e from k_conv_e, on the tile,
+    halo and split-K paths (the split-K reduction derives it too)."""
+    vg.set_variant(variant)
+    vg.set_splitk(split)
+    B, H, W, C, stride = geom
+    Ho, Wo = (H - 1) // stride + 1, (W - 1) // stride + 1
+    c = Case(src, B * Ho * Wo, 128, 9 * C, seed=15 + C, conv=geom, residual=True)
+    if src == vg.SRC_CONV16:
+        c.img.reshape(-1)[::97] = -32768   # |x| = 32768 gives e = 1 where it enters a window
+        c.pm = oracle.pixmax(c.img.astype(np.int32).reshape(-1, C), B * H * W, C)
+        c.e = oracle.conv_e(c.pm, B, H, W, stride)
+    assert c.e.max() > 0
+    c.pm_in_kernel = True
+    c.check(ws_bytes=(64 << 20) if split else 0, what=f"conv {src} {geom} pm")
 
 
 @pytest.mark.parametrize("variant", [-1, 0, 3])

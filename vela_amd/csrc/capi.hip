@@ -356,6 +356,8 @@ int hl2_impl(void* stream, const VgemmASrc* A, int Mp, int Mreal, const int8_t* 
         if (A->Ho != Ho || A->Wo != Wo) return fail(VGEMM_ERR_ARG, "gemm_hl conv source: Ho/Wo must be (H-1)/stride+1, (W-1)/stride+1");
         const long long B = (Mreal + (long long)Ho * Wo - 1) / ((long long)Ho * Wo);
         p.a0 = img; p.K = A->K; p.H = A->H; p.W = A->W; p.C = A->C; p.stride = A->stride; p.Ho = Ho; p.Wo = Wo;
+        // without an e vector, rowmax holds the image's per-pixel maxima and the kernels derive e
+        p.pm = A->e ? nullptr : A->rowmax;
         aext = B * A->H * A->W * (long long)A->C * (A->src == VGEMM_SRC_CONV32 ? 4 : 2);
         break;
     }

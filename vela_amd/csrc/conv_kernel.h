@@ -74,7 +74,7 @@ __global__ void __launch_bounds__(256, 2) conv_halo_kernel(const GemmParams p) {
 #pragma unroll
     for (int ms = 0; ms < MS; ++ms) {
         const int r = rbase + ms * 16 + (lane & 15);
-        er[ms] = (r < p.Mreal && p.e) ? p.e[r] : 0;
+        er[ms] = r < p.Mreal ? row_shift<SRC_CONV16>(p, r) : 0;
     }
     TilePre pre{};
     if constexpr (FUSED) pre = load_tile_pre<EPI, SRC_CONV16, BM, BN>(p, m0, n0);

@@ -195,6 +195,38 @@ struct EpiFlags {
     bool fast, ezero, fold;
 };
 
+// Shift of output row r (src/gemm_hl.cu:102,335-341): SRC_X32 from the row's maximum |x|; a
+// convolution source given per-pixel maxima instead of an e vector takes k_conv_e's rule in-kernel
+// (row_exp of the largest maximum over the in-bounds pixels of the row's 3x3 window, nine cached
+// loads per row); otherwise e[r], or 0 without an e vector.
+__device__ __forceinline__ int conv_window_shift(const GemmParams& p, int r) {
+    const int HoWo = p.Ho * p.Wo;
+    const int b = r / HoWo, pp = r - b * HoWo, oy = pp / p.Wo, ox = pp - oy * p.Wo;
+    const int iy0 = oy * p.stride - 1, ix0 = ox * p.stride - 1;
+    uint32_t m = 0;
+#pragma unroll
+    for (int ky = 0; ky < 3; ++ky) {
+        const int iy = iy0 + ky;
+        if (iy < 0 || iy >= p.H) continue;
+        const uint32_t* row = p.pm + (size_t(b) * p.H + iy) * p.W;
+#pragma unroll
+        for (int kx = 0; kx < 3; ++kx) {
+            const int ix = ix0 + kx;
+            if (ix >= 0 && ix < p.W) m = max(m, row[ix]);
+        }
+    }
+    return rowexp_u32(m);
+}
+
+template <int SRC>
+__device__ __forceinline__ int row_shift(const GemmParams& p, int r) {
+    if constexpr (SRC == SRC_X32) return rowexp_u32(p.xrowmax[r]);
+    if constexpr (SRC == SRC_CONV32 || SRC == SRC_CONV16) {
+        if (p.pm) return conv_window_shift(p, r);
+    }
+    return p.e ? p.e[r] : 0;
+}
+
 // Fill the epilogue constants of columns [n0, n0 + BN) (in LDS-row order) and decide whether the
 // FP64 epilogue is exact for every element of this block.
 template <int EPI, int SRC, int BM, int BN, class S>
@@ -214,7 +246,7 @@ __device__ __forceinline__ EpiFlags block_prologue(const GemmParams& p, int m0, 
         for (int i = tid; i < BM; i += 256) {
             const int r = m0 + i;
             if (r < p.Mreal) {
-                const int er = SRC == SRC_X32 ? rowexp_u32(p.xrowmax[r]) : (p.e ? p.e[r] : 0);
+                const int er = row_shift<SRC>(p, r);
                 emn = min(emn, er);
                 emx = max(emx, er);
             }
@@ -331,7 +363,7 @@ __device__ __forceinline__ TilePre load_tile_pre(const GemmParams& p, int m0, in
     t.c = t.cok ? p.cst[n] : make_int4(0, 0, 0, 0);
     const int r = m0 + tid;
     t.eok = tid < BM && r < p.Mreal;
-    t.e = t.eok ? (SRC == SRC_X32 ? rowexp_u32(p.xrowmax[r]) : (p.e ? p.e[r] : 0)) : 0;
+    t.e = t.eok ? (row_shift<SRC>(p, r)) : 0;
     t.m0 = m0;
     return t;
 }
@@ -889,7 +921,7 @@ __global__ void __launch_bounds__(T::NT, (dma_waves_per_simd<T, EPI>())) gemm_dm
 #pragma unroll
     for (int ms = 0; ms < MS; ++ms) {
         const int r = rbase + ms * 16 + (lane & 15);
-        er[ms] = (r < p.Mreal && p.e && (FUSED || SRC == SRC_CONV16)) ? p.e[r] : 0;
+        er[ms] = (r < p.Mreal && (FUSED || SRC == SRC_CONV16)) ? row_shift<SRC>(p, r) : 0;
     }
     TilePre pre{};
     if constexpr (FUSED) pre = load_tile_pre<EPI, SRC, BM, BN>(p, m0, n0);
@@ -1132,7 +1164,7 @@ __global__ void __launch_bounds__(256) gemm_hl_kernel(const GemmParams p) {
     for (int ms = 0; ms < MS; ++ms) {
         const int r = rbase + ms * 16 + (lane & 15);
         er[ms] = 0;
-        if (r < p.Mreal) er[ms] = SRC == SRC_X32 ? rowexp_u32(p.xrowmax[r]) : (p.e ? p.e[r] : 0);
+        if (r < p.Mreal) er[ms] = row_shift<SRC>(p, r);
     }
 
     // ---- per-thread load tasks (fixed over the K loop)
@@ -1147,9 +1179,9 @@ __global__ void __launch_bounds__(256) gemm_hl_kernel(const GemmParams p) {
         const int r = m0 + a_row[i];
         a_ok[i] = r < p.Mreal;
         a_e[i] = 0;
-        if constexpr (SRC == SRC_X32) a_e[i] = a_ok[i] ? rowexp_u32(p.xrowmax[r]) : 0;
+        if constexpr (SRC == SRC_X32) a_e[i] = a_ok[i] ? row_shift<SRC>(p, r) : 0;
         if constexpr (CONV) {
-            a_e[i] = (a_ok[i] && p.e) ? p.e[r] : 0;
+            a_e[i] = a_ok[i] ? row_shift<SRC>(p, r) : 0;
             const int HoWo = p.Ho * p.Wo;
             const int rr = a_ok[i] ? r : 0;
             const int b = rr / HoWo, pp = rr - b * HoWo, oy = pp / p.Wo, ox = pp - oy * p.Wo;
@@ -1297,7 +1329,7 @@ __global__ void __launch_bounds__(256) splitk_epilogue_kernel(const GemmParams p
         const bool full = c0 + 3 < nout;
         uint32_t mx = 0;
         if (live) {
-            const int er = p.xrowmax ? rowexp_u32(p.xrowmax[r]) : (p.e ? p.e[r] : 0);
+            const int er = p.xrowmax ? rowexp_u32(p.xrowmax[r]) : (p.pm ? conv_window_shift(p, r) : (p.e ? p.e[r] : 0));
             // plane sums of ws columns [wc, wc + 4) over the K splits (16-byte loads: ws_ld % 4 == 0)
             auto sum4 = [&](int wc, v4i& h, v4i& l) {
                 h = v4i{0, 0, 0, 0};

@@ -41,6 +41,7 @@ struct GemmParams {
     int lda;                   // row stride in elements (ld8 / ld16 / ldx)
     const int32_t* e;          // per-row shift (SRC_I8, SRC_I16, SRC_CONV*); may be null
     const uint32_t* xrowmax;   // SRC_X32
+    const uint32_t* pm;        // convolution sources without e: per-pixel max |x| of the image (shift computed in-kernel)
     int K;                     // real K of the source (X32 / I16 / CONV)
     int H, W, C, stride, Ho, Wo;
     // weights
