@@ -34,7 +34,7 @@ PEAK_HBM_GBS = 8000.0        # MI355X HBM3E, 8 TB/s
 METRIC = "effective W8A16 TOPS & % int8 MFMA peak; UNet GEMM-set ms at batch 8"
 
 
-ONLY_NAMES = ("c1", "c2", "c2plain", "c3", "c4a", "c4b", "c4c", "copy")
+ONLY_NAMES = ("c1", "c2", "c2plain", "c2view", "c3", "c4a", "c4b", "c4c", "copy")
 COPY_BYTES = 256 << 20       # the calibration copy of --only copy: 256 MiB read + 256 MiB written
 
 
@@ -109,6 +109,43 @@ def vendor_planar_us(L, stream, steps=10, warmup=3):
             return round(time_launches(lambda: torch._int_mm(A, Wt), stream, steps, warmup) * 1e3, 2)
     except RuntimeError:
         return None
+
+
+class ViewRun:
+    """C2 with the int16 view as its output (AEpi.vhi/vlo/ve): the row-maxima clear, the
+    row-stationary kernel writing each chunk at its running exponent, and the fix-up pass; and, for
+    comparison, the two-pass route (int32 Y + rowmax, then k_quant_rows)."""
+
+    def __init__(self, prob):
+        import torch
+        from vela_amd import gemm as vg
+
+        L = prob.L
+        self.prob, self.L = prob, L
+        F = L.Nout
+        self.hi = torch.empty((L.M, F), dtype=torch.int8, device="cuda")
+        self.lo = torch.empty_like(self.hi)
+        self.e = torch.empty(L.M, dtype=torch.int32, device="cuda")
+        nb = vg.view_workspace_bytes(L.M, L.N, L.epi)
+        self.ws = torch.empty(nb // 4 + 64, dtype=torch.int32, device="cuda")
+        self.E = vg.AEpi(epi=L.epi, Lphi=vg.ptr(prob.lphi), vhi=vg.ptr(self.hi), vlo=vg.ptr(self.lo), ve=vg.ptr(self.e), vld=F,
+                         ws=vg.ptr(self.ws), ws_bytes=nb)
+        # A + W + the int16 view + e + cst
+        self.bytes = 2 * L.M * L.K + L.N * L.K + 2 * L.M * F + 4 * L.M + 16 * L.N
+
+    def fused(self, stream):
+        from vela_amd import gemm as vg
+
+        p, L = self.prob, self.L
+        vg.k_gemm_hl2(p.A, L.Mp, L.M, p.w, p.w.shape[1], L.Np, L.N, L.Kp, p.cst, self.E, stream=stream)
+
+    def two_pass(self, stream):
+        from vela_amd import gemm as vg
+
+        p, L = self.prob, self.L
+        vg.fill_u32(p.rowmax, 0, stream=stream)
+        p.run(stream=stream)
+        vg.k_quant_rows(p.y, L.M, L.Nout, L.Nout, self.hi, self.lo, self.e, L.Nout, stream=stream)
 
 
 def dropin_sources(stream, steps, warmup):
@@ -328,6 +365,16 @@ def main():
             del p
         log(f"[bench] C5 layers launched one at a time: {total:.3f} ms in total")
         return
+    if args.only == "c2view":
+        L = cf.c2(cf.EPI_GEGLU)
+        p = cf.DeviceProblem(L)
+        p.reset()
+        v = ViewRun(p)
+        torch.cuda.synchronize()
+        t = time_launches(lambda: v.fused(stream), stream, args.steps, args.warmup)
+        log(f"[bench] C2 + int16 view: {t * 1e3:.2f} us/call")
+        print(json.dumps({"workload": "C2 GEGLU -> int16 view", "us": round(t * 1e3, 3), "tops": round(L.ops / (t * 1e-3) / 1e12, 2)}), flush=True)
+        return
     if args.only:
         L = only_layer(args.only)
         p = cf.DeviceProblem(L)
@@ -375,6 +422,21 @@ def main():
         "roofline": roof,
         "hipblaslt_planar_gemm_us": vendor_c2,
     }
+
+    # ---- C2 with the int16 view (hi/lo planes + e) as its output, against its own roofline
+    v = ViewRun(prob)
+    torch.cuda.synchronize()
+    tv = time_launches(lambda: v.fused(stream), stream, args.steps, args.warmup)
+    t2 = time_launches(lambda: v.two_pass(stream), stream, max(5, args.steps // 4), max(2, args.warmup // 4))
+    rv = roofline(L.ops, v.bytes, tv * 1e-3)
+    rv.update({"algorithmic_bytes_per_launch": v.bytes, "hbm_floor_us": round(v.bytes / (PEAK_HBM_GBS * 1e9) * 1e6, 2),
+               "mfma_floor_us": round(L.ops / (PEAK_INT8_TOPS * 1e12) * 1e6, 2),
+               "hbm_frac": round(v.bytes / (tv * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)})
+    out["c2_int16_view"] = {"workload": "C2 GEGLU -> int16 view (hi/lo [32768x1280] + e), quant_row_out semantics",
+                            "us": round(tv * 1e3, 2), "tops": round(L.ops / (tv * 1e-3) / 1e12, 2), "roofline": rv,
+                            "us_two_pass_int32_then_quant_rows": round(t2 * 1e3, 2)}
+    log(f"[bench] C2 + int16 view: {out['c2_int16_view']}")
+    del v
 
     # ---- the other configurations (one line each in "configs")
     if not args.no_configs:

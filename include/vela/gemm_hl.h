@@ -50,6 +50,7 @@ struct AEpi {
     int8_t *qhi = nullptr, *qlo = nullptr, *khi = nullptr, *klo = nullptr; int32_t *qe = nullptr, *ke = nullptr;
     int64_t *qhs = nullptr, *qls = nullptr, *qts = nullptr, *khs = nullptr, *kls = nullptr, *kts = nullptr;
     void* ws = nullptr; size_t ws_bytes = 0;
+    int8_t *vhi = nullptr, *vlo = nullptr; int32_t* ve = nullptr; int vld = 0;   // int16 view (include/vgemm.h)
 };
 
 namespace detail {
@@ -72,6 +73,7 @@ inline VgemmAEpi to_c(const AEpi& e) {
     c.qhi = e.qhi; c.qlo = e.qlo; c.khi = e.khi; c.klo = e.klo; c.qe = e.qe; c.ke = e.ke;
     c.qhs = e.qhs; c.qls = e.qls; c.qts = e.qts; c.khs = e.khs; c.kls = e.kls; c.kts = e.kts;
     c.ws = e.ws; c.ws_bytes = e.ws_bytes;
+    c.vhi = e.vhi; c.vlo = e.vlo; c.ve = e.ve; c.vld = e.vld;
     return c;
 }
 }  // namespace detail

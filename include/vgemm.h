@@ -82,6 +82,14 @@ typedef struct VgemmAEpi {
     int8_t *qhi, *qlo, *khi, *klo; int32_t *qe, *ke;
     int64_t *qhs, *qls, *qts, *khs, *kls, *kts;
     void* ws; size_t ws_bytes;          /* optional split-K workspace (device memory) */
+    /* Optional int16 view of the output instead of Y (no counterpart in the reference's fused GEMM;
+     * the semantics of its quant_row_out, src/kernels.cu:317-331, as k_epilogue_geglu_q / k_quant_rows
+     * give them): per output row r < Mreal, e = row_exp(max |y|) into ve[r], q = quant16_32(y, e)
+     * into the planes vhi/vlo [Mreal x vld] (hi = q >> 8, lo = (q & 255) - 128), columns
+     * [nout, vld) padded with (0, -128). EPI_PLAIN / EPI_GEGLU / EPI_GELU with int16 rows or int8
+     * planes, Kp <= 320, no residual, rowmax or statistics; Y is not written (may be NULL); vld % 16
+     * == 0, planes 16-byte aligned. Needs vgemm_view_workspace_bytes() of workspace in ws. */
+    int8_t *vhi, *vlo; int32_t* ve; int vld;
 } VgemmAEpi;
 
 /* Fill an ASrc / AEpi with the reference's default member values (src = SRC_I8, stride = 1, rest 0). */
@@ -136,6 +144,9 @@ void vgemm_set_splitk(int s);
  * changes which blocks share an L2, never a result bit. No counterpart in the reference (its tile
  * raster is CUDA's block order); a tuning and test knob like vgemm_set_splitk. */
 void vgemm_set_tile_order(int order);
+/* Workspace bytes the int16 view (AEpi.vhi) of an Mreal x Nreal call with this epilogue needs:
+ * the row maxima, one exponent byte and one 32-bit mask per (row, 32 output columns). */
+size_t vgemm_view_workspace_bytes(int Mreal, int Nreal, int epi);
 /* Workspace bytes vgemm_hl2 uses for this shape at the current settings (0 = no split-K). */
 size_t vgemm_workspace_bytes(int Mp, int Mreal, int Np, int Nreal, int Kp, int epi);
 

@@ -63,6 +63,7 @@ class AEpi(ctypes.Structure):
         ("qhi", P), ("qlo", P), ("khi", P), ("klo", P), ("qe", P), ("ke", P),
         ("qhs", P), ("qls", P), ("qts", P), ("khs", P), ("kls", P), ("kts", P),
         ("ws", P), ("ws_bytes", SZ),
+        ("vhi", P), ("vlo", P), ("ve", P), ("vld", I),
     ]
 
     def __init__(self, **kw):
@@ -105,6 +106,7 @@ SIGNATURES = [
     ("vgemm_set_tile_order", None, [I]),
     ("vgemm_conv16_halo_rows", I, [I, I, I, I, I]),
     ("vgemm_workspace_bytes", SZ, [I, I, I, I, I, I]),
+    ("vgemm_view_workspace_bytes", SZ, [I, I, I]),
     ("vgemm_i8_create", I, [SZ, ctypes.POINTER(P)]),
     ("vgemm_i8_destroy", I, [P]),
     ("vgemm_i8_run", I, [P, P, P, I, LL, P, I, LL, P, I, LL, I, I, I, I]),

@@ -22,6 +22,9 @@ int conv_halo_bm(int epi, int H, int W, int C, int stride, int Ho, int Wo);
 hipError_t launch_gemm_conv16_halo(int bm, int epi, const GemmParams& p, hipStream_t st);
 hipError_t launch_gemm_raw(int variant, const GemmParams& p, int batch, hipStream_t st);
 hipError_t launch_stripe(int src, int epi, const GemmParams& p, hipStream_t st);
+hipError_t launch_stripe_view(int src, int epi, const GemmParams& p, hipStream_t st);
+hipError_t launch_view_fix(hipStream_t st, const uint32_t* vmax, const uint8_t* vexp, const uint32_t* vmask, int M, int F, int G, int8_t* hi,
+                           int8_t* lo, int ld, int32_t* e);
 hipError_t launch_splitk_epilogue(int epi, const GemmParams& p, hipStream_t st);
 hipError_t launch_quant_rows(hipStream_t st, const int32_t* X, int M, int K, int ldx, int8_t* hi, int8_t* lo, int32_t* e, int Kp);
 hipError_t launch_pixmax(hipStream_t st, const int32_t* X, int rows, int C, uint32_t* pm);
@@ -207,6 +210,20 @@ int pick_tile_order(const vk::GemmParams& p, double a_bytes) {
     return col < 0.75 * row ? 1 : 0;
 }
 
+// Workspace of the int16 view: row maxima [M], masks [M x G] and exponent bytes [M x G], G = the
+// output's 32-column groups, each part 256-byte aligned.
+struct ViewWs { size_t max_off, mask_off, exp_off, bytes; };
+ViewWs view_ws(int M, int nout) {
+    const size_t G = size_t(cdiv(nout, 32));
+    auto a256 = [](size_t v) { return (v + 255) / 256 * 256; };
+    ViewWs w;
+    w.max_off = 0;
+    w.mask_off = a256(size_t(M) * 4);
+    w.exp_off = w.mask_off + a256(size_t(M) * G * 4);
+    w.bytes = w.exp_off + a256(size_t(M) * G);
+    return w;
+}
+
 size_t ws_bytes_for(int variant, int M, int N, int splits) {
     if (splits <= 1) return 0;
     const size_t rows = size_t(cdiv(M, TILES[variant].BM)) * TILES[variant].BM;
@@ -266,6 +283,11 @@ int vgemm_conv16_halo_rows(int H, int W, int C, int stride, int epi) {
     return vk::conv_halo_bm(epi, H, W, C, stride, (H - 1) / stride + 1, (W - 1) / stride + 1);
 }
 
+size_t vgemm_view_workspace_bytes(int Mreal, int Nreal, int epi) {
+    if (Mreal <= 0 || Nreal <= 0) return 0;
+    return view_ws(Mreal, epi == VGEMM_EPI_GEGLU ? Nreal / 2 : Nreal).bytes;
+}
+
 size_t vgemm_workspace_bytes(int Mp, int Mreal, int Np, int Nreal, int Kp, int epi) {
     (void)Mp; (void)Np; (void)epi;
     if (g_variant >= 0 && g_variant < NVARIANT) return ws_bytes_for(g_variant, Mreal, Nreal, pick_splitk(g_variant, Mreal, Nreal, Kp));
@@ -288,6 +310,43 @@ struct WsPolicy {
     bool strict;
 };
 
+// The int16 view of the output (AEpi.vhi/vlo/ve): the row-stationary kernel writes each chunk at its
+// running row exponent with correction bits and row maxima in the workspace, then the fix-up pass
+// settles every row at its final exponent (stripe_kernel.h, producers.hip: view_fix_kernel).
+int view_impl(const VgemmASrc* A, const VgemmAEpi* E, vk::GemmParams& p, int Mreal, int Nreal, const WsPolicy& wsp, hipStream_t st) {
+    const int epi = E->epi;
+    if (epi != VGEMM_EPI_PLAIN && epi != VGEMM_EPI_GEGLU && epi != VGEMM_EPI_GELU)
+        return fail(VGEMM_ERR_ARG, "gemm_hl int16 view: EPI_PLAIN, EPI_GEGLU or EPI_GELU only");
+    if (E->residual || E->rowmax || E->gnstat) return fail(VGEMM_ERR_ARG, "gemm_hl int16 view: no residual, rowmax or statistics");
+    if (A->src != VGEMM_SRC_I16 && A->src != VGEMM_SRC_I8) return fail(VGEMM_ERR_UNSUPPORTED, "gemm_hl int16 view: int16 rows or int8 planes only");
+    if (p.Kp > 320) return fail(VGEMM_ERR_UNSUPPORTED, "gemm_hl int16 view: Kp <= 320 only (the row-stationary kernel)");
+    if (epi == VGEMM_EPI_GEGLU && Nreal % 2) return fail(VGEMM_ERR_ARG, "gemm_hl: EPI_GEGLU needs an even Nreal (interleaved a/g columns)");
+    if (epi != VGEMM_EPI_PLAIN && !E->Lphi) return fail(VGEMM_ERR_ARG, "gemm_hl: EPI_GEGLU/EPI_GELU need Lphi");
+    const int nout = epi == VGEMM_EPI_GEGLU ? Nreal / 2 : Nreal;
+    if (nout % 4 || !E->vlo || !E->ve || E->vld < nout || E->vld % 16 || !aligned16(E->vhi) || !aligned16(E->vlo))
+        return fail(VGEMM_ERR_ARG, "gemm_hl int16 view: output columns %% 4 == 0, vhi/vlo 16-byte aligned, vld >= output columns, vld %% 16 == 0, and ve");
+    if ((long long)Mreal * E->vld > MAX_EXTENT) return fail(VGEMM_ERR_UNSUPPORTED, "gemm_hl int16 view: planes larger than 2 GiB");
+    const ViewWs vw = view_ws(Mreal, nout);
+    if (!wsp.ws || wsp.bytes < vw.bytes)
+        return fail(wsp.strict ? VGEMM_ERR_UNSUPPORTED : VGEMM_ERR_ARG, "gemm_hl int16 view: needs a workspace of %zu bytes (AEpi.ws)", vw.bytes);
+    if (!aligned16(wsp.ws)) return fail(VGEMM_ERR_ARG, "gemm_hl: workspace must be 16-byte aligned");
+    char* ws = static_cast<char*>(wsp.ws);
+    p.vhi = E->vhi; p.vlo = E->vlo; p.vld = E->vld;
+    p.v_bytes = unsigned((long long)Mreal * E->vld);
+    p.vgroups = cdiv(nout, 32);
+    p.vmax = reinterpret_cast<uint32_t*>(ws + vw.max_off);
+    p.vmask = reinterpret_cast<uint32_t*>(ws + vw.mask_off);
+    p.vexp = reinterpret_cast<uint8_t*>(ws + vw.exp_off);
+    p.Y = nullptr; p.y_bytes = 0; p.R = nullptr; p.rowmax = nullptr;
+    stripe_grid(p);
+    int rc = hip_status(vk::launch_fill_u32(st, p.vmax, size_t(Mreal), 0u), "gemm_hl int16 view: row maxima clear");
+    if (rc) return rc;
+    rc = hip_status(vk::launch_stripe_view(A->src, epi, p, st), "gemm_hl int16 view launch");
+    if (rc) return rc;
+    return hip_status(vk::launch_view_fix(st, p.vmax, p.vexp, p.vmask, Mreal, nout, p.vgroups, E->vhi, E->vlo, E->vld, E->ve),
+                      "gemm_hl int16 view fix-up");
+}
+
 int hl2_impl(void* stream, const VgemmASrc* A, int Mp, int Mreal, const int8_t* W, int ldw, int Np, int Nreal, int Kp,
              const int32_t* cst, const VgemmAEpi* E, WsPolicy wsp) {
     if (!A || !E) return fail(VGEMM_ERR_ARG, "gemm_hl: null ASrc/AEpi");
@@ -295,7 +354,7 @@ int hl2_impl(void* stream, const VgemmASrc* A, int Mp, int Mreal, const int8_t* 
     if (Mreal < 0 || Mreal > Mp || Nreal < 0 || Nreal > Np) return fail(VGEMM_ERR_ARG, "gemm_hl: Mreal/Nreal outside Mp/Np");
     if (!W || !cst || ldw < Kp || ldw % 16 || !aligned16(W)) return fail(VGEMM_ERR_ARG, "gemm_hl: W must be 16-byte aligned with ldw >= Kp, ldw %% 16 == 0");
     if (E->epi < 0 || E->epi > VGEMM_EPI_QKV) return fail(VGEMM_ERR_ARG, "gemm_hl: unknown epilogue %d", E->epi);
-    if (E->epi != VGEMM_EPI_QKV && !E->Y) return fail(VGEMM_ERR_ARG, "gemm_hl: null Y");
+    if (E->epi != VGEMM_EPI_QKV && !E->Y && !E->vhi) return fail(VGEMM_ERR_ARG, "gemm_hl: null Y");
     // GroupNorm statistics (src/gemm_hl.h:22, src/engine.h:110): EPI_PLAIN, 32 groups of whole
     // columns, a block's rows in at most two samples
     if (E->gnstat && (E->epi != VGEMM_EPI_PLAIN || Nreal % 32 || E->gnT <= 0 || E->gnT % 64))
@@ -369,6 +428,7 @@ int hl2_impl(void* stream, const VgemmASrc* A, int Mp, int Mreal, const int8_t* 
 
     const int epi = E->epi;
     p.Y = E->Y; p.ldy = E->ldy; p.R = E->residual; p.Lphi = E->Lphi; p.rowmax = E->rowmax;
+    if (E->vhi) return view_impl(A, E, p, Mreal, Nreal, wsp, static_cast<hipStream_t>(stream));
     p.Cs = E->Cs; p.Y1 = E->Y1; p.Y2 = E->Y2;
     p.gnstat = static_cast<vk::GnStat*>(E->gnstat); p.gnT = E->gnT;
     p.heads = E->heads; p.qT = E->T; p.TpQ = E->TpQ; p.TpK = E->TpK; p.qC = E->C;

@@ -309,6 +309,46 @@ hipError_t launch_epilogue_geglu_q(hipStream_t st, const int32_t* Chi, const int
     hipLaunchKernelGGL(epilogue_geglu_q_kernel, dim3(unsigned(M)), dim3(256), 0, st, Chi, Clo, F, ldc, cst, e, L, hi, lo, eo, Kp);
     return hipGetLastError();
 }
+// Fix-up of the int16 view the row-stationary kernel writes (stripe_kernel.h, VIEW): one wave per
+// row, lanes over its 4-column words (coalesced). The row's exponent e = row_exp(max |y|) goes to
+// e[r]. A word of a 32-column group that was quantised at a running exponent ec < e is rewritten
+// from what it holds: with d the kept correction bit, y >> ec = q - d exactly; floor shifts compose,
+// so y >> (e - 1) = (y >> ec) >> (e - 1 - ec), and quant16_32(y, e) = clamp(((y >> (e - 1)) + 1)
+// >> 1). Words [F / 4, ld / 4) get the pad value (0, -128).
+__global__ void __launch_bounds__(256) view_fix_kernel(const uint32_t* __restrict__ vmax, const uint8_t* __restrict__ vexp,
+                                                       const uint32_t* __restrict__ vmask, int M, int F, int G,
+                                                       int8_t* __restrict__ hi, int8_t* __restrict__ lo, int ld, int32_t* __restrict__ e) {
+    const int r = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (r >= M) return;
+    const int ef = rowexp_u32(vmax[r]);
+    if (lane == 0) e[r] = ef;
+    unsigned* h = reinterpret_cast<unsigned*>(hi + size_t(r) * ld);
+    unsigned* l = reinterpret_cast<unsigned*>(lo + size_t(r) * ld);
+    const uint8_t* ex = vexp + size_t(r) * G;
+    const uint32_t* mk = vmask + size_t(r) * G;
+    const int F4 = F >> 2;
+    if (ef > 0) {
+        for (int w = lane; w < F4; w += 64) {
+            const int grp = w >> 3;
+            const int ec = ex[grp];
+            if (ec >= ef) continue;
+            const unsigned bits = mk[grp] >> (4 * (w & 7));
+            const int sh = ef - 1 - ec;
+            const unsigned hw = h[w], lw = l[w];
+            int q[4];
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int q0 = (int(int8_t(hw >> (8 * v))) << 8) | int(((lw >> (8 * v)) & 255u) ^ 0x80u);
+                const int fl = q0 - int((bits >> v) & 1u);
+                q[v] = min(max(((fl >> sh) + 1) >> 1, -32767), 32767);
+            }
+            h[w] = pack_hi4(q[0], q[1], q[2], q[3]);
+            l[w] = pack_lo4(q[0], q[1], q[2], q[3]);
+        }
+    }
+    for (int w = F4 + lane; w < (ld >> 2); w += 64) { h[w] = PAD_HI4; l[w] = PAD_LO4; }
+}
+
 // k_gn_init (src/kernels.cu:173): sum 0, mn INT_MAX, mx INT_MIN, ss 0 for cnt statistics records
 __global__ void __launch_bounds__(256) gn_init_kernel(GnStat* __restrict__ gs, int n) {
     const int i = blockIdx.x * 256 + threadIdx.x;
@@ -320,6 +360,11 @@ __global__ void __launch_bounds__(256) gn_init_kernel(GnStat* __restrict__ gs, i
     }
 }
 
+hipError_t launch_view_fix(hipStream_t st, const uint32_t* vmax, const uint8_t* vexp, const uint32_t* vmask, int M, int F, int G, int8_t* hi,
+                           int8_t* lo, int ld, int32_t* e) {
+    hipLaunchKernelGGL(view_fix_kernel, dim3(blocks_for(M, 4)), dim3(256), 0, st, vmax, vexp, vmask, M, F, G, hi, lo, ld, e);
+    return hipGetLastError();
+}
 hipError_t launch_gn_init(hipStream_t st, GnStat* gs, int n) {
     hipLaunchKernelGGL(gn_init_kernel, dim3(unsigned((n + 255) / 256)), dim3(256), 0, st, gs, n);
     return hipGetLastError();

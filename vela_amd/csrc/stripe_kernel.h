@@ -77,8 +77,9 @@ constexpr unsigned STRIPE_LUT_RAW = 8192;
 enum { FORM_INT = 0, FORM_EXACT = 1 };
 
 // RES: the PLAIN instantiation for calls with a residual (its own kernel, so that the residual
-// loads do not shape the code of the others)
-template <int SRC, int EPI, bool RES = false>
+// loads do not shape the code of the others). VIEW: the int16-view instantiation (no Y; see the
+// view loop below).
+template <int SRC, int EPI, bool RES = false, bool VIEW = false>
 __global__ void __launch_bounds__(256, 2) stripe_kernel(const GemmParams p) {
     using S = StripeCfg;
     constexpr int CH = S::CH, NKS = S::NKS, BM = S::BM;
@@ -90,6 +91,7 @@ __global__ void __launch_bounds__(256, 2) stripe_kernel(const GemmParams p) {
     static_assert(SRC == SRC_I16 || SRC == SRC_I8, "stripe sources");
     static_assert(EPI == EPI_PLAIN || EPI == EPI_GEGLU || EPI == EPI_GELU, "stripe epilogues");
     static_assert(!RES || EPI == EPI_PLAIN, "residual: PLAIN only");
+    static_assert(!(RES && VIEW), "the int16 view takes no residual");
 
     __shared__ __attribute__((aligned(16))) StripeShared<NEEDLUT> sh;
 
@@ -337,7 +339,7 @@ __global__ void __launch_bounds__(256, 2) stripe_kernel(const GemmParams p) {
     };
 
     bool pipelined = false;
-    if constexpr (!RES) {
+    if constexpr (!RES && !VIEW) {
         if (form == FORM_INT) {
             pipelined = true;
             // ---- software-pipelined chunk loop (integer form). The MFMAs of chunk c run interleaved
@@ -491,6 +493,171 @@ __global__ void __launch_bounds__(256, 2) stripe_kernel(const GemmParams p) {
             }
         }
     }
+    if constexpr (VIEW) {
+        // ---- int16 view (quant_row_out semantics, src/kernels.cu:317-331, on this GEMM's outputs).
+        // The MFMAs take W as the A operand and the activations as the B operand, so that the
+        // accumulators are transposed: lane l holds activation row rbase + lc and, of each 32-row W
+        // subtile u, the W rows 8g + 4 lh + v (element i = 4g + v). A chunk's outputs of one row then
+        // sit in two lanes (lh = 0, 1), and its row maximum is the lane's own maximum and one
+        // exchange. The row exponent is not known until every chunk of the row is done, so each chunk
+        // is quantised at the running exponent e_c = row_exp(max |y| over the row's chunks so far in
+        // this block), which the final e can only exceed. Per element the bit d = (y >> e_c) - q (0
+        // or -1; q is the clamped rounding quotient) is kept, so that y >> e_c = q + d can be
+        // recovered; since floor shifts compose, y >> (e - 1) = (y >> e_c) >> (e - 1 - e_c) for any
+        // e > e_c, and the final value (that + 1) >> 1 (clamped) follows exactly. Per (row, 32-column
+        // group) the chunk's e_c and the 32 bits go to the workspace, the row maximum to vmax; the
+        // fix-up pass (producers.hip) rewrites the groups whose e_c fell short of the row's e.
+        constexpr int NU = GEGLU ? 1 : S::NSUB;       // 32-output groups per chunk
+        constexpr int NOV = 16 * NU;                  // outputs of a lane per chunk
+        constexpr int VST = NU * 10;                  // stores per lane per chunk: 8 plane words, a mask, an exponent
+        const __amdgpu_buffer_rsrc_t rH = make_rsrc(p.vhi, p.v_bytes), rLo = make_rsrc(p.vlo, p.v_bytes);
+        const unsigned gbytes = unsigned(p.Mreal) * unsigned(p.vgroups);
+        const __amdgpu_buffer_rsrc_t rM = make_rsrc(p.vmask, gbytes * 4u), rE = make_rsrc(p.vexp, gbytes);
+        const int r = rbase + lc;
+        const bool rok = r < p.Mreal;
+        const int erl = sh.erow[wave * 32 + lc];     // the exact form's shift of the lane's row
+        unsigned mrun = 0;                           // running max |y| of the lane's row
+        const bool lean_v = form == FORM_INT;
+        for (int c = cb; c < ce; ++c) {
+            const int stage = (c - cb) & 1;
+            // chunk c's DMA is done once at most the previous chunk's stores are outstanding (every
+            // lane issues exactly VST stores per chunk: rows, columns and lanes without output store
+            // to an out-of-range offset); the exact form also loads, so it waits for everything
+            if (c > cb && lean_v) vm_wait<VST>();
+            else vm_wait<0>();
+            block_barrier();
+            if (c + 1 < ce) issue(c + 1, stage ^ 1);
+
+            v16i acc_h[S::NSUB], acc_l[S::NSUB];
+#pragma unroll
+            for (int u = 0; u < S::NSUB; ++u)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) { acc_h[u][i] = 0; acc_l[u][i] = 0; }
+            const unsigned char* sW = sh.w[stage];
+            auto wfrag = [&](int t, int u) -> v4i {
+                return *reinterpret_cast<const v4i*>(sW + (t >> 1) * S::KSTEP + swz(32 * u + lc, 2 * (t & 1) + lh));
+            };
+            constexpr int PF = 2;
+            v4i wq[PF][S::NSUB];
+#pragma unroll
+            for (int t = 0; t < PF; ++t)
+#pragma unroll
+                for (int u = 0; u < S::NSUB; ++u) wq[t][u] = wfrag(t, u);
+#pragma unroll
+            for (int t = 0; t < NKS; ++t) {
+                v4i wf[S::NSUB];
+#pragma unroll
+                for (int u = 0; u < S::NSUB; ++u) {
+                    wf[u] = wq[t % PF][u];
+                    if (t + PF < NKS) wq[t % PF][u] = wfrag(t + PF, u);
+                }
+#pragma unroll
+                for (int u = 0; u < S::NSUB; ++u) {
+                    acc_h[u] = __builtin_amdgcn_mfma_i32_32x32x32_i8(wf[u], hf[t], acc_h[u], 0, 0, 0);
+                    acc_l[u] = __builtin_amdgcn_mfma_i32_32x32x32_i8(wf[u], lf[t], acc_l[u], 0, 0, 0);
+                }
+                if (t + PF < NKS) __builtin_amdgcn_sched_group_barrier(0x100, S::NSUB, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, 2 * S::NSUB, 0);
+            }
+
+            // ---- the lane's outputs of chunk c: o = 16 u + i is W row 32 u + j of the chunk, j = 8 (i >> 2) + 4 lh + (i & 3)
+            // (GEGLU: a row j, g row 32 + j, output j). Columns past the output come out 0: their table
+            // entries and W rows are zero (integer form), and the int64 form is masked.
+            const int tb = (c - cb) * CH;
+            const int oc0 = GEGLU ? c * (CH / 2) : c * CH;   // first output column of the chunk
+            int y[NOV];
+            if (form == FORM_INT) {
+#pragma unroll
+                for (int o = 0; o < NOV; ++o) {
+                    const int u = o >> 4, i = o & 15;
+                    const int j = 32 * u + 8 * (i >> 2) + 4 * lh + (i & 3);
+                    const int4 ka = sh.tab[tb + j];
+                    if constexpr (GEGLU) {
+                        const int4 kg = sh.tab[tb + 32 + j];
+                        const int yg = req((acc_h[1][i] << 8) + acc_l[1][i], kg);
+                        unsigned h0, hb;
+                        const int ge = mulsh16(yg, phi(yg), h0);
+                        const unsigned yb = mulsh16b(req((acc_h[0][i] << 8) + acc_l[0][i], ka), ge, hb);
+                        asm("" : "+v"(hb));
+                        const int sat = (int(hb) >> 31) ^ 0x7fffffff;
+                        y[o] = hb > 65535u ? sat : int(yb ^ 0x80000000u);
+                    } else if constexpr (EPI == EPI_GELU) {
+                        const int ya = req((acc_h[u][i] << 8) + acc_l[u][i], ka);
+                        unsigned h0;
+                        y[o] = mulsh16(ya, phi(ya), h0);
+                    } else {
+                        y[o] = req((acc_h[u][i] << 8) + acc_l[u][i], ka);
+                    }
+                }
+            } else {
+#pragma unroll 1
+                for (int o = 0; o < NOV; ++o) {
+                    const int u = o >> 4, i = o & 15;
+                    const int j = 32 * u + 8 * (i >> 2) + 4 * lh + (i & 3);
+                    const int col = oc0 + j;
+                    const int cc = col < nlim ? col : 0;
+                    const int4 ca = p.cst[GEGLU ? 2 * cc : cc];
+                    const int ya = epi1_exact(acc_h[u][i], acc_l[u][i], ca.x, ca.y, ca.z, ca.w, erl);
+                    int v;
+                    if constexpr (GEGLU) {
+                        const int4 cg = p.cst[2 * cc + 1];
+                        const int yg = epi1_exact(acc_h[1][i], acc_l[1][i], cg.x, cg.y, cg.z, cg.w, erl);
+                        const i64 pg = lut_lds ? phi(yg) : lut16i(yg, p.Lphi);
+                        const i64 ge = sat32(rshr(i64(yg) * pg, 16));
+                        v = int(sat32(rshr(i64(ya) * ge, 16)));
+                    } else if constexpr (EPI == EPI_GELU) {
+                        const i64 pa = lut_lds ? phi(ya) : lut16i(ya, p.Lphi);
+                        v = int(sat32(rshr(i64(ya) * pa, 16)));
+                    } else {
+                        v = ya;
+                    }
+                    y[o] = col < nlim ? v : 0;
+                }
+            }
+            // running row maximum of |y| (from the signed maximum and minimum) and exponent
+            int mx = 0, mn = 0;
+#pragma unroll
+            for (int o = 0; o < NOV; ++o) { mx = max(mx, y[o]); mn = min(mn, y[o]); }
+            unsigned m = max(mrun, max(unsigned(mx), 0u - unsigned(mn)));
+            m = max(m, unsigned(__shfl_xor(int(m), 32)));
+            mrun = m;
+            const int ec = rowexp_u32(m);
+            // quantise at ec: t = y >> (ec - 1) (y << 1 for ec = 0), floor y >> ec = t >> 1, rounded
+            // q = clamp((t + 1) >> 1), correction d = (y >> ec) - q in {0, -1}
+            const int sl = ec == 0 ? 1 : 0, sr = ec == 0 ? 0 : ec - 1;
+#pragma unroll
+            for (int u = 0; u < NU; ++u) {
+                unsigned bits = 0;   // bit 8g + v (this lane's half; shifted to 8g + 4 lh + v below)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    int q[4];
+#pragma unroll
+                    for (int vv = 0; vv < 4; ++vv) {
+                        const int t = (y[16 * u + 4 * g + vv] << sl) >> sr;
+                        q[vv] = min(max((t + 1) >> 1, -32767), 32767);
+                        bits |= unsigned((t >> 1) - q[vv]) & (1u << (8 * g + vv));
+                    }
+                    // bytes 1 (hi) and 0 (lo, biased by 128) of the four values, one word each
+                    const unsigned hw = __builtin_amdgcn_perm(unsigned(q[1]), unsigned(q[0]), 0x0c0c0501u) |
+                                        __builtin_amdgcn_perm(unsigned(q[3]), unsigned(q[2]), 0x05010c0cu);
+                    const unsigned lw = (__builtin_amdgcn_perm(unsigned(q[1]), unsigned(q[0]), 0x0c0c0400u) |
+                                         __builtin_amdgcn_perm(unsigned(q[3]), unsigned(q[2]), 0x04000c0cu)) ^ 0x80808080u;
+                    const int col = oc0 + 32 * u + 8 * g + 4 * lh;
+                    const unsigned off = rok && col < nlim ? unsigned(r) * unsigned(p.vld) + unsigned(col) : OOB;
+                    __builtin_amdgcn_raw_buffer_store_b32(hw, rH, int(off), 0, 0);
+                    __builtin_amdgcn_raw_buffer_store_b32(lw, rLo, int(off), 0, 0);
+                }
+                bits <<= 4 * lh;
+                bits |= unsigned(__shfl_xor(int(bits), 32));
+                const int grp = (oc0 >> 5) + u;
+                const bool gok = rok && lh == 0 && grp < p.vgroups;
+                const unsigned gi = unsigned(r) * unsigned(p.vgroups) + unsigned(grp);
+                __builtin_amdgcn_raw_buffer_store_b32(int(bits), rM, int(gok ? gi * 4u : OOB), 0, 0);
+                __builtin_amdgcn_raw_buffer_store_b8((unsigned char)ec, rE, int(gok ? gi : OOB), 0, 0);
+            }
+        }
+        if (rok && lh == 0 && mrun) atomicMax(p.vmax + r, mrun);
+    } else {
     if (!pipelined) {
         for (int c = cb; c < ce; ++c) {
             const int stage = (c - cb) & 1;
@@ -686,7 +853,9 @@ __global__ void __launch_bounds__(256, 2) stripe_kernel(const GemmParams p) {
         }
     }
 
-    if (p.rowmax) {
+    }   // !VIEW
+
+    if (!VIEW && p.rowmax) {
         // lanes with the same lh hold the same 16 rows: reduce over the 32 columns, one atomic per row
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
@@ -714,6 +883,19 @@ hipError_t launch_stripe_t(int epi, const GemmParams& p, hipStream_t st) {
     return hipGetLastError();
 }
 
+template <int SRC>
+hipError_t launch_stripe_view_t(int epi, const GemmParams& p, hipStream_t st) {
+    const dim3 grid(unsigned(p.mtiles * p.ntiles));
+    switch (epi) {
+    case EPI_PLAIN: hipLaunchKernelGGL((stripe_kernel<SRC, EPI_PLAIN, false, true>), grid, dim3(256), 0, st, p); break;
+    case EPI_GEGLU: hipLaunchKernelGGL((stripe_kernel<SRC, EPI_GEGLU, false, true>), grid, dim3(256), 0, st, p); break;
+    case EPI_GELU: hipLaunchKernelGGL((stripe_kernel<SRC, EPI_GELU, false, true>), grid, dim3(256), 0, st, p); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
 hipError_t launch_stripe(int src, int epi, const GemmParams& p, hipStream_t st);
+hipError_t launch_stripe_view(int src, int epi, const GemmParams& p, hipStream_t st);
 
 }  // namespace vk

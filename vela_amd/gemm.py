@@ -19,7 +19,7 @@ SRC_I8, SRC_X32, SRC_CONV32, SRC_I16, SRC_CONV16 = 0, 1, 2, 3, 4
 __all__ = [
     "ASrc", "AEpi", "VgemmError", "EPI_PLAIN", "EPI_SPLIT3", "EPI_GEGLU", "EPI_GELU", "EPI_QKV",
     "SRC_I8", "SRC_X32", "SRC_CONV32", "SRC_I16", "SRC_CONV16", "k_gemm_hl2", "k_gemm_hl", "k_conv_e",
-    "gemm_hl_supported", "set_variant", "get_variant", "set_splitk", "set_tile_order", "conv16_halo_rows", "workspace_bytes", "Gemm",
+    "gemm_hl_supported", "set_variant", "get_variant", "set_splitk", "set_tile_order", "conv16_halo_rows", "workspace_bytes", "view_workspace_bytes", "Gemm",
     "k_quant_rows", "k_epilogue", "k_pixmax", "k_im2col3", "k_epilogue_split", "k_epilogue_geglu_q",
     "fill_u32", "Graph", "ptr", "stream_ptr", "GNSTAT_BYTES", "gn_stats_alloc", "k_gn_init", "gn_stats_read",
 ]
@@ -104,6 +104,11 @@ def conv16_halo_rows(H: int, W: int, C: int, stride: int, epi: int = EPI_PLAIN) 
 
 def workspace_bytes(Mp: int, Mreal: int, Np: int, Nreal: int, Kp: int, epi: int = EPI_PLAIN) -> int:
     return int(load().vgemm_workspace_bytes(Mp, Mreal, Np, Nreal, Kp, epi))
+
+
+def view_workspace_bytes(Mreal: int, Nreal: int, epi: int = EPI_PLAIN) -> int:
+    """Workspace bytes of the int16 view (AEpi.vhi/vlo/ve) for an Mreal x Nreal call."""
+    return int(load().vgemm_view_workspace_bytes(Mreal, Nreal, epi))
 
 
 class Gemm:
