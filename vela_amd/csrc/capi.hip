@@ -210,7 +210,7 @@ int pick_tile_order(const vk::GemmParams& p, double a_bytes) {
     return col < 0.75 * row ? 1 : 0;
 }
 
-// Workspace of the int16 view: row maxima [M], masks [M x G] and exponent bytes [M x G], G = the
+// Workspace of the int16 view: row maxima [M], masks [G x M] and exponent bytes [G x M], G = the
 // output's 32-column groups, each part 256-byte aligned.
 struct ViewWs { size_t max_off, mask_off, exp_off, bytes; };
 ViewWs view_ws(int M, int nout) {

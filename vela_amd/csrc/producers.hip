@@ -48,6 +48,50 @@ __global__ void __launch_bounds__(256) quant_rows_kernel(const int32_t* __restri
     }
 }
 
+// The same for rows of at most 64 NV int4 words held in registers: one 16-byte load per word, the
+// row read once (the general kernel above reads it twice). Needs ldx % 4 == 0 and a 16-byte aligned X.
+template <int NV>
+__global__ void __launch_bounds__(256) quant_rows_vec_kernel(const int32_t* __restrict__ X, int M, int Mp, int K, int ldx,
+                                                             int8_t* __restrict__ hi, int8_t* __restrict__ lo,
+                                                             int32_t* __restrict__ e, int Kp) {
+    const int r = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (r >= Mp) return;
+    unsigned* h = reinterpret_cast<unsigned*>(hi + size_t(r) * Kp);
+    unsigned* l = reinterpret_cast<unsigned*>(lo + size_t(r) * Kp);
+    const int K4 = Kp >> 2;
+    if (r >= M) {
+        for (int k = lane; k < K4; k += 64) { h[k] = PAD_HI4; l[k] = PAD_LO4; }
+        return;
+    }
+    const int4* x = reinterpret_cast<const int4*>(X + size_t(r) * ldx);
+    int4 v[NV];
+    uint32_t m = 0;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int k4 = lane + 64 * j;
+        v[j] = make_int4(0, 0, 0, 0);
+        if (4 * k4 + 3 < K) v[j] = x[k4];
+        else if (4 * k4 < K) {   // the row's last, partial word
+            const int32_t* xs = reinterpret_cast<const int32_t*>(x + k4);
+            v[j].x = xs[0];
+            if (4 * k4 + 1 < K) v[j].y = xs[1];
+            if (4 * k4 + 2 < K) v[j].z = xs[2];
+        }
+        m = max(max(m, max(uabs(v[j].x), uabs(v[j].y))), max(uabs(v[j].z), uabs(v[j].w)));
+    }
+    const int ee = rowexp_u32(wave_umax(m));
+    if (lane == 0) e[r] = ee;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int k4 = lane + 64 * j;
+        if (k4 < K4) {
+            const int q0 = quant16_32(v[j].x, ee), q1 = quant16_32(v[j].y, ee), q2 = quant16_32(v[j].z, ee), q3 = quant16_32(v[j].w, ee);
+            h[k4] = pack_hi4(q0, q1, q2, q3);
+            l[k4] = pack_lo4(q0, q1, q2, q3);
+        }
+    }
+}
+
 // k_pixmax (src/kernels.cu:106-115): pm[row] = max_c |X[row, c]|, one wave per row.
 __global__ void __launch_bounds__(256) pixmax_kernel(const int32_t* __restrict__ X, int rows, int C, uint32_t* __restrict__ pm) {
     const int r = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
@@ -271,7 +315,19 @@ static inline unsigned blocks_for(size_t n, size_t per) { return unsigned((n + p
 
 hipError_t launch_quant_rows(hipStream_t st, const int32_t* X, int M, int K, int ldx, int8_t* hi, int8_t* lo, int32_t* e, int Kp) {
     const int Mp = (M + 31) / 32 * 32;
-    hipLaunchKernelGGL(quant_rows_kernel, dim3(blocks_for(Mp, 4)), dim3(256), 0, st, X, M, Mp, K, ldx, hi, lo, e, Kp);
+    const dim3 grid(blocks_for(Mp, 4));
+    const int words = (Kp / 4 + 63) / 64;   // int4 words per lane
+    if (ldx % 4 == 0 && (reinterpret_cast<uintptr_t>(X) & 15) == 0 && words <= 8) {
+        switch (words) {
+        case 1: hipLaunchKernelGGL(quant_rows_vec_kernel<1>, grid, dim3(256), 0, st, X, M, Mp, K, ldx, hi, lo, e, Kp); break;
+        case 2: hipLaunchKernelGGL(quant_rows_vec_kernel<2>, grid, dim3(256), 0, st, X, M, Mp, K, ldx, hi, lo, e, Kp); break;
+        case 3:
+        case 4: hipLaunchKernelGGL(quant_rows_vec_kernel<4>, grid, dim3(256), 0, st, X, M, Mp, K, ldx, hi, lo, e, Kp); break;
+        default: hipLaunchKernelGGL(quant_rows_vec_kernel<8>, grid, dim3(256), 0, st, X, M, Mp, K, ldx, hi, lo, e, Kp); break;
+        }
+        return hipGetLastError();
+    }
+    hipLaunchKernelGGL(quant_rows_kernel, grid, dim3(256), 0, st, X, M, Mp, K, ldx, hi, lo, e, Kp);
     return hipGetLastError();
 }
 hipError_t launch_pixmax(hipStream_t st, const int32_t* X, int rows, int C, uint32_t* pm) {
@@ -314,7 +370,8 @@ hipError_t launch_epilogue_geglu_q(hipStream_t st, const int32_t* Chi, const int
 // e[r]. A word of a 32-column group that was quantised at a running exponent ec < e is rewritten
 // from what it holds: with d the kept correction bit, y >> ec = q - d exactly; floor shifts compose,
 // so y >> (e - 1) = (y >> ec) >> (e - 1 - ec), and quant16_32(y, e) = clamp(((y >> (e - 1)) + 1)
-// >> 1). Words [F / 4, ld / 4) get the pad value (0, -128).
+// >> 1). Exponents and masks are group-major ([group][row]). Words [F / 4, ld / 4) get the pad
+// value (0, -128).
 __global__ void __launch_bounds__(256) view_fix_kernel(const uint32_t* __restrict__ vmax, const uint8_t* __restrict__ vexp,
                                                        const uint32_t* __restrict__ vmask, int M, int F, int G,
                                                        int8_t* __restrict__ hi, int8_t* __restrict__ lo, int ld, int32_t* __restrict__ e) {
@@ -324,15 +381,13 @@ __global__ void __launch_bounds__(256) view_fix_kernel(const uint32_t* __restric
     if (lane == 0) e[r] = ef;
     unsigned* h = reinterpret_cast<unsigned*>(hi + size_t(r) * ld);
     unsigned* l = reinterpret_cast<unsigned*>(lo + size_t(r) * ld);
-    const uint8_t* ex = vexp + size_t(r) * G;
-    const uint32_t* mk = vmask + size_t(r) * G;
     const int F4 = F >> 2;
     if (ef > 0) {
         for (int w = lane; w < F4; w += 64) {
             const int grp = w >> 3;
-            const int ec = ex[grp];
+            const int ec = vexp[size_t(grp) * M + r];
             if (ec >= ef) continue;
-            const unsigned bits = mk[grp] >> (4 * (w & 7));
+            const unsigned bits = vmask[size_t(grp) * M + r] >> (4 * (w & 7));
             const int sh = ef - 1 - ec;
             const unsigned hw = h[w], lw = l[w];
             int q[4];

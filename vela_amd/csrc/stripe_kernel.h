@@ -509,7 +509,7 @@ __global__ void __launch_bounds__(256, 2) stripe_kernel(const GemmParams p) {
         // fix-up pass (producers.hip) rewrites the groups whose e_c fell short of the row's e.
         constexpr int NU = GEGLU ? 1 : S::NSUB;       // 32-output groups per chunk
         constexpr int NOV = 16 * NU;                  // outputs of a lane per chunk
-        constexpr int VST = NU * 10;                  // stores per lane per chunk: 8 plane words, a mask, an exponent
+        constexpr int VST = NU * 6;                   // stores per lane per chunk: 4 plane pieces, a mask, an exponent
         const __amdgpu_buffer_rsrc_t rH = make_rsrc(p.vhi, p.v_bytes), rLo = make_rsrc(p.vlo, p.v_bytes);
         const unsigned gbytes = unsigned(p.Mreal) * unsigned(p.vgroups);
         const __amdgpu_buffer_rsrc_t rM = make_rsrc(p.vmask, gbytes * 4u), rE = make_rsrc(p.vexp, gbytes);
@@ -628,6 +628,7 @@ __global__ void __launch_bounds__(256, 2) stripe_kernel(const GemmParams p) {
 #pragma unroll
             for (int u = 0; u < NU; ++u) {
                 unsigned bits = 0;   // bit 8g + v (this lane's half; shifted to 8g + 4 lh + v below)
+                unsigned hw[4], lw[4];
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
                     int q[4];
@@ -637,21 +638,37 @@ __global__ void __launch_bounds__(256, 2) stripe_kernel(const GemmParams p) {
                         q[vv] = min(max((t + 1) >> 1, -32767), 32767);
                         bits |= unsigned((t >> 1) - q[vv]) & (1u << (8 * g + vv));
                     }
-                    // bytes 1 (hi) and 0 (lo, biased by 128) of the four values, one word each
-                    const unsigned hw = __builtin_amdgcn_perm(unsigned(q[1]), unsigned(q[0]), 0x0c0c0501u) |
-                                        __builtin_amdgcn_perm(unsigned(q[3]), unsigned(q[2]), 0x05010c0cu);
-                    const unsigned lw = (__builtin_amdgcn_perm(unsigned(q[1]), unsigned(q[0]), 0x0c0c0400u) |
-                                         __builtin_amdgcn_perm(unsigned(q[3]), unsigned(q[2]), 0x04000c0cu)) ^ 0x80808080u;
-                    const int col = oc0 + 32 * u + 8 * g + 4 * lh;
-                    const unsigned off = rok && col < nlim ? unsigned(r) * unsigned(p.vld) + unsigned(col) : OOB;
-                    __builtin_amdgcn_raw_buffer_store_b32(hw, rH, int(off), 0, 0);
-                    __builtin_amdgcn_raw_buffer_store_b32(lw, rLo, int(off), 0, 0);
+                    // bytes 1 (hi) and 0 (lo, biased by 128) of the four values (columns 8g + 4 lh + v)
+                    hw[g] = __builtin_amdgcn_perm(unsigned(q[1]), unsigned(q[0]), 0x0c0c0501u) |
+                            __builtin_amdgcn_perm(unsigned(q[3]), unsigned(q[2]), 0x05010c0cu);
+                    lw[g] = (__builtin_amdgcn_perm(unsigned(q[1]), unsigned(q[0]), 0x0c0c0400u) |
+                             __builtin_amdgcn_perm(unsigned(q[3]), unsigned(q[2]), 0x04000c0cu)) ^ 0x80808080u;
                 }
+                // the two lanes of a row swap halves: lane lh = 0 gathers the 32 hi bytes of the group,
+                // lane lh = 1 the 32 lo bytes, so that each plane's row segment goes out as whole 16-byte
+                // pieces (full 32-byte sectors per row and plane, no partial-sector writes)
+                unsigned wv[8];
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const unsigned recv = unsigned(__shfl_xor(int(lh ? hw[g] : lw[g]), 32));
+                    wv[2 * g] = lh ? recv : hw[g];
+                    wv[2 * g + 1] = lh ? lw[g] : recv;
+                }
+                const v4i s0 = {int(wv[0]), int(wv[1]), int(wv[2]), int(wv[3])}, s1 = {int(wv[4]), int(wv[5]), int(wv[6]), int(wv[7])};
+                const int col = oc0 + 32 * u;
+                const unsigned rb = unsigned(r) * unsigned(p.vld) + unsigned(col);
+                // columns [nlim, 16-column boundary) get y = 0, i.e. the pad value (0, -128)
+                const unsigned o0 = rok && col < nlim ? rb : OOB, o1 = rok && col + 16 < nlim ? rb + 16u : OOB;
+                __builtin_amdgcn_raw_buffer_store_b128(s0, rH, int(lh ? OOB : o0), 0, 0);
+                __builtin_amdgcn_raw_buffer_store_b128(s1, rH, int(lh ? OOB : o1), 0, 0);
+                __builtin_amdgcn_raw_buffer_store_b128(s0, rLo, int(lh ? o0 : OOB), 0, 0);
+                __builtin_amdgcn_raw_buffer_store_b128(s1, rLo, int(lh ? o1 : OOB), 0, 0);
                 bits <<= 4 * lh;
                 bits |= unsigned(__shfl_xor(int(bits), 32));
+                // group-major: the rows of a group are consecutive, so these stores are contiguous
                 const int grp = (oc0 >> 5) + u;
                 const bool gok = rok && lh == 0 && grp < p.vgroups;
-                const unsigned gi = unsigned(r) * unsigned(p.vgroups) + unsigned(grp);
+                const unsigned gi = unsigned(grp) * unsigned(p.Mreal) + unsigned(r);
                 __builtin_amdgcn_raw_buffer_store_b32(int(bits), rM, int(gok ? gi * 4u : OOB), 0, 0);
                 __builtin_amdgcn_raw_buffer_store_b8((unsigned char)ec, rE, int(gok ? gi : OOB), 0, 0);
             }

@@ -71,8 +71,8 @@ struct GemmParams {
     int32_t *qe, *ke;
     long long *qhs, *qls, *qts, *khs, *kls, *kts;
     // int16 view of the output (row-stationary kernel): hi/lo planes [rows x vld] written at each
-    // chunk's running row exponent, with per-(row, 32-column group) exponents vexp and correction
-    // bits vmask for the fix-up pass, and the row maxima vmax (all in the workspace)
+    // chunk's running row exponent, with per-(32-column group, row) exponents vexp and correction
+    // bits vmask (group-major) for the fix-up pass, and the row maxima vmax (all in the workspace)
     int8_t *vhi, *vlo; int vld; unsigned v_bytes;
     uint32_t* vmax; uint8_t* vexp; uint32_t* vmask; int vgroups;
 };
