@@ -14,7 +14,7 @@ replay, every other config's time, and the CPU baseline: the oracle restatement 
 integer semantics (the reference has no CPU GEMM of its own), timed on this host's cores.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-unet] [--no-cpu] [--no-configs]
-       python bench.py --only {c1,c2,c2plain,c3,c4a,c4b,c4c,copy,unet<i>}   (one kernel, for profiler runs)
+       python bench.py --only {c1,c2,c2plain,c2view,c3,c4a,c4b,c4c,copy,norms,unet<i>}   (one kernel, for profiler runs)
        python bench.py --unet-layers   (each C5 layer timed alone)
 """
 from __future__ import annotations
@@ -34,7 +34,7 @@ PEAK_HBM_GBS = 8000.0        # MI355X HBM3E, 8 TB/s
 METRIC = "effective W8A16 TOPS & % int8 MFMA peak; UNet GEMM-set ms at batch 8"
 
 
-ONLY_NAMES = ("c1", "c2", "c2plain", "c2view", "c3", "c4a", "c4b", "c4c", "copy")
+ONLY_NAMES = ("c1", "c2", "c2plain", "c2view", "c3", "c4a", "c4b", "c4c", "copy", "norms")
 COPY_BYTES = 256 << 20       # the calibration copy of --only copy: 256 MiB read + 256 MiB written
 
 
@@ -67,6 +67,31 @@ def time_launches(fn, stream, steps, warmup):
     t1.record(stream)
     torch.cuda.synchronize()
     return t0.elapsed_time(t1) / steps
+
+
+def time_graphed(fn, stream, reps, replays):
+    """Average duration of one `fn` call with no host launch cost in it: `reps` calls captured into one
+    HIP graph on `stream`, replayed `replays` times between HIP events (after two untimed replays)."""
+    import torch
+    from vela_amd import gemm as vg
+
+    g = vg.Graph(stream)
+    g.begin()
+    for _ in range(reps):
+        fn()
+    g.end()
+    for _ in range(2):
+        g.replay()
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for _ in range(replays):
+        g.replay()
+    t1.record(stream)
+    torch.cuda.synchronize()
+    g.destroy()
+    return t0.elapsed_time(t1) / (reps * replays)
 
 
 def pmc_traffic():
@@ -146,6 +171,48 @@ class ViewRun:
         vg.fill_u32(p.rowmax, 0, stream=stream)
         p.run(stream=stream)
         vg.k_quant_rows(p.y, L.M, L.Nout, L.Nout, self.hi, self.lo, self.e, L.Nout, stream=stream)
+
+
+def norms_lines(stream, steps, warmup):
+    """GroupNorm of a UNet activation X [8, 4096, 320] (32 groups) as a resnet runs it after a GEMM
+    that gathered the sum/min/max in its epilogue: fin1, the squared deviations (stats2: reads X),
+    the row apply with SiLU and the pixel maxima (reads X, writes Y); and LayerNorm to the int16 view
+    of the transformer input [8 * 4096, 320]. Bytes are the algorithmic reads and writes."""
+    import torch
+    from vela_amd import gemm as vg
+    from vela_amd import norms as vn
+
+    B, T, C, G = 8, 4096, 320, 32
+    M = B * T
+    g = torch.Generator(device="cuda")
+    g.manual_seed(11)
+    x = torch.randint(-(1 << 20), 1 << 20, (M, C), generator=g, device="cuda", dtype=torch.int32)
+    gam = torch.randint(30000, 90000, (C,), generator=g, device="cuda", dtype=torch.int32)
+    bet = torch.randint(-20000, 20000, (C,), generator=g, device="cuda", dtype=torch.int32)
+    lut = torch.arange(2049, device="cuda", dtype=torch.int32) * 32
+    gs = vg.gn_stats_alloc(B * G)
+    y = torch.empty_like(x)
+    pm = torch.empty(M, device="cuda", dtype=torch.int32)
+    hi = torch.empty((M, C), device="cuda", dtype=torch.int8)
+    lo = torch.empty_like(hi)
+    e = torch.empty(M, device="cuda", dtype=torch.int32)
+    vn.k_gn_stats1(x, B, T, C, G, gs)   # the records a producing GEMM's epilogue would leave
+    torch.cuda.synchronize()
+
+    def t_us(fn):
+        return round(time_graphed(fn, stream, 20, max(2, steps // 20)) * 1e3, 2)
+
+    xb = M * C * 4
+    res = {}
+    us = t_us(lambda: vn.k_gn_stats2(x, B, T, C, G, 100000, gs, stream=stream))
+    res["gn_stats2 [8,4096,320]"] = {"us": us, "gbs": round(xb / (us * 1e-6) / 1e9, 1)}
+    us = t_us(lambda: vn.k_gn_apply_row(x, B, T, C, G, gs, gam, bet, lut, y, pm, None, None, None, 0, stream=stream))
+    res["gn_apply_row + SiLU + pm [8,4096,320]"] = {"us": us, "gbs": round((2 * xb + 4 * M) / (us * 1e-6) / 1e9, 1)}
+    us = t_us(lambda: vn.k_gn_stats1(x, B, T, C, G, gs, stream=stream))
+    res["gn_stats1 [8,4096,320]"] = {"us": us, "gbs": round(xb / (us * 1e-6) / 1e9, 1)}
+    us = t_us(lambda: vn.k_lnorm_q(x, M, C, gam, bet, 100000, hi, lo, e, C, stream=stream))
+    res["lnorm_q [32768,320] -> int16 view"] = {"us": us, "gbs": round((xb + 2 * M * C + 4 * M) / (us * 1e-6) / 1e9, 1)}
+    return res
 
 
 def dropin_sources(stream, steps, warmup):
@@ -365,6 +432,11 @@ def main():
             del p
         log(f"[bench] C5 layers launched one at a time: {total:.3f} ms in total")
         return
+    if args.only == "norms":
+        res = norms_lines(stream, args.steps, args.warmup)
+        log(f"[bench] norms: {res}")
+        print(json.dumps({"workload": "integer norms, UNet 64x64 activation", "lines": res}), flush=True)
+        return
     if args.only == "c2view":
         L = cf.c2(cf.EPI_GEGLU)
         p = cf.DeviceProblem(L)
@@ -461,6 +533,11 @@ def main():
     if not args.no_configs:
         out["dropin_sources"] = dropin_sources(stream, max(5, args.steps // 4), max(2, args.warmup // 4))
         log(f"[bench] drop-in sources: {out['dropin_sources']}")
+
+    # ---- the integer normalisations around the GEMMs, at the UNet's 64x64 resolution
+    if not args.no_configs:
+        out["norms"] = norms_lines(stream, max(5, args.steps // 4), max(2, args.warmup // 4))
+        log(f"[bench] norms: {out['norms']}")
 
     # ---- C5: the UNet GEMM set as one graph
     if not args.no_unet:

@@ -1,7 +1,6 @@
 // The producers and epilogues of the reference's src/kernels.h (emanwrxsti/vela) that feed and
-// finish the GEMM path, as drop-in meow:: functions over libvgemm.so (include/vgemm.h). Only the
-// GEMM-path kernels are here (with k_gn_init, which prepares the statistics records the epilogues
-// fill); the norms themselves, attention and the rest of src/kernels.h are not part of this
+// finish the GEMM path, and the integer GroupNorm / LayerNorm around it, as drop-in meow:: functions
+// over libvgemm.so (include/vgemm.h). Attention and the rest of src/kernels.h are not part of this
 // library. Errors throw std::runtime_error.
 #pragma once
 #include <hip/hip_runtime.h>
@@ -19,6 +18,9 @@ inline void kcheck(int rc) {
     if (rc != VGEMM_OK) throw std::runtime_error(std::string(vgemm_last_error()));
 }
 }  // namespace detail
+
+typedef int64_t i64;   // src/kernels.h:8
+typedef unsigned int u32;
 
 // src/kernels.h:9: the GroupNorm statistics record (same fields and layout as VgemmGnStat)
 struct GnStat {
@@ -63,6 +65,29 @@ inline void k_epilogue_split(hipStream_t st, const int32_t* Chi, const int32_t* 
 inline void k_epilogue_geglu_q(hipStream_t st, const int32_t* Chi, const int32_t* Clo, int M, int F, int ldc, const int4* cst,
                                const int32_t* e, const int32_t* Lphi, int8_t* hi, int8_t* lo, int32_t* eo, int Kp) {
     detail::kcheck(vgemm_epilogue_geglu_q(st, Chi, Clo, M, F, ldc, reinterpret_cast<const int32_t*>(cst), e, Lphi, hi, lo, eo, Kp));
+}
+
+// ---- integer normalisations (src/kernels.h:21-24,59-63,66-67); C % 4 == 0, C <= 2560
+inline void k_gn_stats1(hipStream_t st, const int32_t* X, int B, int T, int C, int groups, GnStat* gs) {
+    detail::kcheck(vgemm_gn_stats1(st, X, B, T, C, groups, gs));
+}
+inline void k_gn_fin1(hipStream_t st, GnStat* gs, int cnt, i64 n) { detail::kcheck(vgemm_gn_fin1(st, gs, cnt, n)); }
+inline void k_gn_stats2(hipStream_t st, const int32_t* X, int B, int T, int C, int groups, i64 den, GnStat* gs) {
+    detail::kcheck(vgemm_gn_stats2(st, X, B, T, C, groups, den, gs));
+}
+inline void k_gn_apply(hipStream_t st, const int32_t* X, int B, int T, int C, int groups, const GnStat* gs, const i64* g, const i64* beta, int32_t* Y) {
+    detail::kcheck(vgemm_gn_apply(st, X, B, T, C, groups, gs, reinterpret_cast<const int64_t*>(g), reinterpret_cast<const int64_t*>(beta), Y));
+}
+inline void k_lnorm(hipStream_t st, const int32_t* X, int M, int C, const i64* g, const i64* beta, i64 den, int32_t* Y) {
+    detail::kcheck(vgemm_lnorm(st, X, M, C, reinterpret_cast<const int64_t*>(g), reinterpret_cast<const int64_t*>(beta), den, Y));
+}
+inline void k_lnorm_q(hipStream_t st, const int32_t* X, int M, int C, const int32_t* g, const int32_t* beta, i64 den, int8_t* hi, int8_t* lo,
+                      int32_t* e, int Kp) {
+    detail::kcheck(vgemm_lnorm_q(st, X, M, C, g, beta, den, hi, lo, e, Kp));
+}
+inline void k_gn_apply_row(hipStream_t st, const int32_t* X, int B, int T, int C, int groups, const GnStat* gs, const int32_t* g, const int32_t* beta,
+                           const int32_t* Lsig, int32_t* Y, uint32_t* pm, int8_t* hi, int8_t* lo, int32_t* e, int Kp) {
+    detail::kcheck(vgemm_gn_apply_row(st, X, B, T, C, groups, gs, g, beta, Lsig, Y, pm, hi, lo, e, Kp));
 }
 
 }  // namespace meow

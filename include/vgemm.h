@@ -144,6 +144,25 @@ void vgemm_set_splitk(int s);
  * changes which blocks share an L2, never a result bit. No counterpart in the reference (its tile
  * raster is CUDA's block order); a tuning and test knob like vgemm_set_splitk. */
 void vgemm_set_tile_order(int order);
+/* ---- Integer normalisations on either side of the GEMM (src/kernels.h:21-24,59-63,66-67), bit-exact
+ * with src/kernels.cu:172-305,349-420: GroupNorm of X[B, T, C] (NHWC rows, `groups` groups of C /
+ * groups channels) from VgemmGnStat records -- gathered by a GEMM epilogue (AEpi.gnstat, after
+ * vgemm_gn_init) and finalised by vgemm_gn_fin1, or by vgemm_gn_stats1 -- and LayerNorm rows.
+ * C % 4 == 0 and C <= 2560 throughout; groups <= 64 and C % groups == 0; X, Y, g and beta 16-byte
+ * aligned; int16-view planes hi/lo [rows x Kp] with Kp >= C, Kp % 4 == 0, 4-byte aligned. */
+int vgemm_gn_stats1(void* stream, const int32_t* X, int B, int T, int C, int groups, void* gs);   /* k_gn_stats1: init, sum/min/max, fin1 */
+int vgemm_gn_fin1(void* stream, void* gs, int cnt, int64_t n);                                   /* k_gn_fin1: mean, e (n = T * C / groups) */
+int vgemm_gn_stats2(void* stream, const int32_t* X, int B, int T, int C, int groups, int64_t den, void* gs);   /* k_gn_stats2: ss, fin2 (sd) */
+int vgemm_gn_apply(void* stream, const int32_t* X, int B, int T, int C, int groups, const void* gs, const int64_t* g, const int64_t* beta,
+                   int32_t* Y);                                                                    /* k_gn_apply (elementwise, 64-bit g/beta) */
+/* k_gn_apply_row: + SiLU through Lsig when not NULL; int32 Y plus pm[row] = max |y| (pm may be NULL), or
+ * the int16 view hi/lo/e when hi != NULL. pm is what a following convolution takes as ASrc.rowmax. */
+int vgemm_gn_apply_row(void* stream, const int32_t* X, int B, int T, int C, int groups, const void* gs, const int32_t* g,
+                       const int32_t* beta, const int32_t* Lsig, int32_t* Y, uint32_t* pm, int8_t* hi, int8_t* lo, int32_t* e, int Kp);
+int vgemm_lnorm(void* stream, const int32_t* X, int M, int C, const int64_t* g, const int64_t* beta, int64_t den, int32_t* Y);   /* k_lnorm */
+int vgemm_lnorm_q(void* stream, const int32_t* X, int M, int C, const int32_t* g, const int32_t* beta, int64_t den, int8_t* hi,
+                  int8_t* lo, int32_t* e, int Kp);                                                 /* k_lnorm_q: the int16 view of the row */
+
 /* Workspace bytes the int16 view (AEpi.vhi) of an Mreal x Nreal call with this epilogue needs:
  * the row maxima, one exponent byte and one 32-bit mask per (row, 32 output columns). */
 size_t vgemm_view_workspace_bytes(int Mreal, int Nreal, int epi);

@@ -75,6 +75,17 @@ _SIGS = {
     "orc_gn_tiles": (None, [P, I, I, I, I, I, I, P, P, P]),
     "orc_gn_blocks": (None, [P, I, I, I, I, P, P, P]),
     "orc_qkv_heads": (None, [P, I, I, I, I, I, I, I] + [P] * 13),
+    "orc_floor_div": (I64, [I64, I64]),
+    "orc_isqrt": (I64, [I64]),
+    "orc_gn_init": (None, [P, I]),
+    "orc_gn_stats1": (None, [P, I, I, I, I, P]),
+    "orc_gn_fin1": (None, [P, I, I64]),
+    "orc_gn_stats2": (None, [P, I, I, I, I, P]),
+    "orc_gn_fin2": (None, [P, I, I64, I64]),
+    "orc_gn_apply": (None, [P, I, I, I, I, P, P, P, P]),
+    "orc_gn_apply_row": (None, [P, I, I, I, I, P, P, P, P, P, P, P, P, P, I]),
+    "orc_lnorm": (None, [P, I, I, P, P, I64, P]),
+    "orc_lnorm_q": (None, [P, I, I, P, P, I64, P, P, P, I]),
 }
 
 _lib = None
@@ -393,3 +404,86 @@ def layer_reference(L, h, rows=None, seed_y=None):
     else:
         gemm(SRC_I16, q16=h["a"], K=h["a"].shape[1], **kw)
     return Y, rowmax
+
+
+# ---------------------------------------------------------------- integer normalisations
+
+# GnStat records (src/kernels.h:9): sum, mn, mx, mean, e, (pad), ss, sd -- 48 bytes
+GN_DTYPE = np.dtype([("sum", "<i8"), ("mn", "<i4"), ("mx", "<i4"), ("mean", "<i8"), ("e", "<i4"), ("pad", "<i4"),
+                     ("ss", "<i8"), ("sd", "<i8")])
+
+
+def floor_div(a: int, b: int) -> int:
+    return int(lib().orc_floor_div(int(a), int(b)))
+
+
+def isqrt(v: int) -> int:
+    return int(lib().orc_isqrt(int(v)))
+
+
+def gn_records(cnt: int) -> np.ndarray:
+    """cnt records as k_gn_init leaves them (src/kernels.cu:173)."""
+    gs = np.zeros(cnt, GN_DTYPE)
+    lib().orc_gn_init(a(gs), cnt)
+    return gs
+
+
+def gn_stats1(X, B, T, C, groups, gs=None):
+    """k_gn_stats1 (src/kernels.cu:745-750): init, sum/min/max, fin1."""
+    X = np.ascontiguousarray(X, np.int32)
+    gs = gn_records(B * groups) if gs is None else gs
+    lib().orc_gn_stats1(a(X), B, T, C, groups, a(gs))
+    lib().orc_gn_fin1(a(gs), B * groups, T * (C // groups))
+    return gs
+
+
+def gn_fin1(gs, n):
+    lib().orc_gn_fin1(a(gs), len(gs), int(n))
+    return gs
+
+
+def gn_stats2(X, B, T, C, groups, den, gs):
+    """k_gn_stats2 (src/kernels.cu:751-755): ss, fin2 (in place)."""
+    X = np.ascontiguousarray(X, np.int32)
+    lib().orc_gn_stats2(a(X), B, T, C, groups, a(gs))
+    lib().orc_gn_fin2(a(gs), B * groups, T * (C // groups), int(den))
+    return gs
+
+
+def gn_apply(X, B, T, C, groups, gs, g64, beta64):
+    X = np.ascontiguousarray(X, np.int32)
+    g64, beta64 = np.ascontiguousarray(g64, np.int64), np.ascontiguousarray(beta64, np.int64)
+    Y = np.zeros((B * T, C), np.int32)
+    lib().orc_gn_apply(a(X), B, T, C, groups, a(gs), a(g64), a(beta64), a(Y))
+    return Y
+
+
+def gn_apply_row(X, B, T, C, groups, gs, g, beta, Lsig=None, Kp=None):
+    """k_gn_apply_row (src/kernels.cu:287-305, 824-830): (Y, pm), or (hi, lo, e) when Kp is given."""
+    X = np.ascontiguousarray(X, np.int32)
+    g, beta = np.ascontiguousarray(g, np.int32), np.ascontiguousarray(beta, np.int32)
+    L = None if Lsig is None else np.ascontiguousarray(Lsig, np.int32)
+    M = B * T
+    if Kp is None:
+        Y = np.zeros((M, C), np.int32); pm = np.zeros(M, np.uint32)
+        lib().orc_gn_apply_row(a(X), B, T, C, groups, a(gs), a(g), a(beta), a(L), a(Y), a(pm), None, None, None, 0)
+        return Y, pm
+    hi = np.zeros((M, Kp), np.int8); lo = np.zeros((M, Kp), np.int8); e = np.zeros(M, np.int32)
+    lib().orc_gn_apply_row(a(X), B, T, C, groups, a(gs), a(g), a(beta), a(L), None, None, a(hi), a(lo), a(e), Kp)
+    return hi, lo, e
+
+
+def lnorm(X, M, C, g64, beta64, den):
+    X = np.ascontiguousarray(X, np.int32)
+    g64, beta64 = np.ascontiguousarray(g64, np.int64), np.ascontiguousarray(beta64, np.int64)
+    Y = np.zeros((M, C), np.int32)
+    lib().orc_lnorm(a(X), M, C, a(g64), a(beta64), int(den), a(Y))
+    return Y
+
+
+def lnorm_q(X, M, C, g, beta, den, Kp):
+    X = np.ascontiguousarray(X, np.int32)
+    g, beta = np.ascontiguousarray(g, np.int32), np.ascontiguousarray(beta, np.int32)
+    hi = np.zeros((M, Kp), np.int8); lo = np.zeros((M, Kp), np.int8); e = np.zeros(M, np.int32)
+    lib().orc_lnorm_q(a(X), M, C, a(g), a(beta), int(den), a(hi), a(lo), a(e), Kp)
+    return hi, lo, e

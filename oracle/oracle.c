@@ -17,6 +17,7 @@
  */
 #include "oracle.h"
 
+#include <math.h>
 #include <stdlib.h>
 #include <string.h>
 #ifdef _OPENMP
@@ -609,4 +610,196 @@ void orc_interleave2(const int8_t* wa, const int32_t* ca, const int8_t* wg, cons
         memcpy(cout + 8 * i, ca + 4 * i, 16);
         memcpy(cout + 8 * i + 4, cg + 4 * i, 16);
     }
+}
+
+/* ------------------------------------------------------------------ integer normalisations */
+
+/* src/intops.cuh:18 */
+int64_t orc_floor_div(int64_t a, int64_t b) {
+    int64_t q = a / b;
+    if ((a % b != 0) && ((a < 0) != (b < 0))) --q;
+    return q;
+}
+
+/* src/intops.cuh:51-56: floor(sqrt(v)) by a double estimate and integer corrections */
+int64_t orc_isqrt(int64_t v) {
+    if (v <= 0) return 0;
+    int64_t s = (int64_t)sqrt((double)v);
+    while (s > 0 && s * s > v) --s;
+    while ((s + 1) * (s + 1) <= v) ++s;
+    return s;
+}
+
+/* src/kernels.cu:173 */
+void orc_gn_init(OrcGnStat* gs, int cnt) {
+    for (int i = 0; i < cnt; ++i) { gs[i].sum = 0; gs[i].mn = INT32_MAX; gs[i].mx = INT32_MIN; gs[i].ss = 0; }
+}
+
+/* src/kernels.cu:175-183: sum, min and max over rows t < T and channels [g cg, (g + 1) cg) of sample b */
+void orc_gn_stats1(const int32_t* X, int B, int T, int C, int groups, OrcGnStat* gs) {
+    const int cg = C / groups;
+    for (int b = 0; b < B; ++b)
+        for (int g = 0; g < groups; ++g) {
+            OrcGnStat* s = gs + b * groups + g;
+            for (int t = 0; t < T; ++t)
+                for (int j = 0; j < cg; ++j) {
+                    const int32_t v = X[((size_t)b * T + t) * C + g * cg + j];
+                    s->sum += v;
+                    if (v < s->mn) s->mn = v;
+                    if (v > s->mx) s->mx = v;
+                }
+        }
+}
+
+/* src/kernels.cu:185-192 */
+void orc_gn_fin1(OrcGnStat* gs, int cnt, int64_t n) {
+    for (int i = 0; i < cnt; ++i) {
+        OrcGnStat* s = gs + i;
+        s->mean = orc_floor_div(s->sum + n / 2, n);
+        const int64_t a = (int64_t)s->mx - s->mean, b = s->mean - (int64_t)s->mn;
+        const int e = orc_row_exp(a > b ? a : b) - 5;
+        s->e = e > 0 ? e : 0;
+    }
+}
+
+/* src/kernels.cu:193-201: ss += dd^2 with dd the rounding shift of x - mean by e (no saturation) */
+void orc_gn_stats2(const int32_t* X, int B, int T, int C, int groups, OrcGnStat* gs) {
+    const int cg = C / groups;
+    for (int b = 0; b < B; ++b)
+        for (int g = 0; g < groups; ++g) {
+            OrcGnStat* s = gs + b * groups + g;
+            const int e = s->e;
+            for (int t = 0; t < T; ++t)
+                for (int j = 0; j < cg; ++j) {
+                    const int64_t d = (int64_t)X[((size_t)b * T + t) * C + g * cg + j] - s->mean;
+                    const int64_t dd = e ? ((d >> e) + ((d >> (e - 1)) & 1)) : d;
+                    s->ss += dd * dd;
+                }
+        }
+}
+
+/* src/kernels.cu:203-210 */
+void orc_gn_fin2(OrcGnStat* gs, int cnt, int64_t n, int64_t den) {
+    for (int i = 0; i < cnt; ++i) {
+        OrcGnStat* s = gs + i;
+        const int64_t var = orc_floor_div(s->ss, n);
+        const int sh = 32 - 2 * s->e;
+        const int64_t one = sh >= 0 ? (INT64_C(1) << sh) : 0;
+        const int64_t eps = orc_floor_div(one + den / 2, den);
+        s->sd = orc_isqrt((int64_t)((uint64_t)(var + eps) << 16));
+    }
+}
+
+/* the normalised Q16 value floor(((x - mean) 2^(25 - e) + sd) / (2 sd)) (src/kernels.cu:217,296); 0 for sd = 0 */
+static int64_t orc_gn_norm(int32_t x, const OrcGnStat* s) {
+    if (s->sd == 0) return 0;
+    const int64_t d = (int64_t)x - s->mean;
+    return orc_floor_div((int64_t)((uint64_t)d << (25 - s->e)) + s->sd, 2 * s->sd);
+}
+
+/* src/kernels.cu:211-219 */
+void orc_gn_apply(const int32_t* X, int B, int T, int C, int groups, const OrcGnStat* gs, const int64_t* g, const int64_t* beta, int32_t* Y) {
+    const int cg = C / groups;
+    for (int b = 0; b < B; ++b)
+        for (int t = 0; t < T; ++t)
+            for (int c = 0; c < C; ++c) {
+                const size_t i = ((size_t)b * T + t) * C + c;
+                const int64_t yy = orc_gn_norm(X[i], gs + b * groups + c / cg);
+                Y[i] = (int32_t)orc_sat32(orc_rshr((int64_t)((uint64_t)yy * (uint64_t)g[c]), 16) + beta[c]);
+            }
+}
+
+/* quant_row_out of one row (src/kernels.cu:317-331): e = row_exp(max |v|), q = quant16_32, pads (0, -128) */
+static void orc_row_view(const int32_t* v, int C, int8_t* h, int8_t* l, int32_t* e, int Kp) {
+    uint32_t m = 0;
+    for (int c = 0; c < C; ++c) {
+        const uint32_t a = v[c] < 0 ? (uint32_t)(-(int64_t)v[c]) : (uint32_t)v[c];
+        if (a > m) m = a;
+    }
+    const int ee = orc_row_exp(m);
+    *e = ee;
+    for (int c = 0; c < Kp; ++c) {
+        const int32_t q = c < C ? orc_quant16_32(v[c], ee) : 0;
+        h[c] = (int8_t)(q >> 8);
+        l[c] = (int8_t)((q & 255) - 128);
+    }
+}
+
+/* src/kernels.cu:287-305 */
+void orc_gn_apply_row(const int32_t* X, int B, int T, int C, int groups, const OrcGnStat* gs, const int32_t* g, const int32_t* beta,
+                      const int32_t* Lsig, int32_t* Y, uint32_t* pm, int8_t* hi, int8_t* lo, int32_t* e, int Kp) {
+    const int cg = C / groups;
+    int32_t* v = (int32_t*)malloc((size_t)C * sizeof(int32_t));
+    for (int row = 0; row < B * T; ++row) {
+        const int b = row / T;
+        uint32_t m = 0;
+        for (int c = 0; c < C; ++c) {
+            const int64_t yy = orc_gn_norm(X[(size_t)row * C + c], gs + b * groups + c / cg);
+            int64_t y = orc_sat32(orc_rshr((int64_t)((uint64_t)yy * (uint64_t)(int64_t)g[c]), 16) + beta[c]);
+            if (Lsig) y = orc_sat32(orc_rshr(y * orc_lut16i(y, Lsig), 16));
+            v[c] = (int32_t)y;
+            const uint32_t a = y < 0 ? (uint32_t)(-y) : (uint32_t)y;
+            if (a > m) m = a;
+        }
+        if (hi) {
+            orc_row_view(v, C, hi + (size_t)row * Kp, lo + (size_t)row * Kp, e + row, Kp);
+        } else {
+            memcpy(Y + (size_t)row * C, v, (size_t)C * sizeof(int32_t));
+            if (pm) pm[row] = m;
+        }
+    }
+    free(v);
+}
+
+/* the LayerNorm statistics of one row (src/kernels.cu:224-238): mean, the shift ex, sd */
+static void orc_lnorm_stats(const int32_t* x, int C, int64_t den, int64_t* mean, int* ex, int64_t* sd) {
+    int64_t sum = 0;
+    int32_t mn = INT32_MAX, mx = INT32_MIN;
+    for (int c = 0; c < C; ++c) { sum += x[c]; if (x[c] < mn) mn = x[c]; if (x[c] > mx) mx = x[c]; }
+    const int64_t n = C;
+    *mean = orc_floor_div(sum + n / 2, n);
+    const int64_t a = (int64_t)mx - *mean, b = *mean - (int64_t)mn;
+    const int e = orc_row_exp(a > b ? a : b) - 5;
+    *ex = e > 0 ? e : 0;
+    int64_t ss = 0;
+    for (int c = 0; c < C; ++c) {
+        const int64_t dd = orc_rshr((int64_t)x[c] - *mean, *ex);
+        ss += dd * dd;
+    }
+    const int64_t var = orc_floor_div(ss, n);
+    const int shb = 32 - 2 * *ex;
+    const int64_t one = shb >= 0 ? (INT64_C(1) << shb) : 0;
+    const int64_t eps = orc_floor_div(one + den / 2, den);
+    *sd = orc_isqrt((int64_t)((uint64_t)(var + eps) << 16));
+}
+
+static int64_t orc_lnorm_value(int32_t x, int64_t mean, int ex, int64_t sd, int64_t g, int64_t beta) {
+    const int64_t yy = sd ? orc_floor_div((int64_t)((uint64_t)((int64_t)x - mean) << (25 - ex)) + sd, 2 * sd) : 0;
+    return orc_sat32(orc_rshr((int64_t)((uint64_t)yy * (uint64_t)g), 16) + beta);
+}
+
+/* src/kernels.cu:221-246 */
+void orc_lnorm(const int32_t* X, int M, int C, const int64_t* g, const int64_t* beta, int64_t den, int32_t* Y) {
+    for (int row = 0; row < M; ++row) {
+        const int32_t* x = X + (size_t)row * C;
+        int64_t mean, sd;
+        int ex;
+        orc_lnorm_stats(x, C, den, &mean, &ex, &sd);
+        for (int c = 0; c < C; ++c) Y[(size_t)row * C + c] = (int32_t)orc_lnorm_value(x[c], mean, ex, sd, g[c], beta[c]);
+    }
+}
+
+/* src/kernels.cu:349-390 */
+void orc_lnorm_q(const int32_t* X, int M, int C, const int32_t* g, const int32_t* beta, int64_t den, int8_t* hi, int8_t* lo,
+                 int32_t* e, int Kp) {
+    int32_t* v = (int32_t*)malloc((size_t)C * sizeof(int32_t));
+    for (int row = 0; row < M; ++row) {
+        const int32_t* x = X + (size_t)row * C;
+        int64_t mean, sd;
+        int ex;
+        orc_lnorm_stats(x, C, den, &mean, &ex, &sd);
+        for (int c = 0; c < C; ++c) v[c] = (int32_t)orc_lnorm_value(x[c], mean, ex, sd, g[c], beta[c]);
+        orc_row_view(v, C, hi + (size_t)row * Kp, lo + (size_t)row * Kp, e + row, Kp);
+    }
+    free(v);
 }

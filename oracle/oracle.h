@@ -109,6 +109,30 @@ void orc_prep_weight(const int8_t* w, int N, int K, int conv3, const int32_t* m,
 void orc_interleave2(const int8_t* wa, const int32_t* ca, const int8_t* wg, const int32_t* cg, int N, int Kp,
                      int8_t* wout, int32_t* cout);
 
+/* ---- integer normalisations: src/kernels.cu:172-305,349-420 with src/intops.cuh:18-56.
+ * Records use the GnStat layout (src/kernels.h:9): sum, mn, mx, mean, e, ss, sd. */
+typedef struct OrcGnStat {
+    int64_t sum;
+    int32_t mn, mx;
+    int64_t mean;
+    int32_t e;
+    int64_t ss, sd;
+} OrcGnStat;
+int64_t orc_floor_div(int64_t a, int64_t b);                 /* src/intops.cuh:18 */
+int64_t orc_isqrt(int64_t v);                                /* src/intops.cuh:51-56 */
+void orc_gn_init(OrcGnStat* gs, int cnt);                    /* src/kernels.cu:173 */
+void orc_gn_stats1(const int32_t* X, int B, int T, int C, int groups, OrcGnStat* gs);  /* :175-183 sum/mn/mx (accumulates) */
+void orc_gn_fin1(OrcGnStat* gs, int cnt, int64_t n);          /* :185-192 */
+void orc_gn_stats2(const int32_t* X, int B, int T, int C, int groups, OrcGnStat* gs);  /* :193-201 ss (accumulates) */
+void orc_gn_fin2(OrcGnStat* gs, int cnt, int64_t n, int64_t den);                       /* :203-210 */
+void orc_gn_apply(const int32_t* X, int B, int T, int C, int groups, const OrcGnStat* gs, const int64_t* g, const int64_t* beta, int32_t* Y);  /* :211-219 */
+/* :287-305 (k_gn_apply_row): Y + pm, or the int16 view when hi != NULL (Lsig may be NULL) */
+void orc_gn_apply_row(const int32_t* X, int B, int T, int C, int groups, const OrcGnStat* gs, const int32_t* g, const int32_t* beta,
+                      const int32_t* Lsig, int32_t* Y, uint32_t* pm, int8_t* hi, int8_t* lo, int32_t* e, int Kp);
+void orc_lnorm(const int32_t* X, int M, int C, const int64_t* g, const int64_t* beta, int64_t den, int32_t* Y);       /* :221-246 */
+void orc_lnorm_q(const int32_t* X, int M, int C, const int32_t* g, const int32_t* beta, int64_t den, int8_t* hi, int8_t* lo,
+                 int32_t* e, int Kp);                                                                                 /* :349-390 */
+
 #ifdef __cplusplus
 }
 #endif

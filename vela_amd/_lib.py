@@ -122,6 +122,13 @@ SIGNATURES = [
     ("vgemm_graph_destroy", I, [P]),
     ("vgemm_fill_u32", I, [P, P, SZ, U32]),
     ("vgemm_gn_init", I, [P, P, I]),
+    ("vgemm_gn_stats1", I, [P, P, I, I, I, I, P]),
+    ("vgemm_gn_fin1", I, [P, P, I, LL]),
+    ("vgemm_gn_stats2", I, [P, P, I, I, I, I, LL, P]),
+    ("vgemm_gn_apply", I, [P, P, I, I, I, I, P, P, P, P]),
+    ("vgemm_gn_apply_row", I, [P, P, I, I, I, I, P, P, P, P, P, P, P, P, P, I]),
+    ("vgemm_lnorm", I, [P, P, I, I, P, P, LL, P]),
+    ("vgemm_lnorm_q", I, [P, P, I, I, P, P, LL, P, P, P, I]),
     ("vgemm_model_open", I, [ctypes.c_char_p, ctypes.POINTER(P)]),
     ("vgemm_model_close", None, [P]),
     ("vgemm_model_count", I, [P]),

@@ -38,6 +38,14 @@ hipError_t launch_epilogue_split(hipStream_t st, const int32_t* Chi, const int32
 hipError_t launch_epilogue_geglu_q(hipStream_t st, const int32_t* Chi, const int32_t* Clo, int M, int F, int ldc, const int4* cst,
                                    const int32_t* e, const int32_t* L, int8_t* hi, int8_t* lo, int32_t* eo, int Kp);
 hipError_t launch_fill_u32(hipStream_t st, uint32_t* p, size_t n, uint32_t value);
+hipError_t launch_gn_fin1(hipStream_t st, GnStat* gs, int cnt, i64 n);
+hipError_t launch_gn_fin2(hipStream_t st, GnStat* gs, int cnt, i64 n, i64 den);
+hipError_t launch_gn_reduce(hipStream_t st, bool sq, const int32_t* X, int B, int T, int C, int groups, GnStat* gs);
+hipError_t launch_gn_apply(hipStream_t st, const int32_t* X, int B, int T, int C, int groups, const GnStat* gs, const i64* g, const i64* beta, int32_t* Y);
+hipError_t launch_gn_apply_row(hipStream_t st, const int32_t* X, int M, int T, int C, int groups, const GnStat* gs, const int32_t* g, const int32_t* beta,
+                               const int32_t* Lsig, int32_t* Y, uint32_t* pm, int8_t* hi, int8_t* lo, int32_t* e, int Kp);
+hipError_t launch_lnorm(hipStream_t st, bool q, const int32_t* X, int M, int C, const void* g, const void* beta, i64 den, int32_t* Y, int8_t* hi, int8_t* lo,
+                        int32_t* e, int Kp);
 hipError_t launch_gn_init(hipStream_t st, GnStat* gs, int n);
 }  // namespace vk
 
@@ -714,6 +722,86 @@ int vgemm_fill_u32(void* stream, uint32_t* p, size_t count, uint32_t value) {
 int vgemm_gn_init(void* stream, void* gs, int count) {
     if (!gs || count <= 0) return fail(VGEMM_ERR_ARG, "gn_init: bad arguments");
     return hip_status(vk::launch_gn_init(static_cast<hipStream_t>(stream), static_cast<vk::GnStat*>(gs), count), "gn_init launch");
+}
+
+// ---- integer normalisations (src/kernels.cu:172-305,349-420, 745-762,820-830)
+namespace {
+int norm_shape(const char* what, const int32_t* X, long long rows, int C) {
+    if (!X || rows <= 0 || C <= 0) return fail(VGEMM_ERR_ARG, "%s: bad arguments", what);
+    if (C % 4 || C > 2560) return fail(VGEMM_ERR_ARG, "%s: C must be a multiple of 4 and at most 2560", what);
+    if (!aligned16(X)) return fail(VGEMM_ERR_ARG, "%s: X must be 16-byte aligned", what);
+    if (rows * C > (1LL << 40)) return fail(VGEMM_ERR_UNSUPPORTED, "%s: too many elements", what);
+    return VGEMM_OK;
+}
+int gn_shape(const char* what, const int32_t* X, int B, int T, int C, int groups, const void* gs) {
+    if (B <= 0 || T <= 0 || !gs) return fail(VGEMM_ERR_ARG, "%s: bad arguments", what);
+    if (int rc = norm_shape(what, X, (long long)B * T, C)) return rc;
+    if (groups <= 0 || groups > 64 || C % groups) return fail(VGEMM_ERR_ARG, "%s: groups must divide C and be at most 64", what);
+    return VGEMM_OK;
+}
+int view_planes(const char* what, int C, const int8_t* hi, const int8_t* lo, const int32_t* e, int Kp) {
+    if (!lo || !e || Kp < C || Kp % 4 || ((uintptr_t)hi | (uintptr_t)lo) & 3) return fail(VGEMM_ERR_ARG, "%s: hi/lo/e with Kp >= C, Kp %% 4 == 0, 4-byte aligned planes", what);
+    return VGEMM_OK;
+}
+}  // namespace
+
+int vgemm_gn_stats1(void* stream, const int32_t* X, int B, int T, int C, int groups, void* gs) {
+    if (int rc = gn_shape("gn_stats1", X, B, T, C, groups, gs)) return rc;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    vk::GnStat* g = static_cast<vk::GnStat*>(gs);
+    const int cnt = B * groups;
+    if (int rc = hip_status(vk::launch_gn_init(st, g, cnt), "gn_stats1 init")) return rc;
+    if (int rc = hip_status(vk::launch_gn_reduce(st, false, X, B, T, C, groups, g), "gn_stats1 reduce")) return rc;
+    return hip_status(vk::launch_gn_fin1(st, g, cnt, (long long)T * (C / groups)), "gn_stats1 fin1");
+}
+
+int vgemm_gn_fin1(void* stream, void* gs, int cnt, int64_t n) {
+    if (!gs || cnt <= 0 || n <= 0) return fail(VGEMM_ERR_ARG, "gn_fin1: bad arguments");
+    return hip_status(vk::launch_gn_fin1(static_cast<hipStream_t>(stream), static_cast<vk::GnStat*>(gs), cnt, n), "gn_fin1 launch");
+}
+
+int vgemm_gn_stats2(void* stream, const int32_t* X, int B, int T, int C, int groups, int64_t den, void* gs) {
+    if (int rc = gn_shape("gn_stats2", X, B, T, C, groups, gs)) return rc;
+    if (den <= 0) return fail(VGEMM_ERR_ARG, "gn_stats2: den must be positive");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    vk::GnStat* g = static_cast<vk::GnStat*>(gs);
+    if (int rc = hip_status(vk::launch_gn_reduce(st, true, X, B, T, C, groups, g), "gn_stats2 reduce")) return rc;
+    return hip_status(vk::launch_gn_fin2(st, g, B * groups, (long long)T * (C / groups), den), "gn_stats2 fin2");
+}
+
+int vgemm_gn_apply(void* stream, const int32_t* X, int B, int T, int C, int groups, const void* gs, const int64_t* g, const int64_t* beta, int32_t* Y) {
+    if (int rc = gn_shape("gn_apply", X, B, T, C, groups, gs)) return rc;
+    if (!g || !beta || !Y) return fail(VGEMM_ERR_ARG, "gn_apply: bad arguments");
+    return hip_status(vk::launch_gn_apply(static_cast<hipStream_t>(stream), X, B, T, C, groups, static_cast<const vk::GnStat*>(gs), reinterpret_cast<const long long*>(g), reinterpret_cast<const long long*>(beta), Y),
+                      "gn_apply launch");
+}
+
+int vgemm_gn_apply_row(void* stream, const int32_t* X, int B, int T, int C, int groups, const void* gs, const int32_t* g, const int32_t* beta,
+                       const int32_t* Lsig, int32_t* Y, uint32_t* pm, int8_t* hi, int8_t* lo, int32_t* e, int Kp) {
+    if (int rc = gn_shape("gn_apply_row", X, B, T, C, groups, gs)) return rc;
+    if (!g || !beta || !aligned16(g) || !aligned16(beta)) return fail(VGEMM_ERR_ARG, "gn_apply_row: g/beta must be 16-byte aligned");
+    if (hi) {
+        if (int rc = view_planes("gn_apply_row", C, hi, lo, e, Kp)) return rc;
+    } else if (!Y || !aligned16(Y)) {
+        return fail(VGEMM_ERR_ARG, "gn_apply_row: Y (16-byte aligned) or hi/lo/e required");
+    }
+    return hip_status(vk::launch_gn_apply_row(static_cast<hipStream_t>(stream), X, B * T, T, C, groups, static_cast<const vk::GnStat*>(gs), g, beta, Lsig,
+                                              Y, pm, hi, lo, e, Kp),
+                      "gn_apply_row launch");
+}
+
+int vgemm_lnorm(void* stream, const int32_t* X, int M, int C, const int64_t* g, const int64_t* beta, int64_t den, int32_t* Y) {
+    if (int rc = norm_shape("lnorm", X, M, C)) return rc;
+    if (!g || !beta || !Y || !aligned16(Y) || den <= 0) return fail(VGEMM_ERR_ARG, "lnorm: bad arguments");
+    return hip_status(vk::launch_lnorm(static_cast<hipStream_t>(stream), false, X, M, C, g, beta, den, Y, nullptr, nullptr, nullptr, 0), "lnorm launch");
+}
+
+int vgemm_lnorm_q(void* stream, const int32_t* X, int M, int C, const int32_t* g, const int32_t* beta, int64_t den, int8_t* hi, int8_t* lo, int32_t* e,
+                  int Kp) {
+    if (int rc = norm_shape("lnorm_q", X, M, C)) return rc;
+    if (!g || !beta || !aligned16(g) || !aligned16(beta) || !hi || den <= 0) return fail(VGEMM_ERR_ARG, "lnorm_q: bad arguments");
+    if (int rc = view_planes("lnorm_q", C, hi, lo, e, Kp)) return rc;
+    return hip_status(vk::launch_lnorm(static_cast<hipStream_t>(stream), true, X, M, C, g, beta, den, nullptr, hi, lo, e, Kp), "lnorm_q launch");
 }
 
 const char* vgemm_last_error(void) { return g_err.c_str(); }
