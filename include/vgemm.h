@@ -126,8 +126,10 @@ int vgemm_conv_e(void* stream, const uint32_t* pm, int B, int H, int W, int stri
 int vgemm_supported(int Mp, int Np, int Kp);
 
 /* meow::g_gemm_hl_variant (src/gemm_hl.h:35, src/gemm_hl.cu:345): tile override, -1 = automatic.
- * This library's variants: 0 = 128x128 tiles, 1 = 64x128, 2 = 128x64 (rows x columns). Values outside
- * the table fall back to automatic selection. */
+ * This library's variants: 0 = 128x128 tiles, 1 = 64x128, 2 = 128x64, 3 = 128x256 (rows x columns),
+ * 4 = the row-stationary kernel (Kp <= 320), 5 = the K-split-over-waves kernel (64x64 tiles, the
+ * four waves of a block splitting K); 4 and 5 apply to the calls their kernels serve and leave the
+ * others to automatic selection, as do values outside the table. */
 void vgemm_set_variant(int v);
 int vgemm_get_variant(void);
 

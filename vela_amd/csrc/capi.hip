@@ -22,6 +22,7 @@ int conv_halo_bm(int epi, int H, int W, int C, int stride, int Ho, int Wo);
 hipError_t launch_gemm_conv16_halo(int bm, int epi, const GemmParams& p, hipStream_t st);
 hipError_t launch_gemm_raw(int variant, const GemmParams& p, int batch, hipStream_t st);
 hipError_t launch_stripe(int src, int epi, const GemmParams& p, hipStream_t st);
+hipError_t launch_kwave(int src, int epi, const GemmParams& p, hipStream_t st);
 hipError_t launch_stripe_view(int src, int epi, const GemmParams& p, hipStream_t st);
 hipError_t launch_view_fix(hipStream_t st, const uint32_t* vmax, const uint8_t* vexp, const uint32_t* vmask, int M, int F, int G, int8_t* hi,
                            int8_t* lo, int ld, int32_t* e);
@@ -109,6 +110,10 @@ int cdiv(long long a, long long b) { return int((a + b - 1) / b); }
 // whole groups of four and 16-byte aligned output, Y extent below 2^31. Blocks of 128 rows stream
 // 64-row W chunks.
 constexpr int VARIANT_STRIPE = 4;
+// Variant 5 forces the K-split-over-waves kernel (kwave_kernel.h) where it applies: int16 rows, int8
+// planes or int16 images with C % 64 == 0, epilogue PLAIN (with or without a residual) / SPLIT3 /
+// GEGLU / GELU, no GroupNorm statistics. 64 x 64 tiles, the four waves of a block splitting K.
+constexpr int VARIANT_KWAVE = 5;
 constexpr int STRIPE_BM = 128, STRIPE_CH = 64;
 constexpr int STRIPE_NCOLS = 1280;   // W rows per block, at most
 
@@ -126,6 +131,17 @@ bool stripe_applies(int src, int epi, const vk::GemmParams& p) {
     const long long yext = ((rows - 1) * p.ldy + nout) * 4;
     return yext <= MAX_EXTENT;
 }
+
+bool kwave_applies(int src, int epi, const vk::GemmParams& p) {
+    if (src != VGEMM_SRC_I16 && src != VGEMM_SRC_I8 && !(src == VGEMM_SRC_CONV16 && p.C % 64 == 0)) return false;
+    if (epi != VGEMM_EPI_PLAIN && epi != VGEMM_EPI_SPLIT3 && epi != VGEMM_EPI_GEGLU && epi != VGEMM_EPI_GELU) return false;
+    return !p.gnstat;
+}
+
+// Automatic use, for unsplit calls only: at most 640 rows and 1280 columns over Kp >= 1024 (measured:
+// the 512-row 3x3 convolutions of 1280 channels 99 -> 65 us and 191 -> 115 us without a workspace,
+// 512 x 1280 x 2560 linears 23.3 -> 21.0 us; wider or taller shapes stay on the tiled kernels).
+bool kwave_auto(const vk::GemmParams& p) { return p.Mreal <= 640 && p.Nreal <= 1280 && p.Kp >= 1024; }
 
 // Automatic use: many rows (the kernel keeps a block's rows in registers and streams all of its
 // columns, so it needs a few hundred row stripes to fill the GPU) and no per-row shifts (rows with
@@ -506,6 +522,16 @@ int hl2_impl(void* stream, const VgemmASrc* A, int Mp, int Mreal, const int8_t* 
         splits = 1;
     }
     if (splits > nK) splits = nK;
+    // few output tiles over a deep K with no split-K workspace (the reference's own AEpi has none):
+    // the K-split-over-waves kernel (forced by variant 5 where it applies)
+    if (kwave_applies(A->src, epi, p) && (g_variant == VARIANT_KWAVE || (g_variant < 0 && splits <= 1 && kwave_auto(p)))) {
+        p.mtiles = cdiv(Mreal, 64);
+        p.ntiles = cdiv(Nreal, 64);
+        p.ksplit = 1;
+        p.kper = (Kp + 63) / 64;
+        p.colmajor = pick_tile_order(p, a_operand_bytes(A, p));
+        return hip_status(vk::launch_kwave(A->src, epi, p, st), "gemm_hl kwave launch");
+    }
     auto run = [&](int e) {
         if (halo_bm) return hip_status(vk::launch_gemm_conv16_halo(halo_bm, e, p, st), "gemm_hl halo conv launch");
         return launch_src(A->src, variant, e, p, st);

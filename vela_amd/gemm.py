@@ -79,7 +79,8 @@ def gemm_hl_supported(Mp: int, Np: int, Kp: int) -> bool:
 
 
 def set_variant(v: int) -> None:
-    """Write meow::g_gemm_hl_variant (src/gemm_hl.h:35): -1 auto, 0 128x128, 1 64x128, 2 128x64."""
+    """Write meow::g_gemm_hl_variant (src/gemm_hl.h:35): -1 auto, 0 128x128, 1 64x128, 2 128x64,
+    3 128x256, 4 row-stationary, 5 K split over the waves of 64x64 tiles."""
     load().vgemm_set_variant(v)
 
 
