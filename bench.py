@@ -14,7 +14,7 @@ replay, every other config's time, and the CPU baseline: the oracle restatement 
 integer semantics (the reference has no CPU GEMM of its own), timed on this host's cores.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-unet] [--no-cpu] [--no-configs]
-       python bench.py --only {c1,c2,c2plain,c2view,c3,c4a,c4b,c4c,copy,norms,unet<i>}   (one kernel, for profiler runs)
+       python bench.py --only {c1,c2,c2plain,c2view,c3,c4a,c4b,c4c,copy,norms,attention,unet<i>}   (one kernel, for profiler runs)
        python bench.py --unet-layers   (each C5 layer timed alone)
 """
 from __future__ import annotations
@@ -34,7 +34,7 @@ PEAK_HBM_GBS = 8000.0        # MI355X HBM3E, 8 TB/s
 METRIC = "effective W8A16 TOPS & % int8 MFMA peak; UNet GEMM-set ms at batch 8"
 
 
-ONLY_NAMES = ("c1", "c2", "c2plain", "c2view", "c3", "c4a", "c4b", "c4c", "copy", "norms")
+ONLY_NAMES = ("c1", "c2", "c2plain", "c2view", "c3", "c4a", "c4b", "c4c", "copy", "norms", "attention")
 COPY_BYTES = 256 << 20       # the calibration copy of --only copy: 256 MiB read + 256 MiB written
 
 
@@ -212,6 +212,49 @@ def norms_lines(stream, steps, warmup):
     res["gn_stats1 [8,4096,320]"] = {"us": us, "gbs": round(xb / (us * 1e-6) / 1e9, 1)}
     us = t_us(lambda: vn.k_lnorm_q(x, M, C, gam, bet, 100000, hi, lo, e, C, stream=stream))
     res["lnorm_q [32768,320] -> int16 view"] = {"us": us, "gbs": round((xb + 2 * M * C + 4 * M) / (us * 1e-6) / 1e9, 1)}
+    return res
+
+
+def attention_lines(stream, steps, warmup):
+    """The exact attention of the UNet's transformer blocks (k_fused_attention), operands from
+    seeded activations through k_quant_heads / k_quant_v: self-attention at 64x64 (B 8, 5 heads,
+    4096 queries and keys) and 32x32 (10 heads, 1024), cross-attention to the 77-token context.
+    ops: three passes of Q.K^T (four int8 plane products each) and one P.V (four), 2048 int8 ops
+    per (query, key) pair -- the reference's own kernel structure (src/attn.cu:1-6)."""
+    import numpy as np
+    import torch
+
+    from vela_amd import attention as va
+
+    def t_us(fn):
+        return round(time_graphed(fn, stream, 10, max(2, steps // 10)) * 1e3, 2)
+
+    g = torch.Generator(device="cuda").manual_seed(0x41545431)
+    # an exp table of the model's shape: Q30 at z = 0, falling by a factor e every 2^16 of z
+    L = torch.from_numpy(np.round(np.exp(-np.arange(1025) * 1024.0 / 65536.0) * 2.0**30).astype(np.int64)).cuda()
+    res = {}
+    for name, B, heads, Tq, Tk in (("self 64x64", 8, 5, 4096, 4096), ("self 32x32", 8, 10, 1024, 1024), ("cross 64x64 -> 77", 8, 5, 4096, 77)):
+        C, G = 64 * heads, B * heads
+        Tqp, Tkp = (Tq + 63) // 64 * 64, (Tk + 63) // 64 * 64
+        ops = {}
+        for part, T, Tp in (("q", Tq, Tqp), ("k", Tk, Tkp)):
+            X = (torch.randn((B * T, C), generator=g, device="cuda") * 3000).to(torch.int32)
+            t = [torch.empty((G * Tp, 64), dtype=torch.int8, device="cuda") for _ in range(2)]
+            t += [torch.empty(G * Tp, dtype=torch.int32, device="cuda")] + [torch.empty(G * Tp, dtype=torch.int64, device="cuda") for _ in range(3)]
+            va.k_quant_heads(X, B, T, C, heads, Tp, *t)
+            ops[part] = t
+        Xv = (torch.randn((B * Tk, C), generator=g, device="cuda") * 30000).to(torch.int32)
+        v = [torch.empty((G * 64, Tkp), dtype=torch.int8, device="cuda") for _ in range(2)]
+        v += [torch.empty(G * 64, dtype=torch.int32, device="cuda"), torch.empty(G * 64, dtype=torch.int64, device="cuda")]
+        va.k_quant_v(Xv, B, Tk, C, heads, Tkp, *v)
+        out = torch.empty((B * Tq, C), dtype=torch.int32, device="cuda")
+        q, k = ops["q"], ops["k"]
+        run = lambda: va.k_fused_attention(q[0], q[1], q[2], q[3], q[4], k[0], k[1], k[2], k[5], v[0], v[1], v[2], v[3], B, heads, Tq, Tqp,   # noqa: E731
+                                           Tk, Tkp, False, L, C, None, None, out, stream=stream)
+        us = t_us(run)
+        nops = 2048.0 * G * Tqp * Tkp
+        res[f"{name}: B {B}, {heads} heads, Tq {Tq}, Tk {Tk}"] = {"us": us, "tops": round(nops / (us * 1e-6) / 1e12, 1),
+                                                                 "mfma_frac": round(nops / (us * 1e-6) / 5e15, 4)}
     return res
 
 
@@ -432,6 +475,11 @@ def main():
             del p
         log(f"[bench] C5 layers launched one at a time: {total:.3f} ms in total")
         return
+    if args.only == "attention":
+        res = attention_lines(stream, args.steps, args.warmup)
+        log(f"[bench] attention: {res}")
+        print(json.dumps({"workload": "exact attention, UNet transformer shapes", "lines": res}), flush=True)
+        return
     if args.only == "norms":
         res = norms_lines(stream, args.steps, args.warmup)
         log(f"[bench] norms: {res}")
@@ -538,6 +586,11 @@ def main():
     if not args.no_configs:
         out["norms"] = norms_lines(stream, max(5, args.steps // 4), max(2, args.warmup // 4))
         log(f"[bench] norms: {out['norms']}")
+
+    # ---- the exact attention of the transformer blocks
+    if not args.no_configs:
+        out["attention"] = attention_lines(stream, max(5, args.steps // 4), max(2, args.warmup // 4))
+        log(f"[bench] attention: {out['attention']}")
 
     # ---- C5: the UNet GEMM set as one graph
     if not args.no_unet:

@@ -1,7 +1,7 @@
 // The producers and epilogues of the reference's src/kernels.h (emanwrxsti/vela) that feed and
-// finish the GEMM path, and the integer GroupNorm / LayerNorm around it, as drop-in meow:: functions
-// over libvgemm.so (include/vgemm.h). Attention and the rest of src/kernels.h are not part of this
-// library. Errors throw std::runtime_error.
+// finish the GEMM path, the integer GroupNorm / LayerNorm around it, and the exact attention with its
+// operand producers, as drop-in meow:: functions over libvgemm.so (include/vgemm.h). The rest of
+// src/kernels.h is not part of this library. Errors throw std::runtime_error.
 #pragma once
 #include <hip/hip_runtime.h>
 
@@ -88,6 +88,30 @@ inline void k_lnorm_q(hipStream_t st, const int32_t* X, int M, int C, const int3
 inline void k_gn_apply_row(hipStream_t st, const int32_t* X, int B, int T, int C, int groups, const GnStat* gs, const int32_t* g, const int32_t* beta,
                            const int32_t* Lsig, int32_t* Y, uint32_t* pm, int8_t* hi, int8_t* lo, int32_t* e, int Kp) {
     detail::kcheck(vgemm_gn_apply_row(st, X, B, T, C, groups, gs, g, beta, Lsig, Y, pm, hi, lo, e, Kp));
+}
+
+// ---- attention (src/kernels.h:42-50,61,73-77)
+inline void k_quant_heads(hipStream_t st, const int32_t* X, int B, int T, int C, int heads, int Tp, int8_t* hi, int8_t* lo, int32_t* e, i64* hs,
+                          i64* ls, i64* tsum) {
+    detail::kcheck(vgemm_quant_heads(st, X, B, T, C, heads, Tp, hi, lo, e, reinterpret_cast<int64_t*>(hs), reinterpret_cast<int64_t*>(ls),
+                                     reinterpret_cast<int64_t*>(tsum)));
+}
+inline void k_quant_heads_pad(hipStream_t st, int G, int T, int Tp, int8_t* hi, int8_t* lo, int32_t* e, i64* hs, i64* ls, i64* tsum) {
+    detail::kcheck(vgemm_quant_heads_pad(st, G, T, Tp, hi, lo, e, reinterpret_cast<int64_t*>(hs), reinterpret_cast<int64_t*>(ls),
+                                         reinterpret_cast<int64_t*>(tsum)));
+}
+inline void k_quant_v(hipStream_t st, const int32_t* X, int B, int Tk, int C, int heads, int Tkp, int8_t* vt_hi, int8_t* vt_lo, int32_t* ev, i64* vsum,
+                      uint32_t* scratch) {
+    detail::kcheck(vgemm_quant_v(st, X, B, Tk, C, heads, Tkp, vt_hi, vt_lo, ev, reinterpret_cast<int64_t*>(vsum), scratch));
+}
+inline void k_fused_attention(hipStream_t st, const int8_t* qhi, const int8_t* qlo, const int32_t* eq, const i64* qhs, const i64* qls, const int8_t* khi,
+                              const int8_t* klo, const int32_t* ek, const i64* ksum, const int8_t* vthi, const int8_t* vtlo, const int32_t* ev,
+                              const i64* vsum, int B, int heads, int Tq, int Tqp, int Tk, int Tkp, bool causal, const i64* Lexp, int C, int32_t* gmx,
+                              i64* gr, int32_t* out, uint32_t* rowmax = nullptr) {
+    detail::kcheck(vgemm_fused_attention(st, qhi, qlo, eq, reinterpret_cast<const int64_t*>(qhs), reinterpret_cast<const int64_t*>(qls), khi, klo, ek,
+                                         reinterpret_cast<const int64_t*>(ksum), vthi, vtlo, ev, reinterpret_cast<const int64_t*>(vsum), B, heads, Tq,
+                                         Tqp, Tk, Tkp, causal ? 1 : 0, reinterpret_cast<const int64_t*>(Lexp), C, gmx, reinterpret_cast<int64_t*>(gr),
+                                         out, rowmax));
 }
 
 }  // namespace meow

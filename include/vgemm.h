@@ -219,6 +219,25 @@ const char* vgemm_last_error(void);
 /* Library version string. */
 const char* vgemm_version(void);
 
+/* ---- attention (src/kernels.h:42-50,61,73-77). Heads of 64 values, G = B * heads groups.
+ * Q/K operands: X[B, T, C] -> hi/lo planes [G * Tp x 64], e / hs / ls / tsum per (g, t) row; rows
+ * t >= T hold the value 0 (hi 0, lo -128, ls -8192). V: X[B, Tk, C] -> transposed planes
+ * [G * 64 x Tkp] with ev and vsum per (g, d); Tkp % 64 == 0, planes 16-byte aligned; scratch unused. */
+int vgemm_quant_heads(void* stream, const int32_t* X, int B, int T, int C, int heads, int Tp, int8_t* hi, int8_t* lo, int32_t* e, int64_t* hs,
+                      int64_t* ls, int64_t* tsum);
+int vgemm_quant_heads_pad(void* stream, int G, int T, int Tp, int8_t* hi, int8_t* lo, int32_t* e, int64_t* hs, int64_t* ls, int64_t* tsum);
+int vgemm_quant_v(void* stream, const int32_t* X, int B, int Tk, int C, int heads, int Tkp, int8_t* vthi, int8_t* vtlo, int32_t* ev, int64_t* vsum,
+                  uint32_t* scratch);
+/* meow::k_fused_attention (src/kernels.h:73-77, src/attn.cu:551-600): exact softmax attention of the
+ * quantised operands, out[(b * Tq + q) * C + h * 64 + d] (rshr(O, 15 - ev)), rowmax[b * Tq + q] =
+ * max(rowmax, |out|) when rowmax != NULL. Tqp % 64 == 0, Tkp % 64 == 0, C % 4 == 0, operands and out
+ * 16-byte aligned; Lexp holds 1025 entries in [0, 2^31). vsum, gmx and gr are accepted and unused
+ * (one launch keeps the row statistics on chip). */
+int vgemm_fused_attention(void* stream, const int8_t* qhi, const int8_t* qlo, const int32_t* eq, const int64_t* qhs, const int64_t* qls,
+                          const int8_t* khi, const int8_t* klo, const int32_t* ek, const int64_t* ksum, const int8_t* vthi, const int8_t* vtlo,
+                          const int32_t* ev, const int64_t* vsum, int B, int heads, int Tq, int Tqp, int Tk, int Tkp, int causal, const int64_t* Lexp,
+                          int C, int32_t* gmx, int64_t* gr, int32_t* out, uint32_t* rowmax);
+
 #ifdef __cplusplus
 }
 #endif

@@ -86,6 +86,10 @@ _SIGS = {
     "orc_gn_apply_row": (None, [P, I, I, I, I, P, P, P, P, P, P, P, P, P, I]),
     "orc_lnorm": (None, [P, I, I, P, P, I64, P]),
     "orc_lnorm_q": (None, [P, I, I, P, P, I64, P, P, P, I]),
+    "orc_quant_heads": (None, [P, I, I, I, I, I, P, P, P, P, P, P]),
+    "orc_quant_heads_pad": (None, [I, I, I, P, P, P, P, P, P]),
+    "orc_quant_v": (None, [P, I, I, I, I, I, P, P, P, P]),
+    "orc_attention": (None, [P, P, P, P, P, P, P, P, P, I, I, I, I, I, I, I, P, I, P, P]),
 }
 
 _lib = None
@@ -487,3 +491,49 @@ def lnorm_q(X, M, C, g, beta, den, Kp):
     hi = np.zeros((M, Kp), np.int8); lo = np.zeros((M, Kp), np.int8); e = np.zeros(M, np.int32)
     lib().orc_lnorm_q(a(X), M, C, a(g), a(beta), int(den), a(hi), a(lo), a(e), Kp)
     return hi, lo, e
+
+
+# ---------------------------------------------------------------- attention (src/kernels.cu:611-672,799-805; src/attn.cu)
+
+def quant_heads(X, B, T, C, heads, Tp):
+    """k_quant_heads: X[B*T, C] int32 -> (hi, lo [G*Tp, 64] int8, e [G*Tp], hs, ls, tsum [G*Tp] int64)."""
+    X = np.ascontiguousarray(X, np.int32)
+    G = B * heads
+    hi = np.zeros((G * Tp, 64), np.int8); lo = np.zeros((G * Tp, 64), np.int8)
+    e = np.zeros(G * Tp, np.int32); hs = np.zeros(G * Tp, np.int64); ls = np.zeros(G * Tp, np.int64); ts = np.zeros(G * Tp, np.int64)
+    lib().orc_quant_heads(a(X), B, T, C, heads, Tp, a(hi), a(lo), a(e), a(hs), a(ls), a(ts))
+    return hi, lo, e, hs, ls, ts
+
+
+def quant_heads_pad(G, T, Tp, hi, lo, e, hs, ls, ts):
+    """k_quant_heads_pad on the arrays (in place)."""
+    lib().orc_quant_heads_pad(G, T, Tp, a(hi), a(lo), a(e), a(hs), a(ls), a(ts))
+
+
+def quant_v(X, B, Tk, C, heads, Tkp):
+    """k_quant_v: X[B*Tk, C] int32 -> (vthi, vtlo [G*64, Tkp] int8, ev [G*64] int32, vsum [G*64] int64)."""
+    X = np.ascontiguousarray(X, np.int32)
+    G = B * heads
+    vth = np.zeros((G * 64, Tkp), np.int8); vtl = np.zeros((G * 64, Tkp), np.int8)
+    ev = np.zeros(G * 64, np.int32); vs = np.zeros(G * 64, np.int64)
+    lib().orc_quant_v(a(X), B, Tk, C, heads, Tkp, a(vth), a(vtl), a(ev), a(vs))
+    return vth, vtl, ev, vs
+
+
+def attention(qh, ql, eq, kh, kl, ek, vth, vtl, ev, B, heads, Tq, Tqp, Tk, Tkp, causal, Lexp, C, rowmax=None):
+    """The exact attention: out [B*Tq, C] int32 (columns h*64.. of head h), and the row maxima
+    folded into `rowmax` (uint32 [B*Tq], updated in place) when given."""
+    arrs = [np.ascontiguousarray(x, t) for x, t in ((qh, np.int8), (ql, np.int8), (eq, np.int32), (kh, np.int8), (kl, np.int8),
+                                                   (ek, np.int32), (vth, np.int8), (vtl, np.int8), (ev, np.int32))]
+    L = np.ascontiguousarray(Lexp, np.int64)
+    out = np.zeros((B * Tq, C), np.int32)
+    rm = None if rowmax is None else rowmax
+    lib().orc_attention(*[a(x) for x in arrs], B, heads, Tq, Tqp, Tk, Tkp, 1 if causal else 0, a(L), C, a(out), a(rm) if rm is not None else None)
+    return out
+
+
+def exp_table():
+    """An exp table of the reference's shape (1025 entries, Q30 at z = 0, falling by e every 2^16 of z;
+    the model's own table comes from the model file, src/engine.cu:59)."""
+    z = np.arange(1025, dtype=np.float64) * 1024.0
+    return np.round(np.exp(-z / 65536.0) * 2.0**30).astype(np.int64)

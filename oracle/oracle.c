@@ -803,3 +803,148 @@ void orc_lnorm_q(const int32_t* X, int M, int C, const int32_t* g, const int32_t
     }
     free(v);
 }
+
+/* ------------------------------------------------------------------ attention */
+
+/* src/kernels.cu:611-631 (quant_heads_k): each (g, t) row of 64 values, e = row_exp(max |x|),
+ * quant16, split16, and the sums of hi, lo and q; rows t >= T are the value 0 = (0, -128) */
+void orc_quant_heads(const int32_t* X, int B, int T, int C, int heads, int Tp, int8_t* hi, int8_t* lo, int32_t* e, int64_t* hs,
+                     int64_t* ls, int64_t* tsum) {
+    const int G = B * heads;
+    for (int g = 0; g < G; ++g)
+        for (int t = 0; t < Tp; ++t) {
+            const size_t w = (size_t)g * Tp + t;
+            if (t >= T) {
+                for (int d = 0; d < 64; ++d) { hi[w * 64 + d] = 0; lo[w * 64 + d] = -128; }
+                e[w] = 0; hs[w] = 0; ls[w] = -128 * 64; tsum[w] = 0;
+                continue;
+            }
+            const int b = g / heads, h = g % heads;
+            const int32_t* x = X + ((size_t)b * T + t) * C + h * 64;
+            uint32_t m = 0;
+            for (int d = 0; d < 64; ++d) {
+                const uint32_t a = x[d] < 0 ? (uint32_t)(-(int64_t)x[d]) : (uint32_t)x[d];
+                if (a > m) m = a;
+            }
+            const int ee = orc_row_exp(m);
+            int64_t sh = 0, sl = 0, st = 0;
+            for (int d = 0; d < 64; ++d) {
+                const int64_t q = orc_quant16(x[d], ee);
+                int8_t a, c;
+                orc_split16(q, &a, &c);
+                hi[w * 64 + d] = a; lo[w * 64 + d] = c;
+                sh += a; sl += c; st += q;
+            }
+            e[w] = ee; hs[w] = sh; ls[w] = sl; tsum[w] = st;
+        }
+}
+
+/* src/kernels.cu:799-805 */
+void orc_quant_heads_pad(int G, int T, int Tp, int8_t* hi, int8_t* lo, int32_t* e, int64_t* hs, int64_t* ls, int64_t* tsum) {
+    for (int g = 0; g < G; ++g)
+        for (int t = T; t < Tp; ++t) {
+            const size_t w = (size_t)g * Tp + t;
+            for (int d = 0; d < 64; ++d) { hi[w * 64 + d] = 0; lo[w * 64 + d] = -128; }
+            e[w] = 0; hs[w] = 0; ls[w] = -128 * 64; tsum[w] = 0;
+        }
+}
+
+/* src/kernels.cu:632-672 (quant_v_max_k, quant_v_sum_k, quant_v_write_k): per (g, d) column of the
+ * Tk rows: ev = row_exp(max |x|), vsum = sum of quant16; the transposed planes [g * 64 + d][t], the
+ * value 0 for t >= Tk */
+void orc_quant_v(const int32_t* X, int B, int Tk, int C, int heads, int Tkp, int8_t* vth, int8_t* vtl, int32_t* ev, int64_t* vsum) {
+    const int G = B * heads;
+    for (int g = 0; g < G; ++g) {
+        const int b = g / heads, h = g % heads;
+        for (int d = 0; d < 64; ++d) {
+            uint32_t m = 0;
+            for (int t = 0; t < Tk; ++t) {
+                const int32_t v = X[((size_t)b * Tk + t) * C + h * 64 + d];
+                const uint32_t a = v < 0 ? (uint32_t)(-(int64_t)v) : (uint32_t)v;
+                if (a > m) m = a;
+            }
+            const int e = orc_row_exp(m);
+            int64_t s = 0;
+            for (int t = 0; t < Tkp; ++t) {
+                const int64_t q = t < Tk ? orc_quant16(X[((size_t)b * Tk + t) * C + h * 64 + d], e) : 0;
+                int8_t a, c;
+                orc_split16(q, &a, &c);
+                vth[((size_t)g * 64 + d) * Tkp + t] = a;
+                vtl[((size_t)g * 64 + d) * Tkp + t] = c;
+                s += q;
+            }
+            ev[g * 64 + d] = e;
+            vsum[g * 64 + d] = s;
+        }
+    }
+}
+
+/* exp table lookup (src/attn.cu:85-91, src/kernels.cu:692-693): 0 for z >= 2^20, else the linear
+ * interpolation between entries z >> 10 and (z >> 10) + 1 with fraction z & 1023 (floor shift) */
+static int64_t orc_lutexp(uint32_t z, const int64_t* L) {
+    if (z >= (16u << 16)) return 0;
+    const int64_t i = z >> 10, f = z & 1023;
+    return L[i] + (((L[i + 1] - L[i]) * f) >> 10);
+}
+
+/* The exact attention of src/attn.cu:1-6 and src/kernels.cu:673-722 from the int16 values of the
+ * planes (q = 256 hi + lo + 128): per query row, S = sum_d Q_d K_d over the valid keys (k < Tk, and
+ * k <= q when causal), s = rshr(S, 19 - eq - ek), mx = max s, E = lutexp(mx - s), sumE = sum E,
+ * r = floor(2^62 / sumE) (0 for sumE <= 0), P = min(32767, (E r + 2^46) >> 47) (mod 2^64; 0 for
+ * E <= 0), O_d = sum_k P_k V_kd, out = rshr(O, 15 - ev[d]). */
+void orc_attention(const int8_t* qh, const int8_t* ql, const int32_t* eq, const int8_t* kh, const int8_t* kl, const int32_t* ek,
+                   const int8_t* vth, const int8_t* vtl, const int32_t* ev, int B, int heads, int Tq, int Tqp, int Tk, int Tkp,
+                   int causal, const int64_t* Lexp, int C, int32_t* out, uint32_t* rowmax) {
+    const int G = B * heads;
+    #pragma omp parallel for schedule(dynamic) collapse(2)
+    for (int g = 0; g < G; ++g) {
+        for (int q = 0; q < Tq; ++q) {
+            const int b = g / heads, h = g % heads;
+            int32_t* s = (int32_t*)malloc(sizeof(int32_t) * (size_t)(Tk > 0 ? Tk : 1));
+            int64_t* E = (int64_t*)malloc(sizeof(int64_t) * (size_t)(Tk > 0 ? Tk : 1));
+            const size_t rq = (size_t)g * Tqp + q;
+            int32_t mx = INT32_MIN;
+            int nk = 0;
+            for (int k = 0; k < Tk; ++k) {
+                if (causal && k > q) break;
+                const size_t rk = (size_t)g * Tkp + k;
+                int64_t S = 0;
+                for (int d = 0; d < 64; ++d) {
+                    const int64_t qv = 256 * (int64_t)qh[rq * 64 + d] + ql[rq * 64 + d] + 128;
+                    const int64_t kv = 256 * (int64_t)kh[rk * 64 + d] + kl[rk * 64 + d] + 128;
+                    S += qv * kv;
+                }
+                s[k] = (int32_t)orc_rshr(S, 19 - (int64_t)eq[rq] - ek[rk]);
+                if (s[k] > mx) mx = s[k];
+                nk = k + 1;
+            }
+            int64_t sumE = 0;
+            for (int k = 0; k < nk; ++k) { E[k] = orc_lutexp((uint32_t)mx - (uint32_t)s[k], Lexp); sumE += E[k]; }
+            const uint64_t r = sumE > 0 ? (uint64_t)orc_floor_div(INT64_C(1) << 62, sumE) : 0;
+            uint32_t am = 0;
+            for (int d = 0; d < 64; ++d) {
+                int64_t O = 0;
+                for (int k = 0; k < nk; ++k) {
+                    int64_t P = 0;
+                    if (E[k] > 0) {
+                        const uint64_t pp = ((uint64_t)E[k] * r + (UINT64_C(1) << 46)) >> 47;
+                        P = pp > 32767 ? 32767 : (int64_t)pp;
+                    }
+                    const size_t iv = ((size_t)g * 64 + d) * Tkp + k;
+                    O += P * (256 * (int64_t)vth[iv] + vtl[iv] + 128);
+                }
+                const int32_t o = (int32_t)orc_rshr(O, 15 - (int64_t)ev[g * 64 + d]);
+                out[((size_t)b * Tq + q) * C + h * 64 + d] = o;
+                const uint32_t a = o < 0 ? (uint32_t)(-(int64_t)o) : (uint32_t)o;
+                if (a > am) am = a;
+            }
+            /* rows of one (b, q) come from `heads` groups: the max is taken under a lock */
+            if (rowmax) {
+                #pragma omp critical(orc_attention_rowmax)
+                if (am > rowmax[(size_t)b * Tq + q]) rowmax[(size_t)b * Tq + q] = am;
+            }
+            free(s);
+            free(E);
+        }
+    }
+}

@@ -133,6 +133,19 @@ void orc_lnorm(const int32_t* X, int M, int C, const int64_t* g, const int64_t* 
 void orc_lnorm_q(const int32_t* X, int M, int C, const int32_t* g, const int32_t* beta, int64_t den, int8_t* hi, int8_t* lo,
                  int32_t* e, int Kp);                                                                                 /* :349-390 */
 
+/* ---- attention: the operand producers and the exact softmax attention (src/kernels.h:42-50,61,
+ * src/kernels.cu:611-672,799-805; src/attn.cu:1-6 with src/kernels.cu:673-722 as its unfused form).
+ * Heads of 64, G = B * heads groups; Q/K planes [G * Tp x 64] with e, hs, ls, tsum per row; V
+ * transposed planes [G * 64 x Tkp] with ev and vsum per (g, d). Lexp: 1025 exp-table entries. */
+void orc_quant_heads(const int32_t* X, int B, int T, int C, int heads, int Tp, int8_t* hi, int8_t* lo, int32_t* e, int64_t* hs,
+                     int64_t* ls, int64_t* tsum);                                                                   /* :611-631 */
+void orc_quant_heads_pad(int G, int T, int Tp, int8_t* hi, int8_t* lo, int32_t* e, int64_t* hs, int64_t* ls, int64_t* tsum);  /* :799-805 */
+void orc_quant_v(const int32_t* X, int B, int Tk, int C, int heads, int Tkp, int8_t* vth, int8_t* vtl, int32_t* ev, int64_t* vsum);  /* :632-672 */
+/* out[(b * Tq + q) * C + h * 64 + d] for q < Tq; rowmax[b * Tq + q] = max(rowmax, |out|) when rowmax != NULL */
+void orc_attention(const int8_t* qh, const int8_t* ql, const int32_t* eq, const int8_t* kh, const int8_t* kl, const int32_t* ek,
+                   const int8_t* vth, const int8_t* vtl, const int32_t* ev, int B, int heads, int Tq, int Tqp, int Tk, int Tkp,
+                   int causal, const int64_t* Lexp, int C, int32_t* out, uint32_t* rowmax);
+
 #ifdef __cplusplus
 }
 #endif

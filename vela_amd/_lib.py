@@ -129,6 +129,10 @@ SIGNATURES = [
     ("vgemm_gn_apply_row", I, [P, P, I, I, I, I, P, P, P, P, P, P, P, P, P, I]),
     ("vgemm_lnorm", I, [P, P, I, I, P, P, LL, P]),
     ("vgemm_lnorm_q", I, [P, P, I, I, P, P, LL, P, P, P, I]),
+    ("vgemm_quant_heads", I, [P, P, I, I, I, I, I, P, P, P, P, P, P]),
+    ("vgemm_quant_heads_pad", I, [P, I, I, I, P, P, P, P, P, P]),
+    ("vgemm_quant_v", I, [P, P, I, I, I, I, I, P, P, P, P, P]),
+    ("vgemm_fused_attention", I, [P, P, P, P, P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, I, I, P, I, P, P, P, P]),
     ("vgemm_model_open", I, [ctypes.c_char_p, ctypes.POINTER(P)]),
     ("vgemm_model_close", None, [P]),
     ("vgemm_model_count", I, [P]),

@@ -11,6 +11,7 @@
 
 #include "../../include/vgemm.h"
 #include "vk_common.h"
+#include "attn.h"
 
 namespace vk {
 hipError_t launch_gemm_i8(int variant, int epi, const GemmParams& p, int batch, hipStream_t st);
@@ -828,6 +829,54 @@ int vgemm_lnorm_q(void* stream, const int32_t* X, int M, int C, const int32_t* g
     if (!g || !beta || !aligned16(g) || !aligned16(beta) || !hi || den <= 0) return fail(VGEMM_ERR_ARG, "lnorm_q: bad arguments");
     if (int rc = view_planes("lnorm_q", C, hi, lo, e, Kp)) return rc;
     return hip_status(vk::launch_lnorm(static_cast<hipStream_t>(stream), true, X, M, C, g, beta, den, nullptr, hi, lo, e, Kp), "lnorm_q launch");
+}
+
+// ---- attention (src/kernels.h:42-50,61,73-77)
+
+int vgemm_quant_heads(void* stream, const int32_t* X, int B, int T, int C, int heads, int Tp, int8_t* hi, int8_t* lo, int32_t* e, int64_t* hs,
+                      int64_t* ls, int64_t* tsum) {
+    if (!X || !hi || !lo || !e || !hs || !ls || !tsum || B <= 0 || heads <= 0 || T <= 0 || Tp < T || C < 64 * heads)
+        return fail(VGEMM_ERR_ARG, "quant_heads: bad arguments");
+    return hip_status(vk::launch_quant_heads(static_cast<hipStream_t>(stream), X, B, T, C, heads, Tp, hi, lo, e, reinterpret_cast<long long*>(hs),
+                                             reinterpret_cast<long long*>(ls), reinterpret_cast<long long*>(tsum)),
+                      "quant_heads launch");
+}
+
+int vgemm_quant_heads_pad(void* stream, int G, int T, int Tp, int8_t* hi, int8_t* lo, int32_t* e, int64_t* hs, int64_t* ls, int64_t* tsum) {
+    if (G <= 0 || T < 0) return fail(VGEMM_ERR_ARG, "quant_heads_pad: bad arguments");
+    if (Tp <= T) return VGEMM_OK;   // nothing to pad (src/kernels.cu:807)
+    if (!hi || !lo || !e || !hs || !ls || !tsum) return fail(VGEMM_ERR_ARG, "quant_heads_pad: bad arguments");
+    return hip_status(vk::launch_quant_heads_pad(static_cast<hipStream_t>(stream), G, T, Tp, hi, lo, e, reinterpret_cast<long long*>(hs),
+                                                 reinterpret_cast<long long*>(ls), reinterpret_cast<long long*>(tsum)),
+                      "quant_heads_pad launch");
+}
+
+int vgemm_quant_v(void* stream, const int32_t* X, int B, int Tk, int C, int heads, int Tkp, int8_t* vthi, int8_t* vtlo, int32_t* ev, int64_t* vsum,
+                  uint32_t* scratch) {
+    (void)scratch;   // the column maxima stay inside one block per group here
+    if (!X || !vthi || !vtlo || !ev || !vsum || B <= 0 || heads <= 0 || Tk <= 0 || Tkp < Tk || C < 64 * heads)
+        return fail(VGEMM_ERR_ARG, "quant_v: bad arguments");
+    if (Tkp % 64 || !aligned16(vthi) || !aligned16(vtlo)) return fail(VGEMM_ERR_ARG, "quant_v: Tkp % 64 and 16-byte aligned planes required");
+    return hip_status(vk::launch_quant_v(static_cast<hipStream_t>(stream), X, B, Tk, C, heads, Tkp, vthi, vtlo, ev, reinterpret_cast<long long*>(vsum)),
+                      "quant_v launch");
+}
+
+int vgemm_fused_attention(void* stream, const int8_t* qhi, const int8_t* qlo, const int32_t* eq, const int64_t* qhs, const int64_t* qls,
+                          const int8_t* khi, const int8_t* klo, const int32_t* ek, const int64_t* ksum, const int8_t* vthi, const int8_t* vtlo,
+                          const int32_t* ev, const int64_t* vsum, int B, int heads, int Tq, int Tqp, int Tk, int Tkp, int causal, const int64_t* Lexp,
+                          int C, int32_t* gmx, int64_t* gr, int32_t* out, uint32_t* rowmax) {
+    (void)vsum; (void)gmx; (void)gr;   // one launch: the row statistics never leave the kernel
+    if (Tqp % 64 || Tkp % 64) return fail(VGEMM_ERR_ARG, "fused attention: Tqp/Tkp alignment");   // src/attn.cu:554
+    if (!qhi || !qlo || !eq || !qhs || !qls || !khi || !klo || !ek || !ksum || !vthi || !vtlo || !ev || !Lexp || !out || B <= 0 || heads <= 0 ||
+        Tq <= 0 || Tq > Tqp || Tk <= 0 || Tk > Tkp || C < 64 * heads || C % 4)
+        return fail(VGEMM_ERR_ARG, "fused attention: bad arguments");
+    if (!aligned16(qhi) || !aligned16(qlo) || !aligned16(khi) || !aligned16(klo) || !aligned16(vthi) || !aligned16(vtlo) || !aligned16(out))
+        return fail(VGEMM_ERR_ARG, "fused attention: operands must be 16-byte aligned");
+    if ((long long)B * heads > 65535) return fail(VGEMM_ERR_UNSUPPORTED, "fused attention: at most 65535 groups");
+    const vk::AttnArgs a{qhi, qlo, eq, reinterpret_cast<const long long*>(qhs), reinterpret_cast<const long long*>(qls), khi, klo, ek,
+                         reinterpret_cast<const long long*>(ksum), vthi, vtlo, ev, heads, Tq, Tqp, Tk, Tkp, causal ? 1 : 0,
+                         reinterpret_cast<const long long*>(Lexp), C, out, rowmax};
+    return hip_status(vk::launch_attention(static_cast<hipStream_t>(stream), a, B * heads), "fused attention launch");
 }
 
 const char* vgemm_last_error(void) { return g_err.c_str(); }
