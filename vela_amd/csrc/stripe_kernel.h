@@ -112,8 +112,22 @@ __global__ void __launch_bounds__(256, 2) stripe_kernel(const GemmParams p) {
         sh.umax = 0;
     }
 
+    // ---- the block's column constants (cst[n] for thread column j = tid + 256 q), loaded first so that
+    // their latency passes under the row loads below rather than in the block set-up
+    const int ncols = (ce - cb) * CH;
+    v4i craw[S::CPT];
+    {
+        const __amdgpu_buffer_rsrc_t rC = make_rsrc(p.cst, unsigned(p.Nreal) * 16u);
+#pragma unroll
+        for (int q = 0; q < S::CPT; ++q) {
+            const int j = tid + 256 * q;
+            const int n = cb * CH + (j / CH) * CH + wrow_of_lds<EPI, CH>(j % CH);
+            craw[q] = bload16(rC, j < ncols && n < p.Nreal ? unsigned(n) * 16u : OOB);
+        }
+    }
+
     // ---- the wave's activation rows (A operand: lane row lc, K bytes [32t + 16lh, +16) of substep t):
-    // loads first, so that they are older than every DMA below
+    // loads before every DMA below, so that they are older
     v4i hf[NKS], lf[NKS];
     {
         const __amdgpu_buffer_rsrc_t rA0 = make_rsrc(p.a0, p.a0_bytes);
@@ -216,7 +230,6 @@ __global__ void __launch_bounds__(256, 2) stripe_kernel(const GemmParams p) {
                 lv[q] = v;
             }
         }
-        const int ncols = (ce - cb) * CH;
         int4 cc[S::CPT];
         int smn = INT_MAX, smx = INT_MIN, bad = 0, bmx = 0, wbad = 0;
         double um = 0.0;
@@ -227,7 +240,7 @@ __global__ void __launch_bounds__(256, 2) stripe_kernel(const GemmParams p) {
             if (j < ncols) {
                 const int n = cb * CH + (j / CH) * CH + wrow_of_lds<EPI, CH>(j % CH);
                 if (n < p.Nreal) {
-                    const int4 c = p.cst[n];
+                    const int4 c = make_int4(craw[q][0], craw[q][1], craw[q][2], craw[q][3]);
                     cc[q] = c;
                     const i64 mag = (c.x < 0 ? -i64(c.x) : i64(c.x)) * i64(p.Kp);
                     if (mag >= (1LL << 30) || c.y < -1000 || c.y > 1000) bad = 1;
