@@ -31,6 +31,10 @@
 // instructions and one LDS read, repeated. The int64 form and residual calls keep the plain loop:
 // a chunk's MFMAs, then its epilogue.
 //
+// Set-up order: the column constants, the GELU table DMA and chunk cb's W DMA are issued before the
+// activation rows, a fixed number of loads per lane, so that the set-up (table expansion, bounds
+// checks, column table) waits for its own data and runs while the rows are in flight.
+//
 // Memory ordering: the W DMA of chunk c + 1 is issued right after the barrier of chunk c, and the
 // only vector-memory instructions after it in chunk c are that chunk's output stores, a fixed
 // number per lane (every lane stores unconditionally; rows and columns outside the output go to
@@ -101,7 +105,6 @@ __global__ void __launch_bounds__(256, 2) stripe_kernel(const GemmParams p) {
     const int m0 = ti.mt * BM;
     const int nch = (p.Nreal + CH - 1) / CH;
     const int cb = ti.nt * p.kper, ce = min(nch, cb + p.kper);   // this block's chunks
-    const int nk32 = (p.Kp + 31) >> 5;   // K substeps with data
     const int rbase = m0 + wave * 32;
     const int nlim = GEGLU ? (p.Nreal >> 1) : p.Nreal;
     if (cb >= ce) return;   // (the host sizes the grid so that every block has a chunk)
@@ -125,45 +128,12 @@ __global__ void __launch_bounds__(256, 2) stripe_kernel(const GemmParams p) {
             craw[q] = bload16(rC, j < ncols && n < p.Nreal ? unsigned(n) * 16u : OOB);
         }
     }
-
-    // ---- the wave's activation rows (A operand: lane row lc, K bytes [32t + 16lh, +16) of substep t):
-    // loads before every DMA below, so that they are older
-    v4i hf[NKS], lf[NKS];
+    // and the row shift of row m0 + tid (0 without per-row shifts: a null buffer reads zeros)
+    int erv;
     {
-        const __amdgpu_buffer_rsrc_t rA0 = make_rsrc(p.a0, p.a0_bytes);
-        const __amdgpu_buffer_rsrc_t rA1 = make_rsrc(SRC == SRC_I8 ? p.a1 : p.a0, SRC == SRC_I8 ? p.a1_bytes : p.a0_bytes);
-        const int r = rbase + lc;
-        const bool rok = r < p.Mreal;
-        v4i raw[NKS][SRC == SRC_I16 ? 2 : 1];
-#pragma unroll
-        for (int t = 0; t < NKS; ++t) {
-            const int k0 = t * 32 + 16 * lh;
-            if (t < nk32) {
-                if constexpr (SRC == SRC_I16) {
-                    // 16 int16 values = two 16-byte pieces; K % 8 == 0, so each piece is all in or all out
-                    const unsigned off = (unsigned(r) * unsigned(p.lda) + unsigned(k0)) * 2u;
-                    raw[t][0] = bload16(rA0, rok && k0 < p.K ? off : OOB);
-                    raw[t][1] = bload16(rA0, rok && k0 + 8 < p.K ? off + 16u : OOB);
-                } else {
-                    const unsigned off = unsigned(r) * unsigned(p.lda) + unsigned(k0);
-                    const bool ok = rok && k0 < p.Kp;
-                    hf[t] = bload16(rA0, ok ? off : OOB);
-                    lf[t] = bload16(rA1, ok ? off : OOB);
-                }
-            } else {
-                if constexpr (SRC == SRC_I16) raw[t][0] = raw[t][1] = v4i{0, 0, 0, 0};
-                else hf[t] = lf[t] = v4i{0, 0, 0, 0};
-            }
-        }
-        if constexpr (SRC == SRC_I16) {
-#pragma unroll
-            for (int t = 0; t < NKS; ++t) {
-                const v4i x0 = raw[t][0], x1 = raw[t][1];
-                const unsigned d[8] = {unsigned(x0[0]), unsigned(x0[1]), unsigned(x0[2]), unsigned(x0[3]),
-                                       unsigned(x1[0]), unsigned(x1[1]), unsigned(x1[2]), unsigned(x1[3])};
-                split16x16(d, hf[t], lf[t]);
-            }
-        }
+        const __amdgpu_buffer_rsrc_t rE = make_rsrc(p.e, p.e ? unsigned(p.Mreal) * 4u : 0u);
+        const bool ok = tid < BM && m0 + tid < p.Mreal;
+        erv = int(__builtin_amdgcn_raw_buffer_load_b32(rE, int(ok ? unsigned(m0 + tid) * 4u : OOB), 0, 0));
     }
 
     // ---- DMA: the GELU table (raw), then W chunk cb
@@ -207,8 +177,37 @@ __global__ void __launch_bounds__(256, 2) stripe_kernel(const GemmParams p) {
     };
     issue(cb, 0);
 
+    // ---- the wave's activation rows (A operand: lane row lc, K bytes [32t + 16lh, +16) of substep t).
+    // Issued after every DMA above and unconditionally (substeps past K read out of range, as zeros),
+    // so that exactly AL row loads follow the data the block set-up needs: the set-up then waits for
+    // that data alone and runs while the rows are still in flight.
+    constexpr int AL = 2 * NKS;
+    v4i hf[NKS], lf[NKS];
+    v4i raw[NKS][SRC == SRC_I16 ? 2 : 1];
+    {
+        const __amdgpu_buffer_rsrc_t rA0 = make_rsrc(p.a0, p.a0_bytes);
+        const __amdgpu_buffer_rsrc_t rA1 = make_rsrc(SRC == SRC_I8 ? p.a1 : p.a0, SRC == SRC_I8 ? p.a1_bytes : p.a0_bytes);
+        const int r = rbase + lc;
+        const bool rok = r < p.Mreal;
+#pragma unroll
+        for (int t = 0; t < NKS; ++t) {
+            const int k0 = t * 32 + 16 * lh;
+            if constexpr (SRC == SRC_I16) {
+                // 16 int16 values = two 16-byte pieces; K % 8 == 0, so each piece is all in or all out
+                const unsigned off = (unsigned(r) * unsigned(p.lda) + unsigned(k0)) * 2u;
+                raw[t][0] = bload16(rA0, rok && k0 < p.K ? off : OOB);
+                raw[t][1] = bload16(rA0, rok && k0 + 8 < p.K ? off + 16u : OOB);
+            } else {
+                const unsigned off = unsigned(r) * unsigned(p.lda) + unsigned(k0);
+                const bool ok = rok && k0 < p.Kp;
+                hf[t] = bload16(rA0, ok ? off : OOB);
+                lf[t] = bload16(rA1, ok ? off : OOB);
+            }
+        }
+    }
+
     // ---- block set-up: column constants of chunks [cb, ce), the expanded GELU table, flags
-    vm_wait<S::DMA_INS>();   // the table DMA (older than chunk cb's)
+    vm_wait<AL>();   // the column constants, the table and chunk cb's W (older than the row loads)
     block_barrier();
     int form;
     {
@@ -257,7 +256,7 @@ __global__ void __launch_bounds__(256, 2) stripe_kernel(const GemmParams p) {
         }
         int emn = INT_MAX, emx = INT_MIN;
         if (tid < BM) {
-            const int er = (m0 + tid < p.Mreal && p.e) ? p.e[m0 + tid] : 0;
+            const int er = erv;
             sh.erow[tid] = er;
             if (m0 + tid < p.Mreal) emn = emx = er;
         }
@@ -310,6 +309,17 @@ __global__ void __launch_bounds__(256, 2) stripe_kernel(const GemmParams p) {
             }
         }
         __syncthreads();
+    }
+
+    // ---- the rows' hi/lo split (int16 rows), once they have arrived
+    if constexpr (SRC == SRC_I16) {
+#pragma unroll
+        for (int t = 0; t < NKS; ++t) {
+            const v4i x0 = raw[t][0], x1 = raw[t][1];
+            const unsigned d[8] = {unsigned(x0[0]), unsigned(x0[1]), unsigned(x0[2]), unsigned(x0[3]),
+                                   unsigned(x1[0]), unsigned(x1[1]), unsigned(x1[2]), unsigned(x1[3])};
+            split16x16(d, hf[t], lf[t]);
+        }
     }
 
     const __amdgpu_buffer_rsrc_t rY = make_rsrc(p.Y, p.y_bytes);
