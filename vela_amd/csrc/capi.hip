@@ -153,6 +153,7 @@ bool stripe_auto(const vk::GemmParams& p) { return cdiv(p.Mreal, STRIPE_BM) >= 2
 
 // Blocks = row stripes x column ranges: as few column ranges as the table allows, raised until
 // there are two blocks per CU.
+constexpr int STRIPE_PRIO_PCT = 55;
 void stripe_grid(vk::GemmParams& p) {
     const int nch = cdiv(p.Nreal, STRIPE_CH);
     const int mt = cdiv(p.Mreal, STRIPE_BM);
@@ -163,6 +164,13 @@ void stripe_grid(vk::GemmParams& p) {
     p.ntiles = cs;
     p.kper = kper;
     p.ksplit = 1;
+    // With NCU < blocks <= 2 NCU every block is resident from the start, the first NCU one per CU;
+    // on each CU the older block keeps issue priority (oldest wave first) until it ends, and the
+    // younger then runs alone. The younger blocks (index >= NCU) raise their priority for their first
+    // STRIPE_PRIO_PCT % of chunks, so that the two blocks of a CU end closer together.
+    const int nblk = mt * cs;
+    p.young0 = nblk > NCU && nblk <= 2 * NCU ? NCU : 0;
+    p.prio_chunks = (kper * STRIPE_PRIO_PCT + 50) / 100;
 }
 
 // Tile variant and split-K, from measurements over the BASELINE and UNet shapes on MI355X:

@@ -105,6 +105,12 @@ __global__ void __launch_bounds__(256, 2) stripe_kernel(const GemmParams p) {
     const int m0 = ti.mt * BM;
     const int nch = (p.Nreal + CH - 1) / CH;
     const int cb = ti.nt * p.kper, ce = min(nch, cb + p.kper);   // this block's chunks
+    // a block dispatched second to its CU runs its first prio_chunks chunks at raised priority
+    const bool young = p.young0 && p.prio_chunks > 0 && int(blockIdx.x) >= p.young0;
+    if (young) __builtin_amdgcn_s_setprio(1);
+    auto prio_step = [&](int c) __attribute__((always_inline)) {
+        if (young && c - cb == p.prio_chunks) __builtin_amdgcn_s_setprio(0);
+    };
     const int rbase = m0 + wave * 32;
     const int nlim = GEGLU ? (p.Nreal >> 1) : p.Nreal;
     if (cb >= ce) return;   // (the host sizes the grid so that every block has a chunk)
@@ -496,6 +502,7 @@ __global__ void __launch_bounds__(256, 2) stripe_kernel(const GemmParams p) {
                 mfma_chunk(0);
                 fold();
                 for (int c = cb + 1; c < ce; ++c) {
+            prio_step(c);
                     const int stage = (c - cb) & 1;
                     // chunk c's DMA is done once at most the previous chunk body's stores are outstanding
                     if (c == cb + 1) vm_wait<0>();
@@ -542,6 +549,7 @@ __global__ void __launch_bounds__(256, 2) stripe_kernel(const GemmParams p) {
         unsigned mrun = 0;                           // running max |y| of the lane's row
         const bool lean_v = form == FORM_INT;
         for (int c = cb; c < ce; ++c) {
+            prio_step(c);
             const int stage = (c - cb) & 1;
             // chunk c's DMA is done once at most the previous chunk's stores are outstanding (every
             // lane issues exactly VST stores per chunk: rows, columns and lanes without output store
@@ -700,6 +708,7 @@ __global__ void __launch_bounds__(256, 2) stripe_kernel(const GemmParams p) {
     } else {
     if (!pipelined) {
         for (int c = cb; c < ce; ++c) {
+            prio_step(c);
             const int stage = (c - cb) & 1;
             // chunk c's DMA is done once at most the previous chunk's stores are outstanding
             if (c > cb && lean) vm_wait<STORES>();

@@ -60,6 +60,10 @@ struct GemmParams {
     // tiling; colmajor: tile order over the XCDs (0: each XCD takes whole row stripes, every column
     // tile and K range of them; 1: each XCD takes (K range, column tile) groups, every row tile of them)
     int mtiles, ntiles, colmajor;
+    // row-stationary kernel: blocks from index young0 on (0: none) raise their wave priority for their
+    // first prio_chunks chunks (the blocks dispatched second to a CU, which otherwise yield issue
+    // slots to the older block until it ends)
+    int young0, prio_chunks;
     // strided batch (EPI_RAW)
     long long sA, sW, sC;
     // GroupNorm statistics of the output (EPI_PLAIN_GN): GnStat[sample * 32 + group], gnT rows per
