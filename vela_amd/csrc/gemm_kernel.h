@@ -1044,6 +1044,8 @@ __global__ void __launch_bounds__(T::NT, (dma_waves_per_simd<T, EPI>())) gemm_dm
 
     // the first stages load while the block prologue runs
     const int n = ke - kb;
+    PrioBands pb;
+    pb.init(n, p.prio_bands);
 #pragma unroll
     for (int s = 0; s < NST - 1; ++s)
         if (s < n) issue(kb + s, s);
@@ -1107,6 +1109,7 @@ __global__ void __launch_bounds__(T::NT, (dma_waves_per_simd<T, EPI>())) gemm_dm
         for (int u = 0; u < NST; ++u) {
             const int s = s0 + u;
             if (s < n) {
+                pb.step(s);
                 // this stage's DMA done (the later stages' may still be in flight), then publish it
                 if (NST >= 4 && s + 2 < n) vm_wait<(NST >= 4 ? 2 : 0) * D::PER_STAGE>();
                 else if (NST >= 3 && s + 1 < n) vm_wait<D::PER_STAGE>();

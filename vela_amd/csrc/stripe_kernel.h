@@ -106,10 +106,13 @@ __global__ void __launch_bounds__(256, 2) stripe_kernel(const GemmParams p) {
     const int nch = (p.Nreal + CH - 1) / CH;
     const int cb = ti.nt * p.kper, ce = min(nch, cb + p.kper);   // this block's chunks
     // a block dispatched second to its CU runs its first prio_chunks chunks at raised priority
-    const bool young = p.young0 && p.prio_chunks > 0 && int(blockIdx.x) >= p.young0;
+    const bool young = !p.prio_bands && p.young0 && p.prio_chunks > 0 && int(blockIdx.x) >= p.young0;
     if (young) __builtin_amdgcn_s_setprio(1);
+    PrioBands pb;
+    pb.init(ce - cb, p.prio_bands);
     auto prio_step = [&](int c) __attribute__((always_inline)) {
         if (young && c - cb == p.prio_chunks) __builtin_amdgcn_s_setprio(0);
+        pb.step(c - cb);
     };
     const int rbase = m0 + wave * 32;
     const int nlim = GEGLU ? (p.Nreal >> 1) : p.Nreal;

@@ -64,6 +64,8 @@ struct GemmParams {
     // first prio_chunks chunks (the blocks dispatched second to a CU, which otherwise yield issue
     // slots to the older block until it ends)
     int young0, prio_chunks;
+    // wave priority by progress in prio_bands bands (0 or 1: off; tile and row-stationary kernels)
+    int prio_bands;
     // strided batch (EPI_RAW)
     long long sA, sW, sC;
     // GroupNorm statistics of the output (EPI_PLAIN_GN): GnStat[sample * 32 + group], gnT rows per
@@ -183,6 +185,37 @@ __device__ __forceinline__ void vm_wait() {
 
 // workgroup barrier that orders memory accesses in the compiler (no implicit waits)
 __device__ __forceinline__ void block_barrier() { asm volatile("s_barrier" : : : "memory"); }
+
+// Wave priority by progress. Blocks resident on one CU start together, and the sequencer issues from
+// the oldest wave first, so the block dispatched first runs ahead and the last one finishes alone.
+// With PrioBands a block's steps [0, n) fall into `bands` equal bands, band b running at priority
+// bands - 1 - b: a block that falls a band behind the others on its CU takes issue priority until it
+// has caught up, so that the blocks of a CU end close together. The priority is back to 0 in the
+// last band.
+struct PrioBands {
+    int b, next, n, bands;
+    __device__ __forceinline__ static void set(int pr) {
+        if (pr >= 3) __builtin_amdgcn_s_setprio(3);
+        else if (pr == 2) __builtin_amdgcn_s_setprio(2);
+        else if (pr == 1) __builtin_amdgcn_s_setprio(1);
+        else __builtin_amdgcn_s_setprio(0);
+    }
+    __device__ __forceinline__ void init(int n_, int bands_) {
+        n = n_;
+        bands = min(bands_, 4);
+        b = 0;
+        next = bands > 1 ? (n + bands - 1) / bands : 0x7fffffff;
+        if (bands > 1) set(bands - 1);
+    }
+    // at the start of step s (called for every s in order)
+    __device__ __forceinline__ void step(int s) {
+        if (s == next) {
+            ++b;
+            set(bands - 1 - b);
+            next = b + 1 >= bands ? 0x7fffffff : ((b + 1) * n + bands - 1) / bands;
+        }
+    }
+};
 
 // LDS byte address of a pointer into __shared__ memory (generic -> local address-space cast)
 __device__ __forceinline__ unsigned lds_addr(const void* p) {
