@@ -140,10 +140,12 @@ __device__ __forceinline__ uint32_t uabs(int v) { return v < 0 ? uint32_t(-i64(v
 // ---------------------------------------------------------------- fast exact epilogue pieces
 
 // double -> int32 with saturation (v_cvt_i32_f64 clamps out-of-range values; the argument is
-// always an integer-valued double here)
+// always an integer-valued double here). Not volatile: the result depends on the operand alone.
+// Inline asm still limits the scheduler around it, so code that overlaps MFMA latency with this
+// conversion (the attention scores) clamps and converts in C++ instead.
 __device__ __forceinline__ int cvt_sat(double x) {
     int r;
-    asm volatile("v_cvt_i32_f64 %0, %1" : "=v"(r) : "v"(x));
+    asm("v_cvt_i32_f64 %0, %1" : "=v"(r) : "v"(x));
     return r;
 }
 
