@@ -69,7 +69,9 @@ template <bool LUT>
 struct StripeShared {
     unsigned char w[2][StripeCfg::STAGE];
     int4 tab[StripeCfg::NCOLS];   // per column {m, s, C lo, C hi} of the integer form
-    int2 lut[LUT ? 2050 : 1];   // lut[i + 1] = (1024 L[i], L[i+1] - L[i]); lut[0] below, lut[2049] above the table
+    // lut[i + 1] = (1024 L[i] - d 1024 (i - 1024) mod 2^32, d = L[i+1] - L[i]); lut[0] below, lut[2049]
+    // above the table: 1024 phi(x) = lut[j].x + lut[j].y x (mod 2^32) for x in entry j's range
+    int2 lut[LUT ? 2050 : 1];
     int erow[StripeCfg::BM];    // per-row shifts of the block (int64 form)
     unsigned long long umax;
     int flag[8];                // emin, emax, smin, smax, column bound failed, table range failed, max |b|, |wsum| > 128 Kp
@@ -233,7 +235,8 @@ __global__ void __launch_bounds__(256, 2) stripe_kernel(const GemmParams p) {
                 else if (i >= 1 && i < 2049) {
                     const int a = raw[i - 1], nx = i - 1 == 2047 ? L2048 : raw[i];
                     if (a < 0 || a > 65536 || nx < 0 || nx > 65536) lbad = 1;
-                    v = make_int2(int(unsigned(a) << 10), nx - a);
+                    // the entry's offset taken at x = 0 instead of at its first x, 1024 (i - 1025)
+                    v = make_int2(int((unsigned(a) << 10) - unsigned(nx - a) * unsigned(1024 * (i - 1025))), nx - a);
                 }
                 lv[q] = v;
             }
@@ -346,10 +349,12 @@ __global__ void __launch_bounds__(256, 2) stripe_kernel(const GemmParams p) {
     const bool lut_lds = NEEDLUT && !sh.flag[5];  // the expanded table in LDS is valid (0 <= L <= 65536)
 
     // phi(x) for tables with 0 <= L <= 65536: x clamped to [-2^20 - 1, 2^20], entry (x >> 10) + 1025
+    // (1024 L[i] + d (x - 1024 (i - 1025))) >> 10 as one 24-bit multiply-add mod 2^32: the exact value
+    // lies in [0, 2^26] and |d| <= 65536, |xc| <= 2^20 + 1 fit the 24-bit operands
     auto phi = [&](int x) -> int {
         const int xc = min(max(x, -1048577), 1048576);
         const int2 t = sh.lut[(xc >> 10) + 1025];
-        return (t.x + __mul24(t.y, xc & 1023)) >> 10;
+        return int(unsigned(t.x) + unsigned(__mul24(t.y, xc))) >> 10;
     };
     // (a b + 2^15) >> 16 as a 64-bit product: the high word and the 32-bit result
     auto mulsh16 = [&](int a, int b, unsigned& hi) -> int {
@@ -505,7 +510,7 @@ __global__ void __launch_bounds__(256, 2) stripe_kernel(const GemmParams p) {
                 mfma_chunk(0);
                 fold();
                 for (int c = cb + 1; c < ce; ++c) {
-            prio_step(c);
+                    prio_step(c);
                     const int stage = (c - cb) & 1;
                     // chunk c's DMA is done once at most the previous chunk body's stores are outstanding
                     if (c == cb + 1) vm_wait<0>();
