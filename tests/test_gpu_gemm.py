@@ -264,6 +264,30 @@ def test_conv16_with_shifts(variant):
     c.check(what=f"conv16 e v{variant}")
 
 
+@pytest.mark.parametrize("variant", [-1, 1, 0])
+@pytest.mark.parametrize("geom", [(2, 6, 5, 64, 1), (1, 9, 7, 128, 2), (2, 8, 8, 192, 1)])
+def test_conv32_dma_tiles(geom, variant):
+    """SRC_CONV32 with C % 64 == 0 on the DMA tile kernel (raw int32 rows staged in LDS, quantised
+    per fragment; variants -1 and 1) and on the register-staged kernel (variant 0): images whose
+    values fit 16 bits (every row e = 0, so whole waves take the clamp-only form; +-32768 and
+    +-32767 present), then caller shifts e in [0, 17] on full-width int32 values."""
+    vg.set_variant(variant)
+    B, H, W, C, stride = geom
+    Ho, Wo = (H - 1) // stride + 1, (W - 1) // stride + 1
+    c = Case(vg.SRC_CONV32, B * Ho * Wo, 192, 9 * C, seed=41 + C, conv=geom, residual=True)
+    small = rng(42).integers(-32768, 32768, c.img.shape).astype(np.int32)
+    small.reshape(-1)[::53] = -32768
+    small.reshape(-1)[::59] = 32767
+    c.img = small
+    c.kw["img"] = small
+    c.e = np.zeros(c.M, np.int32)
+    c.check(what=f"conv32 e=0 {geom} v{variant}")
+    c2 = Case(vg.SRC_CONV32, B * Ho * Wo, 192, 9 * C, seed=43 + C, conv=geom, residual=True)
+    c2.e = rng(44).integers(0, 18, c2.M).astype(np.int32)
+    c2.e[::5] = 0
+    c2.check(what=f"conv32 e {geom} v{variant}")
+
+
 # (B, H, W, C) of stride-1 SRC_CONV16 problems that run the halo kernel (128-row tiles of whole
 # output rows)
 HALO_GEOMS = [

@@ -61,6 +61,9 @@ typedef Tile<128, 256, 4, 2> TileD3;
 __device__ __forceinline__ int swz(int row, int chunk) { return row * 64 + ((chunk ^ (((row >> 1) + (row >> 3)) & 3)) << 4); }
 // byte offset of 16-byte chunk `chunk` (0..7) of a 128-byte LDS row (raw int16 activations), same property
 __device__ __forceinline__ int swz16(int row, int chunk) { return row * 128 + ((chunk ^ ((row & 7) ^ ((row >> 3) & 1))) << 4); }
+// byte offset of 16-byte chunk `chunk` (0..15) of a 256-byte LDS row (raw int32 image values): the 16
+// rows read together by one fragment load hit 16 distinct chunk positions
+__device__ __forceinline__ int swz32(int row, int chunk) { return row * 256 + ((chunk ^ (row & 15)) << 4); }
 __device__ __forceinline__ int swz_key(int row) { return ((row >> 1) + (row >> 3)) & 3; }
 __device__ __forceinline__ int swz16_key(int row) { return (row & 7) ^ ((row >> 3) & 1); }
 
@@ -105,6 +108,16 @@ __device__ __forceinline__ void quant_pack16(const v4i* x, int e, unsigned* d) {
         const int q0 = quant16_32(x[j >> 1][(2 * j) & 3], e);
         const int q1 = quant16_32(x[j >> 1][(2 * j + 1) & 3], e);
         d[j] = __builtin_amdgcn_perm(unsigned(q1), unsigned(q0), 0x05040100u);
+    }
+}
+
+// 16 int32 values quantised with shift 0 (quant16_32(v, 0) = v clamped to +-32767), packed to int16 pairs
+__device__ __forceinline__ void clamp_pack16(const v4i* x, unsigned* d) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int a = min(max(x[j >> 1][(2 * j) & 3], -32767), 32767);
+        const int b = min(max(x[j >> 1][(2 * j + 1) & 3], -32767), 32767);
+        d[j] = __builtin_amdgcn_perm(unsigned(b), unsigned(a), 0x05040100u);
     }
 }
 
@@ -852,20 +865,27 @@ __device__ __forceinline__ TileIdx tile_index(const GemmParams& p) {
     return t;
 }
 
-// ================================================================ DMA main loop (I8, I16, CONV16, RAW)
+// ================================================================ DMA main loop (I8, I16, CONV16, CONV32, RAW)
 
+// LDS stages of the raw int32 image rows: two (48 KB per 64 x 128 block, three blocks per CU)
+// measured 116 us on the C3 shape against 153 us with three stages (two blocks per CU)
+#ifndef VK_RAW32_STAGES
+#define VK_RAW32_STAGES 2
+#endif
 template <int SRC, int EPI, class T>
 struct DmaCfg {
     static constexpr bool TWO = EPI != EPI_RAW;
     static constexpr bool FUSED = EPI != EPI_PARTIAL && EPI != EPI_RAW;
     static constexpr bool NEEDLUT = EPI == EPI_GEGLU || EPI == EPI_GELU;
     static constexpr bool RAW16 = SRC == SRC_I16 || SRC == SRC_CONV16;   // raw int16 rows in LDS
+    static constexpr bool RAW32 = SRC == SRC_CONV32;                    // raw int32 image rows in LDS
     static constexpr int W_BYTES = T::BN * 64;
-    static constexpr int A_BYTES = RAW16 ? T::BM * 128 : (TWO ? 2 : 1) * T::BM * 64;
+    static constexpr int A_BYTES = RAW32 ? T::BM * 256 : RAW16 ? T::BM * 128 : (TWO ? 2 : 1) * T::BM * 64;
     static constexpr int STAGE = W_BYTES + A_BYTES;
 #ifndef VK_DMA_STAGES
-    // LDS stages: three, or two where a GELU table must fit beside them for two blocks per CU
-    static constexpr int NST = NEEDLUT && T::BM * T::BN < 128 * 256 ? 2 : 3;
+    // LDS stages: three, or two where a GELU table must fit beside them for two blocks per CU (raw
+    // int32 rows: VK_RAW32_STAGES)
+    static constexpr int NST = RAW32 ? VK_RAW32_STAGES : NEEDLUT && T::BM * T::BN < 128 * 256 ? 2 : 3;
 #else
     static constexpr int NST = NEEDLUT && T::BM * T::BN < 128 * 256 ? 2 : VK_DMA_STAGES;
 #endif
@@ -921,7 +941,7 @@ __global__ void __launch_bounds__(T::NT, (dma_waves_per_simd<T, EPI>())) gemm_dm
 #pragma unroll
     for (int ms = 0; ms < MS; ++ms) {
         const int r = rbase + ms * 16 + (lane & 15);
-        er[ms] = (r < p.Mreal && (FUSED || SRC == SRC_CONV16)) ? row_shift<SRC>(p, r) : 0;
+        er[ms] = (r < p.Mreal && (FUSED || SRC == SRC_CONV16 || SRC == SRC_CONV32)) ? row_shift<SRC>(p, r) : 0;
     }
     TilePre pre{};
     if constexpr (FUSED) pre = load_tile_pre<EPI, SRC, BM, BN>(p, m0, n0);
@@ -952,25 +972,29 @@ __global__ void __launch_bounds__(T::NT, (dma_waves_per_simd<T, EPI>())) gemm_dm
         w_k[j] = 16 * ((lane & 3) ^ swz_key(lr));
         w_off[j] = nrow < p.Nreal ? unsigned(nrow) * unsigned(p.ldw) + unsigned(w_k[j]) : OOB;
     }
-    constexpr int A_ROWS_INS = D::RAW16 ? 8 : 16;                      // rows per DMA instruction
-    constexpr int A_INS_PLANE = D::RAW16 ? D::A_INS : D::A_INS / (TWO ? 2 : 1);
+    constexpr int A_ROWS_INS = D::RAW32 ? 4 : D::RAW16 ? 8 : 16;       // rows per DMA instruction
+    constexpr int A_INS_PLANE = D::RAW16 || D::RAW32 ? D::A_INS : D::A_INS / (TWO ? 2 : 1);
     unsigned a_off[A_INS_PLANE];
     int a_k[A_INS_PLANE], a_pix[A_INS_PLANE];
     unsigned a_mask[A_INS_PLANE];
     // SRC_CONV16 with C % 64 == 0: a 64-wide K step never straddles a 3x3 tap, so the tap and the
     // channel offset of a step are block-wide scalars and each lane only checks its tap mask
-    const bool conv_fast = SRC == SRC_CONV16 && (p.C & 63) == 0;
+    // (SRC_CONV32 runs here only with C % 64 == 0: the host sends other convolutions to the
+    // register-staged kernel)
+    const bool conv_fast = (SRC == SRC_CONV16 || SRC == SRC_CONV32) && (p.C & 63) == 0;
     const unsigned cmagic = SRC == SRC_CONV16 ? unsigned((0x100000000ull + unsigned(p.C) - 1) / unsigned(p.C)) : 0u;
 #pragma unroll
     for (int j = 0; j < A_INS_PLANE; ++j) {
-        const int row = A_ROWS_INS * (wave * A_INS_PLANE + j) + (D::RAW16 ? (lane >> 3) : (lane >> 2));
+        const int row = A_ROWS_INS * (wave * A_INS_PLANE + j) + (D::RAW32 ? (lane >> 4) : D::RAW16 ? (lane >> 3) : (lane >> 2));
         const int r = m0 + row;
         const bool rok = r < p.Mreal;
-        if constexpr (D::RAW16) a_k[j] = 8 * ((lane & 7) ^ swz16_key(row));
+        if constexpr (D::RAW32) a_k[j] = 4 * ((lane & 15) ^ (row & 15));
+        else if constexpr (D::RAW16) a_k[j] = 8 * ((lane & 7) ^ swz16_key(row));
         else a_k[j] = 16 * ((lane & 3) ^ swz_key(row));
         if constexpr (SRC == SRC_I16) {
             a_off[j] = rok ? (unsigned(r) * unsigned(p.lda) + unsigned(a_k[j])) * 2u : OOB;
-        } else if constexpr (SRC == SRC_CONV16) {
+        } else if constexpr (SRC == SRC_CONV16 || SRC == SRC_CONV32) {
+            constexpr int EB = SRC == SRC_CONV32 ? 4 : 2;   // bytes per image value
             const int HoWo = p.Ho * p.Wo;
             const int rr = rok ? r : 0;
             const int b = rr / HoWo, pp = rr - b * HoWo, oy = pp / p.Wo, ox = pp - oy * p.Wo;
@@ -984,7 +1008,7 @@ __global__ void __launch_bounds__(T::NT, (dma_waves_per_simd<T, EPI>())) gemm_dm
             a_mask[j] = mask;
             // byte offset of channel a_k of pixel (iy0, ix0); negative at the border, but only taps
             // inside the image are ever added to it
-            a_pix[j] = (((b * p.H + iy0) * p.W + ix0) * p.C + a_k[j]) * 2;
+            a_pix[j] = (((b * p.H + iy0) * p.W + ix0) * p.C + a_k[j]) * EB;
             a_off[j] = unsigned(a_pix[j]);
         } else {
             a_off[j] = rok ? unsigned(r) * unsigned(p.lda) + unsigned(a_k[j]) : OOB;
@@ -1007,6 +1031,16 @@ __global__ void __launch_bounds__(T::NT, (dma_waves_per_simd<T, EPI>())) gemm_dm
             for (int j = 0; j < A_INS_PLANE; ++j) {
                 const unsigned off = (atail && kbase + a_k[j] >= p.K) ? OOB : a_off[j];
                 dma16(rA0, off, unsigned(kbase) * 2u, sA + (wave * A_INS_PLANE + j) * 1024);
+            }
+        } else if constexpr (SRC == SRC_CONV32) {
+            // implicit 3x3 im2col of the int32 image (conv_fast shapes only)
+            const int tap = kbase / p.C, c0 = kbase - tap * p.C;
+            const int ky = (tap * 11) >> 5, kx = tap - 3 * ky;
+            const int soff = ((ky * p.W + kx) * p.C + c0) * 4;
+#pragma unroll
+            for (int j = 0; j < A_INS_PLANE; ++j) {
+                const bool ok = tap < 9 && ((a_mask[j] >> tap) & 1u);
+                dma16(rA0, ok ? unsigned(a_pix[j] + soff) : OOB, 0u, sA + (wave * A_INS_PLANE + j) * 1024);
             }
         } else if constexpr (SRC == SRC_CONV16) {
             if (conv_fast) {
@@ -1055,7 +1089,7 @@ __global__ void __launch_bounds__(T::NT, (dma_waves_per_simd<T, EPI>())) gemm_dm
     bool e_any = false;
 #pragma unroll
     for (int ms = 0; ms < MS; ++ms) e_any |= er[ms] != 0;
-    const bool wave_e0 = SRC == SRC_CONV16 ? __builtin_amdgcn_ballot_w64(e_any) == 0 : true;
+    const bool wave_e0 = SRC == SRC_CONV16 || SRC == SRC_CONV32 ? __builtin_amdgcn_ballot_w64(e_any) == 0 : true;
 
     v4i acc_h[NS][MS], acc_l[TWO ? NS : 1][TWO ? MS : 1];
 #pragma unroll
@@ -1074,7 +1108,16 @@ __global__ void __launch_bounds__(T::NT, (dma_waves_per_simd<T, EPI>())) gemm_dm
 #pragma unroll
         for (int ms = 0; ms < MS; ++ms) {
             const int row = wm * T::WTM + ms * 16 + fr;
-            if constexpr (D::RAW16) {
+            if constexpr (D::RAW32) {
+                // the lane's 16 K values (four 16-byte chunks), quantised to int16 and split
+                v4i x[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) x[q] = *reinterpret_cast<const v4i*>(sA + swz32(row, 4 * fg + q));
+                unsigned d[8];
+                if (wave_e0) clamp_pack16(x, d);
+                else quant_pack16(x, er[ms], d);
+                split16x16(d, hf[ms], lf[ms]);
+            } else if constexpr (D::RAW16) {
                 const v4i x0 = *reinterpret_cast<const v4i*>(sA + swz16(row, 2 * fg));
                 const v4i x1 = *reinterpret_cast<const v4i*>(sA + swz16(row, 2 * fg + 1));
                 unsigned d[8] = {unsigned(x0[0]), unsigned(x0[1]), unsigned(x0[2]), unsigned(x0[3]),
@@ -1465,6 +1508,9 @@ hipError_t launch_gemm_src(int variant, int epi, const GemmParams& p, int batch,
         default: return launch_gemm_epi<SRC, TileD0, true>(epi, p, batch, st);
         }
     } else {
+        // int32 images with C % 64 == 0: 64 x 128 tiles on the DMA kernel (raw int32 rows in LDS)
+        if constexpr (SRC == SRC_CONV32)
+            if (variant == 1 && (p.C & 63) == 0) return launch_gemm_epi<SRC, TileD1, true>(epi, p, batch, st);
         switch (variant) {
         case 1: return launch_gemm_epi<SRC, TileV1, false>(epi, p, batch, st);
         case 2: return launch_gemm_epi<SRC, TileV2, false>(epi, p, batch, st);
