@@ -512,6 +512,8 @@ int hl2_impl(void* stream, const VgemmASrc* A, int Mp, int Mreal, const int8_t* 
     // int32 images with C % 64 == 0 run 64 x 128 tiles on the DMA kernel, which stages the raw int32
     // rows in LDS and quantises them per fragment (C3 shape: 116 us, 218 us on the register-staged kernel)
     if (A->src == VGEMM_SRC_CONV32 && g_variant < 0 && p.C % 64 == 0) variant = 1;
+    // int32 rows likewise (K % 4 == 0)
+    if (A->src == VGEMM_SRC_X32 && g_variant < 0 && p.K % 4 == 0) variant = 1;
     if (epi == VGEMM_EPI_QKV) variant = 0;   // whole heads per wave (the reference forces its 64 x 64 tile, src/gemm_hl.cu:358)
     if (p.gnstat) {
         // statistics regions = the reference's tile; the block must hold whole regions (128 x 128

@@ -865,7 +865,7 @@ __device__ __forceinline__ TileIdx tile_index(const GemmParams& p) {
     return t;
 }
 
-// ================================================================ DMA main loop (I8, I16, CONV16, CONV32, RAW)
+// ================================================================ DMA main loop (I8, I16, X32, CONV16, CONV32, RAW)
 
 // LDS stages of the raw int32 image rows: two (48 KB per 64 x 128 block, three blocks per CU)
 // measured 116 us on the C3 shape against 153 us with three stages (two blocks per CU)
@@ -878,7 +878,7 @@ struct DmaCfg {
     static constexpr bool FUSED = EPI != EPI_PARTIAL && EPI != EPI_RAW;
     static constexpr bool NEEDLUT = EPI == EPI_GEGLU || EPI == EPI_GELU;
     static constexpr bool RAW16 = SRC == SRC_I16 || SRC == SRC_CONV16;   // raw int16 rows in LDS
-    static constexpr bool RAW32 = SRC == SRC_CONV32;                    // raw int32 image rows in LDS
+    static constexpr bool RAW32 = SRC == SRC_CONV32 || SRC == SRC_X32;  // raw int32 rows in LDS
     static constexpr int W_BYTES = T::BN * 64;
     static constexpr int A_BYTES = RAW32 ? T::BM * 256 : RAW16 ? T::BM * 128 : (TWO ? 2 : 1) * T::BM * 64;
     static constexpr int STAGE = W_BYTES + A_BYTES;
@@ -941,7 +941,7 @@ __global__ void __launch_bounds__(T::NT, (dma_waves_per_simd<T, EPI>())) gemm_dm
 #pragma unroll
     for (int ms = 0; ms < MS; ++ms) {
         const int r = rbase + ms * 16 + (lane & 15);
-        er[ms] = (r < p.Mreal && (FUSED || SRC == SRC_CONV16 || SRC == SRC_CONV32)) ? row_shift<SRC>(p, r) : 0;
+        er[ms] = (r < p.Mreal && (FUSED || D::RAW32 || SRC == SRC_CONV16)) ? row_shift<SRC>(p, r) : 0;
     }
     TilePre pre{};
     if constexpr (FUSED) pre = load_tile_pre<EPI, SRC, BM, BN>(p, m0, n0);
@@ -993,6 +993,8 @@ __global__ void __launch_bounds__(T::NT, (dma_waves_per_simd<T, EPI>())) gemm_dm
         else a_k[j] = 16 * ((lane & 3) ^ swz_key(row));
         if constexpr (SRC == SRC_I16) {
             a_off[j] = rok ? (unsigned(r) * unsigned(p.lda) + unsigned(a_k[j])) * 2u : OOB;
+        } else if constexpr (SRC == SRC_X32) {
+            a_off[j] = rok ? (unsigned(r) * unsigned(p.lda) + unsigned(a_k[j])) * 4u : OOB;
         } else if constexpr (SRC == SRC_CONV16 || SRC == SRC_CONV32) {
             constexpr int EB = SRC == SRC_CONV32 ? 4 : 2;   // bytes per image value
             const int HoWo = p.Ho * p.Wo;
@@ -1031,6 +1033,14 @@ __global__ void __launch_bounds__(T::NT, (dma_waves_per_simd<T, EPI>())) gemm_dm
             for (int j = 0; j < A_INS_PLANE; ++j) {
                 const unsigned off = (atail && kbase + a_k[j] >= p.K) ? OOB : a_off[j];
                 dma16(rA0, off, unsigned(kbase) * 2u, sA + (wave * A_INS_PLANE + j) * 1024);
+            }
+        } else if constexpr (SRC == SRC_X32) {
+            // int32 rows, K % 4 == 0 (the host's condition), so each 16-byte piece is all in or all out
+            const bool atail = kbase + 64 > p.K;
+#pragma unroll
+            for (int j = 0; j < A_INS_PLANE; ++j) {
+                const unsigned off = (atail && kbase + a_k[j] >= p.K) ? OOB : a_off[j];
+                dma16(rA0, off, unsigned(kbase) * 4u, sA + (wave * A_INS_PLANE + j) * 1024);
             }
         } else if constexpr (SRC == SRC_CONV32) {
             // implicit 3x3 im2col of the int32 image (conv_fast shapes only)
@@ -1089,7 +1099,7 @@ __global__ void __launch_bounds__(T::NT, (dma_waves_per_simd<T, EPI>())) gemm_dm
     bool e_any = false;
 #pragma unroll
     for (int ms = 0; ms < MS; ++ms) e_any |= er[ms] != 0;
-    const bool wave_e0 = SRC == SRC_CONV16 || SRC == SRC_CONV32 ? __builtin_amdgcn_ballot_w64(e_any) == 0 : true;
+    const bool wave_e0 = SRC == SRC_CONV16 || D::RAW32 ? __builtin_amdgcn_ballot_w64(e_any) == 0 : true;
 
     v4i acc_h[NS][MS], acc_l[TWO ? NS : 1][TWO ? MS : 1];
 #pragma unroll
@@ -1508,9 +1518,12 @@ hipError_t launch_gemm_src(int variant, int epi, const GemmParams& p, int batch,
         default: return launch_gemm_epi<SRC, TileD0, true>(epi, p, batch, st);
         }
     } else {
-        // int32 images with C % 64 == 0: 64 x 128 tiles on the DMA kernel (raw int32 rows in LDS)
+        // int32 images with C % 64 == 0 and int32 rows with K % 4 == 0: 64 x 128 tiles on the DMA
+        // kernel (raw int32 rows in LDS)
         if constexpr (SRC == SRC_CONV32)
             if (variant == 1 && (p.C & 63) == 0) return launch_gemm_epi<SRC, TileD1, true>(epi, p, batch, st);
+        if constexpr (SRC == SRC_X32)
+            if (variant == 1 && (p.K & 3) == 0) return launch_gemm_epi<SRC, TileD1, true>(epi, p, batch, st);
         switch (variant) {
         case 1: return launch_gemm_epi<SRC, TileV1, false>(epi, p, batch, st);
         case 2: return launch_gemm_epi<SRC, TileV2, false>(epi, p, batch, st);
