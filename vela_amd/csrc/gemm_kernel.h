@@ -1017,22 +1017,40 @@ __global__ void __launch_bounds__(T::NT, (dma_waves_per_simd<T, EPI>())) gemm_dm
         }
     }
 
+    // implicit im2col position of the next K step to issue, (tap, channel): the steps are issued in
+    // order kb, kb + 1, ..., so it advances by 64 channels per call instead of dividing each time
+    int nx_tap = 0, nx_c0 = 0;
+    if constexpr (SRC == SRC_CONV16 || SRC == SRC_CONV32) {
+        if (conv_fast) {
+            nx_tap = (kb * 64) / p.C;
+            nx_c0 = kb * 64 - nx_tap * p.C;
+        }
+    }
     auto issue = [&](int kt, int stage) {
         const unsigned sbase = lds_addr(smem) + stage * D::STAGE;
         const int kbase = kt * 64;
-        const bool wtail = kbase + 64 > p.Kp;
+        // the K step lies wholly inside K (uniform): no per-lane range test
+        if (kbase + 64 <= p.Kp) {
 #pragma unroll
-        for (int j = 0; j < D::W_INS; ++j) {
-            const unsigned off = (wtail && kbase + w_k[j] >= p.Kp) ? OOB : w_off[j];
-            dma16(rW, off, unsigned(kbase), sbase + (wave * D::W_INS + j) * 1024);
+            for (int j = 0; j < D::W_INS; ++j) dma16(rW, w_off[j], unsigned(kbase), sbase + (wave * D::W_INS + j) * 1024);
+        } else {
+#pragma unroll
+            for (int j = 0; j < D::W_INS; ++j) {
+                const unsigned off = kbase + w_k[j] >= p.Kp ? OOB : w_off[j];
+                dma16(rW, off, unsigned(kbase), sbase + (wave * D::W_INS + j) * 1024);
+            }
         }
         const unsigned sA = sbase + D::W_BYTES;
         if constexpr (SRC == SRC_I16) {
-            const bool atail = kbase + 64 > p.K;
+            if (kbase + 64 <= p.K) {
 #pragma unroll
-            for (int j = 0; j < A_INS_PLANE; ++j) {
-                const unsigned off = (atail && kbase + a_k[j] >= p.K) ? OOB : a_off[j];
-                dma16(rA0, off, unsigned(kbase) * 2u, sA + (wave * A_INS_PLANE + j) * 1024);
+                for (int j = 0; j < A_INS_PLANE; ++j) dma16(rA0, a_off[j], unsigned(kbase) * 2u, sA + (wave * A_INS_PLANE + j) * 1024);
+            } else {
+#pragma unroll
+                for (int j = 0; j < A_INS_PLANE; ++j) {
+                    const unsigned off = kbase + a_k[j] >= p.K ? OOB : a_off[j];
+                    dma16(rA0, off, unsigned(kbase) * 2u, sA + (wave * A_INS_PLANE + j) * 1024);
+                }
             }
         } else if constexpr (SRC == SRC_X32) {
             // int32 rows, K % 4 == 0 (the host's condition), so each 16-byte piece is all in or all out
@@ -1044,7 +1062,9 @@ __global__ void __launch_bounds__(T::NT, (dma_waves_per_simd<T, EPI>())) gemm_dm
             }
         } else if constexpr (SRC == SRC_CONV32) {
             // implicit 3x3 im2col of the int32 image (conv_fast shapes only)
-            const int tap = kbase / p.C, c0 = kbase - tap * p.C;
+            const int tap = nx_tap, c0 = nx_c0;
+            nx_c0 += 64;
+            if (nx_c0 >= p.C) { nx_c0 -= p.C; ++nx_tap; }
             const int ky = (tap * 11) >> 5, kx = tap - 3 * ky;
             const int soff = ((ky * p.W + kx) * p.C + c0) * 4;
 #pragma unroll
@@ -1055,7 +1075,9 @@ __global__ void __launch_bounds__(T::NT, (dma_waves_per_simd<T, EPI>())) gemm_dm
         } else if constexpr (SRC == SRC_CONV16) {
             if (conv_fast) {
                 // implicit 3x3 im2col, tap-major K: k = tap*C + c (src/gemm_hl.cu:104-114)
-                const int tap = kbase / p.C, c0 = kbase - tap * p.C;
+                const int tap = nx_tap, c0 = nx_c0;
+                nx_c0 += 64;
+                if (nx_c0 >= p.C) { nx_c0 -= p.C; ++nx_tap; }
                 const int ky = (tap * 11) >> 5, kx = tap - 3 * ky;   // tap / 3, tap % 3 for tap < 9
                 const int soff = ((ky * p.W + kx) * p.C + c0) * 2;
 #pragma unroll
