@@ -86,7 +86,9 @@ __device__ __forceinline__ void wave_order_lds() {
 
 }  // namespace
 
-// grid (Tqp / 64, G), 256 threads
+// grid (Tqp / 64, G), 256 threads. SMALL: at most two key tiles (Tkp <= 128, cross-attention): the
+// first pass keeps the rounded scores in registers and the other two passes reuse them.
+template <bool SMALL>
 __global__ void __launch_bounds__(256) attn_kernel(const AttnArgs a) {
     __shared__ LutE s_lut[1024];
     __shared__ __attribute__((aligned(16))) int8_t s_p[4][2][16 * PSTRIDE];   // per wave: P planes [query][key]
@@ -155,11 +157,34 @@ __global__ void __launch_bounds__(256) attn_kernel(const AttnArgs a) {
         return z < (1u << 20) ? v : 0.0;
     };
 
+    // the scores of tile kt: recomputed, or (SMALL) the ones pass 0 kept
+    constexpr int NKEEP = SMALL ? 2 : 1;
+    int keep[NKEEP][4][4];
+    auto tile_scores = [&](int kt, int (&sv)[4][4]) __attribute__((always_inline)) {
+        if constexpr (SMALL) {
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) sv[ks][j] = kt ? keep[NKEEP - 1][ks][j] : keep[0][ks][j];
+        } else {
+            scores(kt, sv);
+        }
+    };
+
     // ---- pass 0: the row maximum
     int mx[4] = {INT_MIN, INT_MIN, INT_MIN, INT_MIN};
     for (int kt = 0; kt < nT; ++kt) {
         int sv[4][4];
         scores(kt, sv);
+        if constexpr (SMALL) {
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    if (kt == 0) keep[0][ks][j] = sv[ks][j];
+                    else keep[NKEEP - 1][ks][j] = sv[ks][j];
+                }
+        }
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
@@ -173,7 +198,7 @@ __global__ void __launch_bounds__(256) attn_kernel(const AttnArgs a) {
     double se[4] = {0.0, 0.0, 0.0, 0.0};
     for (int kt = 0; kt < nT; ++kt) {
         int sv[4][4];
-        scores(kt, sv);
+        tile_scores(kt, sv);
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
@@ -198,7 +223,7 @@ __global__ void __launch_bounds__(256) attn_kernel(const AttnArgs a) {
     for (int kt = 0; kt < nT; ++kt) {
         const int k0 = kt * AT_K;
         int sv[4][4];
-        scores(kt, sv);
+        tile_scores(kt, sv);
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
@@ -391,7 +416,8 @@ __global__ void __launch_bounds__(256) quant_v_write_kernel(const int32_t* __res
 // ---------------------------------------------------------------- launchers
 
 hipError_t launch_attention(hipStream_t st, const AttnArgs& a, int G) {
-    hipLaunchKernelGGL(attn_kernel, dim3(unsigned(a.Tqp / AT_Q), unsigned(G)), dim3(256), 0, st, a);
+    if (a.Tkp <= 2 * AT_K) hipLaunchKernelGGL(attn_kernel<true>, dim3(unsigned(a.Tqp / AT_Q), unsigned(G)), dim3(256), 0, st, a);
+    else hipLaunchKernelGGL(attn_kernel<false>, dim3(unsigned(a.Tqp / AT_Q), unsigned(G)), dim3(256), 0, st, a);
     return hipGetLastError();
 }
 
