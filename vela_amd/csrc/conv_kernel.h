@@ -86,9 +86,10 @@ __global__ void __launch_bounds__(256, 2) conv_halo_kernel(const GemmParams p) {
     unsigned w_off[HC::W_INS];
 #pragma unroll
     for (int j = 0; j < HC::W_INS; ++j) {
-        const int lr = 16 * (wave * HC::W_INS + j) + (lane >> 2);
+        const int R = 8 * (wave * HC::W_INS + j) + (lane >> 3), lc = (lane & 7) ^ swz16_key(R);   // pswz, as gemm_dma_kernel
+        const int lr = 2 * R + (lc >> 2);
         const int nrow = n0 + (FUSED ? wrow_of_lds<EPI, BN>(lr) : lr);
-        const int wk = 16 * ((lane & 3) ^ swz_key(lr));
+        const int wk = 16 * (lc & 3);
         w_off[j] = nrow < p.Nreal ? unsigned(nrow) * unsigned(p.ldw) + unsigned(wk) : OOB;
     }
     // ---- patch lane state: instruction q of this wave covers patch pixels 8*(4q + wave) + lane/8,
@@ -172,7 +173,7 @@ __global__ void __launch_bounds__(256, 2) conv_halo_kernel(const GemmParams p) {
 #pragma unroll
         for (int ns = 0; ns < NS; ++ns) {
             const int row = (FUSED ? wsub_row<EPI, T>(0, ns) : ns * 16) + fr;
-            const v4i wf = *reinterpret_cast<const v4i*>(sW + swz(row, fg));
+            const v4i wf = *reinterpret_cast<const v4i*>(sW + pswz(row, fg));
 #pragma unroll
             for (int ms = 0; ms < MS; ++ms) {
                 acc_h[ns][ms] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf, hf[ms], acc_h[ns][ms], 0, 0, 0);

@@ -55,12 +55,19 @@ typedef Tile<128, 64, 4, 1> TileD2;
 // eight waves, 4 x 2: each A stripe feeds 256 columns (half the A traffic of 128-column tiles)
 typedef Tile<128, 256, 4, 2> TileD3;
 
-// Byte offset of 16-byte chunk `chunk` (0..3) of a 64-byte LDS row. The XOR makes the rows read
-// by one MFMA fragment load hit distinct bank groups whether the LDS serves 8 or 16 lanes of a
-// 16-byte read per cycle.
+// LDS layouts of the K-step tiles. A fragment load (ds_read_b128) has each group of 16 lanes read
+// one 16-byte chunk of 16 consecutive rows. Measured on gfx950 (a probe with SQ_LDS_BANK_CONFLICT):
+// 128-byte rows under swz16 read conflict-free, while 64-byte rows under any XOR swizzle of their
+// four chunks cost four conflict cycles per instruction (the load takes twice as long).
+//
+// Byte offset of 16-byte chunk `chunk` (0..3) of a 64-byte LDS row, XOR-swizzled (the register-staged
+// kernel, which writes its tiles from registers)
 __device__ __forceinline__ int swz(int row, int chunk) { return row * 64 + ((chunk ^ (((row >> 1) + (row >> 3)) & 3)) << 4); }
-// byte offset of 16-byte chunk `chunk` (0..7) of a 128-byte LDS row (raw int16 activations), same property
+// byte offset of 16-byte chunk `chunk` (0..7) of a 128-byte LDS row (raw int16 activations): conflict-free
 __device__ __forceinline__ int swz16(int row, int chunk) { return row * 128 + ((chunk ^ ((row & 7) ^ ((row >> 3) & 1))) << 4); }
+// 64-byte rows (W, int8 planes) stored in pairs as 128-byte rows under swz16: chunk c (0..3) of row r
+// is chunk 4 (r & 1) + c of LDS row r / 2. The DMA still reads two whole 64-byte rows per 8 lanes.
+__device__ __forceinline__ int pswz(int row, int chunk) { return swz16(row >> 1, 4 * (row & 1) + chunk); }
 // byte offset of 16-byte chunk `chunk` (0..15) of a 256-byte LDS row (raw int32 image values): the 16
 // rows read together by one fragment load hit 16 distinct chunk positions
 __device__ __forceinline__ int swz32(int row, int chunk) { return row * 256 + ((chunk ^ (row & 15)) << 4); }
@@ -967,9 +974,12 @@ __global__ void __launch_bounds__(T::NT, (dma_waves_per_simd<T, EPI>())) gemm_dm
     int w_k[D::W_INS];
 #pragma unroll
     for (int j = 0; j < D::W_INS; ++j) {
-        const int lr = 16 * (wave * D::W_INS + j) + (lane >> 2);
+        // instruction j fills 128-byte LDS rows 8 (wave * W_INS + j) + lane / 8 (pswz): lane l holds
+        // the chunk that the swizzle puts at position l % 8, of W row 2 R + (chunk >> 2)
+        const int R = 8 * (wave * D::W_INS + j) + (lane >> 3), lc = (lane & 7) ^ swz16_key(R);
+        const int lr = 2 * R + (lc >> 2);
         const int nrow = n0 + (FUSED ? wrow_of_lds<EPI, BN>(lr) : lr);
-        w_k[j] = 16 * ((lane & 3) ^ swz_key(lr));
+        w_k[j] = 16 * (lc & 3);
         w_off[j] = nrow < p.Nreal ? unsigned(nrow) * unsigned(p.ldw) + unsigned(w_k[j]) : OOB;
     }
     constexpr int A_ROWS_INS = D::RAW32 ? 4 : D::RAW16 ? 8 : 16;       // rows per DMA instruction
@@ -985,12 +995,15 @@ __global__ void __launch_bounds__(T::NT, (dma_waves_per_simd<T, EPI>())) gemm_dm
     const unsigned cmagic = SRC == SRC_CONV16 ? unsigned((0x100000000ull + unsigned(p.C) - 1) / unsigned(p.C)) : 0u;
 #pragma unroll
     for (int j = 0; j < A_INS_PLANE; ++j) {
-        const int row = A_ROWS_INS * (wave * A_INS_PLANE + j) + (D::RAW32 ? (lane >> 4) : D::RAW16 ? (lane >> 3) : (lane >> 2));
+        // int8 planes (pswz, as W): LDS row R = 8 g + lane / 8 of the plane holds rows 2 R, 2 R + 1
+        const int g = wave * A_INS_PLANE + j;
+        const int R8 = 8 * g + (lane >> 3), lc8 = (lane & 7) ^ swz16_key(R8);
+        const int row = D::RAW32 ? A_ROWS_INS * g + (lane >> 4) : D::RAW16 ? A_ROWS_INS * g + (lane >> 3) : 2 * R8 + (lc8 >> 2);
         const int r = m0 + row;
         const bool rok = r < p.Mreal;
         if constexpr (D::RAW32) a_k[j] = 4 * ((lane & 15) ^ (row & 15));
         else if constexpr (D::RAW16) a_k[j] = 8 * ((lane & 7) ^ swz16_key(row));
-        else a_k[j] = 16 * ((lane & 3) ^ swz_key(row));
+        else a_k[j] = 16 * (lc8 & 3);
         if constexpr (SRC == SRC_I16) {
             a_off[j] = rok ? (unsigned(r) * unsigned(p.lda) + unsigned(a_k[j])) * 2u : OOB;
         } else if constexpr (SRC == SRC_X32) {
@@ -1160,14 +1173,14 @@ __global__ void __launch_bounds__(T::NT, (dma_waves_per_simd<T, EPI>())) gemm_dm
                 }
                 split16x16(d, hf[ms], lf[ms]);
             } else {
-                hf[ms] = *reinterpret_cast<const v4i*>(sA + swz(row, fg));
-                if constexpr (TWO) lf[ms] = *reinterpret_cast<const v4i*>(sA + BM * 64 + swz(row, fg));
+                hf[ms] = *reinterpret_cast<const v4i*>(sA + pswz(row, fg));
+                if constexpr (TWO) lf[ms] = *reinterpret_cast<const v4i*>(sA + BM * 64 + pswz(row, fg));
             }
         }
 #pragma unroll
         for (int ns = 0; ns < NS; ++ns) {
             const int row = (FUSED ? wsub_row<EPI, T>(wn, ns) : (wn * NS + ns) * 16) + fr;
-            const v4i wf = *reinterpret_cast<const v4i*>(sW + swz(row, fg));
+            const v4i wf = *reinterpret_cast<const v4i*>(sW + pswz(row, fg));
 #pragma unroll
             for (int ms = 0; ms < MS; ++ms) {
                 acc_h[ns][ms] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf, hf[ms], acc_h[ns][ms], 0, 0, 0);
