@@ -159,16 +159,19 @@ __global__ void __launch_bounds__(256, 2) stripe_kernel(const GemmParams p) {
     }
     const int L2048 = NEEDLUT ? p.Lphi[2048] : 0;
     const v4i rW = make_rsrc_words(p.w, p.w_bytes);
-    // instruction j of this wave fills K step ks = q / 4, LDS rows 16 rg .. 16 rg + 15 (rg = q % 4) of
-    // a chunk, q = 5 wave + j; lane l reads 16 bytes of W row wrow(16 rg + l / 4) at its swizzled K
-    // position. With l4 = l / 4: wrow(16 rg + l4) = wrow(l4) + a constant of rg, and the swizzle key
-    // of row 16 rg + l4 is (key(l4) + 2 rg) mod 4, so three per-lane values cover every instruction.
+    // W rows of a K step sit in pairs in 128-byte LDS rows (pswz). Instruction j of this wave fills K
+    // step ks = q / 4, LDS rows 8 rg .. 8 rg + 7 (rg = q % 4, the W rows 16 rg .. 16 rg + 15) of a
+    // chunk, q = 5 wave + j; lane l holds the 16-byte piece that swz16 puts at position l % 8 of LDS
+    // row R = 8 rg + l / 8: piece pc = (l % 8) ^ (l / 8) ^ (rg % 2) (the swz16 key of R), which is K
+    // chunk pc % 4 of W row 16 rg + x, x = 2 (l / 8) + pc / 4. So wrow(16 rg + x) = wrow(x) + a
+    // constant of rg, and three per-lane values cover every instruction.
     constexpr int RG = CH / 16;
     static_assert(RG == 4 && S::DMA_INS * 4 == (NKS / 2) * RG, "DMA mapping");
-    const int l4 = lane >> 2;
-    const int wb = GEGLU ? 2 * l4 : l4;                                   // wrow(l4)
-    const int wk0 = 16 * ((lane & 3) ^ swz_key(l4));                      // K offset, rg even
-    const int wk1 = 16 * ((lane & 3) ^ ((swz_key(l4) + 2) & 3));          // K offset, rg odd
+    const int pce = (lane & 7) ^ (lane >> 3);                             // piece, rg even
+    const int lx = 2 * (lane >> 3) + (pce >> 2);
+    const int wb = GEGLU ? 2 * lx : lx;                                   // wrow(x)
+    const int wk0 = 16 * (pce & 3);                                       // K offset, rg even
+    const int wk1 = 16 * ((pce ^ 1) & 3);                                 // K offset, rg odd
     const unsigned wlane = unsigned(wb) * unsigned(p.ldw);
     auto issue = [&](int c, int stage) {
         const int n0 = c * CH;
@@ -392,7 +395,7 @@ __global__ void __launch_bounds__(256, 2) stripe_kernel(const GemmParams p) {
             auto mfma_step = [&](const unsigned char* sW, int t) __attribute__((always_inline)) {
 #pragma unroll
                 for (int u = 0; u < S::NSUB; ++u) {
-                    const v4i wf = *reinterpret_cast<const v4i*>(sW + (t >> 1) * S::KSTEP + swz(32 * u + lc, 2 * (t & 1) + lh));
+                    const v4i wf = *reinterpret_cast<const v4i*>(sW + (t >> 1) * S::KSTEP + pswz(32 * u + lc, 2 * (t & 1) + lh));
                     acc_h[u] = __builtin_amdgcn_mfma_i32_32x32x32_i8(hf[t], wf, t ? acc_h[u] : vzero, 0, 0, 0);
                     acc_l[u] = __builtin_amdgcn_mfma_i32_32x32x32_i8(lf[t], wf, t ? acc_l[u] : vzero, 0, 0, 0);
                 }
@@ -464,7 +467,7 @@ __global__ void __launch_bounds__(256, 2) stripe_kernel(const GemmParams p) {
             constexpr int VPM = GEGLU ? 10 : (EPI == EPI_GELU ? 7 : 4);
             constexpr int PFB = 2;
             auto wfrag = [&](const unsigned char* sW, int t, int u) __attribute__((always_inline)) {
-                return *reinterpret_cast<const v4i*>(sW + (t >> 1) * S::KSTEP + swz(32 * u + lc, 2 * (t & 1) + lh));
+                return *reinterpret_cast<const v4i*>(sW + (t >> 1) * S::KSTEP + pswz(32 * u + lc, 2 * (t & 1) + lh));
             };
             auto body = [&](int stage, int tbp, int ocp, auto rmax, auto full) __attribute__((always_inline)) {
                 const unsigned char* sW = sh.w[stage];
@@ -574,7 +577,7 @@ __global__ void __launch_bounds__(256, 2) stripe_kernel(const GemmParams p) {
                 for (int i = 0; i < 16; ++i) { acc_h[u][i] = 0; acc_l[u][i] = 0; }
             const unsigned char* sW = sh.w[stage];
             auto wfrag = [&](int t, int u) -> v4i {
-                return *reinterpret_cast<const v4i*>(sW + (t >> 1) * S::KSTEP + swz(32 * u + lc, 2 * (t & 1) + lh));
+                return *reinterpret_cast<const v4i*>(sW + (t >> 1) * S::KSTEP + pswz(32 * u + lc, 2 * (t & 1) + lh));
             };
             constexpr int PF = 2;
             v4i wq[PF][S::NSUB];
@@ -734,7 +737,7 @@ __global__ void __launch_bounds__(256, 2) stripe_kernel(const GemmParams p) {
             // The W fragments of step t + 2 are read from LDS before the MFMAs of step t, so that their
             // latency hides behind four MFMAs of this wave.
             auto wfrag = [&](int t, int u) -> v4i {
-                return *reinterpret_cast<const v4i*>(sW + (t >> 1) * S::KSTEP + swz(32 * u + lc, 2 * (t & 1) + lh));
+                return *reinterpret_cast<const v4i*>(sW + (t >> 1) * S::KSTEP + pswz(32 * u + lc, 2 * (t & 1) + lh));
             };
             constexpr int PF = 2;
             v4i wq[PF][S::NSUB];
