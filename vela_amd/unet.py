@@ -27,6 +27,18 @@ class GemmSet:
             if not keep_host:
                 p.h = None   # regenerated from the seed when checked
             self.probs.append(p)
+        # every row-maximum buffer of the set is a slice of one allocation, so that the timed graph
+        # clears them all with one fill kernel at its start (each buffer is written only by its own
+        # layer's GEMM, which runs later in the same replay)
+        n_rm = sum(p.rowmax.numel() for p in self.probs if p.rowmax is not None)
+        self.rowmax_all = torch.zeros(max(n_rm, 1), dtype=torch.int32, device=device)
+        off = 0
+        for p in self.probs:
+            if p.rowmax is not None:
+                n = p.rowmax.numel()
+                p.rowmax = self.rowmax_all[off:off + n]
+                p.E.rowmax = vg.ptr(p.rowmax)
+                off += n
         self.stream = torch.cuda.Stream(device=device)
         self.graph: vg.Graph | None = None
 
@@ -35,11 +47,11 @@ class GemmSet:
         return sum(L.ops for L in self.layers)
 
     def _enqueue(self, reseed: bool = True):
+        if not reseed:
+            vg.fill_u32(self.rowmax_all, 0)
         for p in self.probs:
             if reseed:
                 p.reset()
-            elif p.rowmax is not None:
-                vg.fill_u32(p.rowmax, 0)
             p.run(stream=self.stream)
 
     def run_eager(self):
@@ -47,12 +59,13 @@ class GemmSet:
             self._enqueue()
 
     def capture(self, reseed: bool = True):
-        """Capture the whole set into one graph: for each layer in forward order, rowmax zeroing by a
-        kernel (the engine clears every rowmax buffer it allocates, src/engine.cu:161) and the GEMM.
+        """Capture the whole set into one graph: the GEMMs in forward order, with every rowmax
+        buffer zeroed by a kernel before its GEMM (the engine clears every rowmax buffer it allocates,
+        src/engine.cu:161; here one fill over all of them at the start of the timed graph).
         With reseed, residual layers first copy their seeded residual back into Y, so that every
         replay computes the same bytes (the parity tests); without it, Y accumulates in place from
         replay to replay as the forward's residual stream does, and the graph holds only the GEMMs,
-        the rowmax fills and conv_in's pixel-max and im2col3 passes (the timed C5 set)."""
+        the rowmax fill and conv_in's pixel-max and im2col3 passes (the timed C5 set)."""
         self.run_eager()                      # first calls outside capture
         self.stream.synchronize()
         self.graph = vg.Graph(self.stream)
