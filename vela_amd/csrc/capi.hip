@@ -506,7 +506,16 @@ int hl2_impl(void* stream, const VgemmASrc* A, int Mp, int Mreal, const int8_t* 
 
     // stride-1 3x3 convolutions of int16 images with C % 64 == 0 run the halo-reuse kernel unless a
     // tile variant is forced; its K steps are 64-channel chunks (each covering all nine taps)
-    const int halo_bm = A->src == VGEMM_SRC_CONV16 && g_variant < 0 ? vk::conv_halo_bm(epi, p.H, p.W, p.C, p.stride, p.Ho, p.Wo) : 0;
+    int halo_bm = A->src == VGEMM_SRC_CONV16 && g_variant < 0 ? vk::conv_halo_bm(epi, p.H, p.W, p.C, p.stride, p.Ho, p.Wo) : 0;
+    if (halo_bm) {
+        // a halo grid that stays below one block per CU (no K split) against a tile grid that fills
+        // the chip: the tile kernel (measured: 2048 x 5760 x 1280, C = 640 at 16 x 16, 72 -> 54 us)
+        const int hv = halo_bm == 128 ? 0 : 1;
+        const long long htiles = (long long)cdiv(Mreal, TILES[hv].BM) * cdiv(Nreal, TILES[hv].BN);
+        const int hsplits = wsp.ws && epi != VGEMM_EPI_QKV && !E->gnstat ? pick_splitk(hv, Mreal, Nreal, Kp) : 1;
+        const long long tiles1 = (long long)cdiv(Mreal, TILES[1].BM) * cdiv(Nreal, TILES[1].BN);
+        if (htiles * hsplits < NCU && tiles1 >= NCU) halo_bm = 0;
+    }
     int variant = halo_bm ? (halo_bm == 128 ? 0 : 1) : g_variant >= 0 && g_variant < NVARIANT ? g_variant : pick_variant(Mreal, Nreal, Kp);
     if (variant >= 3 && (A->src == VGEMM_SRC_X32 || A->src == VGEMM_SRC_CONV32)) variant = 0;
     // int32 images with C % 64 == 0 run 64 x 128 tiles on the DMA kernel, which stages the raw int32
