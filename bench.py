@@ -437,8 +437,8 @@ def main():
     if args.only and args.only not in ONLY_NAMES and not (args.only.startswith("unet") and args.only[4:].isdigit()):
         ap.error(f"--only: unknown configuration {args.only}")
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path (the GEMM shards by rows with no "
-              "communication; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        print("bench.py measures one GPU: this build has no multi-GPU path (the GEMM would shard by output rows "
+              "with replicated weights and no communication). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
     import torch
