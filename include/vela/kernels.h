@@ -114,4 +114,15 @@ inline void k_fused_attention(hipStream_t st, const int8_t* qhi, const int8_t* q
                                          out, rowmax));
 }
 
+// src/kernels.h:31-35: the elementwise kernels between the GEMMs
+inline void k_act(hipStream_t st, int32_t* X, size_t n, const int32_t* L) { detail::kcheck(vgemm_act(st, X, n, L)); }
+inline void k_geglu(hipStream_t st, int32_t* A, const int32_t* G, size_t n, const int32_t* Lphi) { detail::kcheck(vgemm_geglu(st, A, G, n, Lphi)); }
+inline void k_add(hipStream_t st, int32_t* X, const int32_t* Y, size_t n) { detail::kcheck(vgemm_add(st, X, Y, n)); }
+inline void k_concat(hipStream_t st, const int32_t* A, int Ca, const int32_t* B, int Cb, int rows, int32_t* out, GnStat* gs = nullptr, int T = 0) {
+    detail::kcheck(vgemm_concat(st, A, Ca, B, Cb, rows, out, gs, T));
+}
+inline void k_upsample2(hipStream_t st, const int32_t* X, int B, int H, int W, int C, int32_t* out) {
+    detail::kcheck(vgemm_upsample2(st, X, B, H, W, C, out));
+}
+
 }  // namespace meow

@@ -210,6 +210,18 @@ int vgemm_graph_destroy(void* exec);
  * cudaMemsetAsync that zeroes rowmax buffers, src/engine.cu:161). */
 int vgemm_fill_u32(void* stream, uint32_t* p, size_t count, uint32_t value);
 
+/* ---- integer elementwise kernels between the GEMMs (src/kernels.h:31-35, src/kernels.cu:537-566,
+ * launchers :767-771), bit-exact; in place where the reference is. L is a 2049-entry Q16 table
+ * (lut.sigmoid for SiLU, lut.phi for GELU), interpolated by lut16i. */
+int vgemm_act(void* stream, int32_t* X, size_t n, const int32_t* L);                       /* k_act: x = sat32(rshr(x lut(x), 16)) */
+int vgemm_geglu(void* stream, int32_t* A, const int32_t* G, size_t n, const int32_t* L);   /* k_geglu: a = sat32(rshr(a sat32(rshr(g lut(g), 16)), 16)) */
+int vgemm_add(void* stream, int32_t* X, const int32_t* Y, size_t n);                        /* k_add: x = sat32(x + y) */
+/* k_concat: out[r] = [A[r] (Ca) | B[r] (Cb)] for rows rows; with gs (GnStat[samples * 32]) also the
+ * GroupNorm sum/min/max of out per the reference's rule (per 256-element region, T rows per sample;
+ * needs (Ca + Cb) % 32 == 0 and (T (Ca + Cb)) % 256 == 0, else "concat GN stats: shape"). */
+int vgemm_concat(void* stream, const int32_t* A, int Ca, const int32_t* B, int Cb, int rows, int32_t* out, void* gs, int T);
+int vgemm_upsample2(void* stream, const int32_t* X, int B, int H, int W, int C, int32_t* out);   /* k_upsample2: NHWC nearest x2 */
+
 /* meow::k_gn_init (src/kernels.h:25, src/kernels.cu:173): sum = ss = 0, mn = INT_MAX, mx = INT_MIN for
  * `count` VgemmGnStat records, by a kernel (capture-safe). */
 int vgemm_gn_init(void* stream, void* gs, int count);

@@ -57,6 +57,11 @@ _SIGS = {
     "orc_lut16i_n": (None, [P, P, P, SZ]),
     "orc_epi1_n": (None, [P, P, P, P, P, SZ]),
     "orc_quant_rows": (None, [P, I, I, I, P, P, P, I]),
+    "orc_act": (None, [P, SZ, P]),
+    "orc_geglu_n": (None, [P, P, SZ, P]),
+    "orc_add": (None, [P, P, SZ]),
+    "orc_concat": (None, [P, I, P, I, I, P, P, I]),
+    "orc_upsample2": (None, [P, I, I, I, I, P]),
     "orc_pixmax": (None, [P, I, I, P]),
     "orc_im2col3": (None, [P, P, I, I, I, I, I, P, P, P, I]),
     "orc_conv_e": (None, [P, I, I, I, I, P]),
@@ -430,6 +435,40 @@ def gn_records(cnt: int) -> np.ndarray:
     gs = np.zeros(cnt, GN_DTYPE)
     lib().orc_gn_init(a(gs), cnt)
     return gs
+
+
+# ---------------------------------------------------------------- elementwise (src/kernels.cu:536-561)
+
+def act(X, L):
+    """k_act: a copy of X with x = sat32(rshr(x lut16i(x, L), 16))."""
+    X = np.array(X, np.int32, copy=True); L = np.ascontiguousarray(L, np.int32)
+    lib().orc_act(a(X), X.size, a(L)); return X
+
+
+def geglu_n(A, G, L):
+    """k_geglu: a copy of A with a = sat32(rshr(a sat32(rshr(g lut16i(g, L), 16)), 16))."""
+    A = np.array(A, np.int32, copy=True); G = np.ascontiguousarray(G, np.int32); L = np.ascontiguousarray(L, np.int32)
+    lib().orc_geglu_n(a(A), a(G), A.size, a(L)); return A
+
+
+def add(X, Y):
+    """k_add: a copy of X with x = sat32(x + y)."""
+    X = np.array(X, np.int32, copy=True); Y = np.ascontiguousarray(Y, np.int32)
+    lib().orc_add(a(X), a(Y), X.size); return X
+
+
+def concat(A, Ca, B, Cb, rows, gs=None, T=0):
+    """k_concat: out [rows x (Ca + Cb)]; gs (GN_DTYPE records) accumulated in place when given."""
+    A = np.ascontiguousarray(A, np.int32); B = np.ascontiguousarray(B, np.int32)
+    out = np.zeros((rows, Ca + Cb), np.int32)
+    lib().orc_concat(a(A), Ca, a(B), Cb, rows, a(out), a(gs), T)
+    return out
+
+
+def upsample2(X, B, H, W, C):
+    X = np.ascontiguousarray(X, np.int32)
+    out = np.zeros((B, 2 * H, 2 * W, C), np.int32)
+    lib().orc_upsample2(a(X), B, H, W, C, a(out)); return out
 
 
 def gn_stats1(X, B, T, C, groups, gs=None):

@@ -806,6 +806,74 @@ void orc_lnorm_q(const int32_t* X, int M, int C, const int32_t* g, const int32_t
 
 /* ------------------------------------------------------------------ attention */
 
+/* ---------------------------------------------------------------- elementwise (src/kernels.cu:536-561)
+ * One element at a time in the reference's order, with its primitives: act_k, geglu_k, add_k,
+ * concat_k (+ the gnacc per-block records) and upsample2_k. */
+
+/* :537 act_k: x = sat32(rshr(x lut16i(x, L), 16)) */
+void orc_act(int32_t* X, size_t n, const int32_t* L) {
+    for (size_t i = 0; i < n; ++i) {
+        const int64_t x = X[i];
+        X[i] = (int32_t)orc_sat32(orc_rshr(x * orc_lut16i(x, L), 16));
+    }
+}
+
+/* :538-542 geglu_k: a = sat32(rshr(a sat32(rshr(g lut16i(g, L), 16)), 16)) */
+void orc_geglu_n(int32_t* A, const int32_t* G, size_t n, const int32_t* L) {
+    for (size_t i = 0; i < n; ++i) A[i] = orc_geglu(A[i], G[i], L);
+}
+
+/* :543 add_k: x = sat32(x + y) */
+void orc_add(int32_t* X, const int32_t* Y, size_t n) {
+    for (size_t i = 0; i < n; ++i) X[i] = (int32_t)orc_sat32((int64_t)X[i] + Y[i]);
+}
+
+/* :544-556 concat_k: element i of out (row i / Co, column i % Co) from A or B. With gs, the block of
+ * 256 consecutive elements i (blockDim = NT = 256, :9) gathers per group c / (Co / 32) the sum, min
+ * and max of its live elements (gnacc_add, :66) and flushes each group whose min is not INT_MAX to
+ * record (first element's row / T) * 32 + group (gnacc_flush, :67-69). */
+void orc_concat(const int32_t* A, int Ca, const int32_t* B, int Cb, int rows, int32_t* out, OrcGnStat* gs, int T) {
+    const int Co = Ca + Cb;
+    const size_t tot = (size_t)rows * Co;
+    for (size_t i = 0; i < tot; ++i) {
+        const size_t r = i / Co;
+        const int c = (int)(i % Co);
+        out[i] = c < Ca ? A[r * Ca + c] : B[r * Cb + (c - Ca)];
+    }
+    if (!gs) return;
+    const int cg = Co >> 5;
+    for (size_t b0 = 0; b0 < tot; b0 += 256) {
+        int64_t sum[32];
+        int32_t mn[32], mx[32];
+        for (int g = 0; g < 32; ++g) { sum[g] = 0; mn[g] = INT32_MAX; mx[g] = INT32_MIN; }
+        for (size_t i = b0; i < b0 + 256 && i < tot; ++i) {
+            const int g = (int)(i % Co) / cg;
+            sum[g] += out[i];
+            if (out[i] < mn[g]) mn[g] = out[i];
+            if (out[i] > mx[g]) mx[g] = out[i];
+        }
+        const int sample = (int)(b0 / Co / T);
+        for (int g = 0; g < 32; ++g) {
+            OrcGnStat* s = gs + sample * 32 + g;
+            gn_flush_region(sum[g], mn[g], mx[g], &s->sum, &s->mn, &s->mx);
+        }
+    }
+}
+
+/* :557-561 upsample2_k: out[b, y, x, c] = X[b, y / 2, x / 2, c] over the 2H x 2W image */
+void orc_upsample2(const int32_t* X, int B, int H, int W, int C, int32_t* out) {
+    const size_t tot = (size_t)B * 4 * H * W * C;
+    for (size_t i = 0; i < tot; ++i) {
+        const int c = (int)(i % C);
+        size_t p = i / C;
+        const int x = (int)(p % (2 * W));
+        p /= 2 * W;
+        const int y = (int)(p % (2 * H));
+        const size_t b = p / (2 * H);
+        out[i] = X[((b * H + (y >> 1)) * W + (x >> 1)) * C + c];
+    }
+}
+
 /* src/kernels.cu:611-631 (quant_heads_k): each (g, t) row of 64 values, e = row_exp(max |x|),
  * quant16, split16, and the sums of hi, lo and q; rows t >= T are the value 0 = (0, -128) */
 void orc_quant_heads(const int32_t* X, int B, int T, int C, int heads, int Tp, int8_t* hi, int8_t* lo, int32_t* e, int64_t* hs,

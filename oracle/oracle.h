@@ -133,6 +133,14 @@ void orc_lnorm(const int32_t* X, int M, int C, const int64_t* g, const int64_t* 
 void orc_lnorm_q(const int32_t* X, int M, int C, const int32_t* g, const int32_t* beta, int64_t den, int8_t* hi, int8_t* lo,
                  int32_t* e, int Kp);                                                                                 /* :349-390 */
 
+/* ---- the elementwise kernels between the GEMMs (src/kernels.h:31-35, src/kernels.cu:537-561) */
+void orc_act(int32_t* X, size_t n, const int32_t* L);                                 /* :537 in place */
+void orc_geglu_n(int32_t* A, const int32_t* G, size_t n, const int32_t* L);          /* :538-542 in place */
+void orc_add(int32_t* X, const int32_t* Y, size_t n);                                 /* :543 in place */
+/* :544-556: out = [A | B] per row; gs (may be NULL): GroupNorm records by the per-256-element rule */
+void orc_concat(const int32_t* A, int Ca, const int32_t* B, int Cb, int rows, int32_t* out, OrcGnStat* gs, int T);
+void orc_upsample2(const int32_t* X, int B, int H, int W, int C, int32_t* out);     /* :557-561 */
+
 /* ---- attention: the operand producers and the exact softmax attention (src/kernels.h:42-50,61,
  * src/kernels.cu:611-672,799-805; src/attn.cu:1-6 with src/kernels.cu:673-722 as its unfused form).
  * Heads of 64, G = B * heads groups; Q/K planes [G * Tp x 64] with e, hs, ls, tsum per row; V

@@ -236,3 +236,24 @@ def test_conv16_halo_rows(geom, epi, rows):
 
 def test_version():
     assert b"gfx950" in _lib.load().vgemm_version()
+
+
+def test_elementwise_errors():
+    """The elementwise entry points' checks (src/kernels.cu:763-771): empty work is a no-op, null
+    pointers and negative sizes fail, and concat with GroupNorm records needs Co % 32 == 0 and
+    (T Co) % 256 == 0 (the reference's "concat GN stats: shape")."""
+    lib = _lib.load()
+    fake = ctypes.c_void_p(0x1000)
+    assert lib.vgemm_act(None, None, 0, None) == 0
+    assert lib.vgemm_add(None, None, None, 0) == 0
+    assert lib.vgemm_act(None, None, 5, fake) != 0
+    assert lib.vgemm_geglu(None, fake, None, 5, fake) != 0
+    assert lib.vgemm_add(None, fake, None, 5) != 0
+    rc = lib.vgemm_concat(None, fake, 40, fake, 8, 4, fake, fake, 8)
+    assert rc != 0 and b"concat GN stats: shape" in lib.vgemm_last_error()
+    rc = lib.vgemm_concat(None, fake, 32, fake, 32, 4, fake, fake, 2)   # T Co = 128
+    assert rc != 0 and b"concat GN stats: shape" in lib.vgemm_last_error()
+    assert lib.vgemm_concat(None, fake, -1, fake, 8, 4, fake, None, 0) != 0
+    assert lib.vgemm_concat(None, fake, 8, fake, 8, 0, fake, None, 0) == 0
+    assert lib.vgemm_upsample2(None, fake, 1, 2, 2, -4, fake) != 0
+    assert lib.vgemm_upsample2(None, None, 0, 2, 2, 4, None) == 0

@@ -148,6 +148,11 @@ SIGNATURES = [
     ("vgemm_model_table", I, [P, ctypes.c_char_p, ctypes.POINTER(P), ctypes.POINTER(I)]),
     ("vgemm_last_error", ctypes.c_char_p, []),
     ("vgemm_version", ctypes.c_char_p, []),
+    ("vgemm_act", I, [P, P, SZ, P]),
+    ("vgemm_geglu", I, [P, P, P, SZ, P]),
+    ("vgemm_add", I, [P, P, P, SZ]),
+    ("vgemm_concat", I, [P, P, I, P, I, I, P, P, I]),
+    ("vgemm_upsample2", I, [P, P, I, I, I, I, P]),
 ]
 
 _lib = None

@@ -49,6 +49,11 @@ hipError_t launch_gn_apply_row(hipStream_t st, const int32_t* X, int M, int T, i
 hipError_t launch_lnorm(hipStream_t st, bool q, const int32_t* X, int M, int C, const void* g, const void* beta, i64 den, int32_t* Y, int8_t* hi, int8_t* lo,
                         int32_t* e, int Kp);
 hipError_t launch_gn_init(hipStream_t st, GnStat* gs, int n);
+hipError_t launch_act(hipStream_t st, int32_t* X, size_t n, const int32_t* L);
+hipError_t launch_geglu(hipStream_t st, int32_t* A, const int32_t* G, size_t n, const int32_t* L);
+hipError_t launch_add(hipStream_t st, int32_t* X, const int32_t* Y, size_t n);
+hipError_t launch_concat(hipStream_t st, const int32_t* A, int Ca, const int32_t* B, int Cb, int rows, int32_t* out, GnStat* gs, int T);
+hipError_t launch_upsample2(hipStream_t st, const int32_t* X, int B, int H, int W, int C, int32_t* out);
 }  // namespace vk
 
 namespace {
@@ -769,6 +774,41 @@ int vgemm_fill_u32(void* stream, uint32_t* p, size_t count, uint32_t value) {
     if (!p && count) return fail(VGEMM_ERR_ARG, "fill_u32: null pointer");
     if (!count) return ok();
     return hip_status(vk::launch_fill_u32(static_cast<hipStream_t>(stream), p, count, value), "fill_u32 launch");
+}
+
+// ---- elementwise kernels (src/kernels.cu:537-566, 767-771)
+int vgemm_act(void* stream, int32_t* X, size_t n, const int32_t* L) {
+    if (!n) return ok();
+    if (!X || !L) return fail(VGEMM_ERR_ARG, "act: null pointer");
+    return hip_status(vk::launch_act(static_cast<hipStream_t>(stream), X, n, L), "act launch");
+}
+
+int vgemm_geglu(void* stream, int32_t* A, const int32_t* G, size_t n, const int32_t* L) {
+    if (!n) return ok();
+    if (!A || !G || !L) return fail(VGEMM_ERR_ARG, "geglu: null pointer");
+    return hip_status(vk::launch_geglu(static_cast<hipStream_t>(stream), A, G, n, L), "geglu launch");
+}
+
+int vgemm_add(void* stream, int32_t* X, const int32_t* Y, size_t n) {
+    if (!n) return ok();
+    if (!X || !Y) return fail(VGEMM_ERR_ARG, "add: null pointer");
+    return hip_status(vk::launch_add(static_cast<hipStream_t>(stream), X, Y, n), "add launch");
+}
+
+int vgemm_concat(void* stream, const int32_t* A, int Ca, const int32_t* B, int Cb, int rows, int32_t* out, void* gs, int T) {
+    if (Ca < 0 || Cb < 0 || rows < 0 || (Ca && !A) || (Cb && !B)) return fail(VGEMM_ERR_ARG, "concat: bad arguments");
+    const int Co = Ca + Cb;
+    if (gs && (Co % 32 || T <= 0 || ((long long)T * Co) % 256)) return fail(VGEMM_ERR_ARG, "concat GN stats: shape");   // src/kernels.cu:768
+    if (!rows || !Co) return ok();
+    if (!out) return fail(VGEMM_ERR_ARG, "concat: bad arguments");
+    return hip_status(vk::launch_concat(static_cast<hipStream_t>(stream), A, Ca, B, Cb, rows, out, static_cast<vk::GnStat*>(gs), T), "concat launch");
+}
+
+int vgemm_upsample2(void* stream, const int32_t* X, int B, int H, int W, int C, int32_t* out) {
+    if (B < 0 || H < 0 || W < 0 || C < 0) return fail(VGEMM_ERR_ARG, "upsample2: bad arguments");
+    if (!B || !H || !W || !C) return ok();
+    if (!X || !out) return fail(VGEMM_ERR_ARG, "upsample2: null pointer");
+    return hip_status(vk::launch_upsample2(static_cast<hipStream_t>(stream), X, B, H, W, C, out), "upsample2 launch");
 }
 
 int vgemm_gn_init(void* stream, void* gs, int count) {
