@@ -1,4 +1,6 @@
-"""Writes tests/golden/tiny_model.poisd, a small synthetic POISDv1 model file.
+"""Writes tests/golden/tiny_model.poisd, a small synthetic POISDv1 model file; `block_tensors()` gives
+the arrays of a second synthetic model (written by the tests that need it) with two resnet blocks and
+one transformer block at reduced width.
 
 The real model (sd-turbo-int.poisd, 1.2 GB) is not available offline, so this file stands in for it:
 every tensor the reference's reader requires (src/poisd.cpp:47-49), in miniature, plus the kinds
@@ -96,6 +98,83 @@ def tensors():
               ("te.int16_table", r.integers(-30000, 30000, 10).astype(np.int16))]
     # a scalar (rank 0) and an empty tensor
     items += [("c.rank0", np.array(7, np.int32)), ("c.empty", np.zeros((0, 5), np.int32))]
+    return items
+
+
+# the block model (block_tensors): resnet A 64 -> 128 channels with a 1x1 shortcut, resnet B 128 -> 128,
+# a transformer of XF_HEADS heads of 64 (C = 128), GEGLU width XF_F, cross-attention context width CTX_C
+RESNET_A = "unet.down_blocks.1.resnets.0"
+RESNET_B = "unet.down_blocks.1.resnets.1"
+XF = "unet.down_blocks.1.attentions.0"
+XF_HEADS, XF_C, XF_F, CTX_C = 2, 128, 256, 96
+
+
+def sigmoid_table() -> np.ndarray:
+    """Q16 sigmoid over the 2049 grid points of lut16i (x in [-16, 16), step 1/64)."""
+    x = (np.arange(2049) - 1024) / 64.0
+    return np.round(65536.0 / (1.0 + np.exp(-x))).astype(np.int32)
+
+
+def exp_table32() -> np.ndarray:
+    """1025 entries, 2^30 at z = 0, falling by e every 2^16 of z (grid step 1024)."""
+    z = np.arange(1025, dtype=np.float64) * 1024.0
+    return np.round(np.exp(-z / 65536.0) * 2.0**30).astype(np.int32)
+
+
+def _linear_scaled(items, r, base, N, K):
+    """A linear whose requantisation keeps the output's scale near the input's: s around
+    log2(sqrt(K) * 73 * m) (73 = the standard deviation of a uniform int8 weight)."""
+    w = r.integers(-127, 128, (N, K)).astype(np.int8)
+    m = r.integers(1 << 14, 1 << 15, N).astype(np.int32)
+    s0 = int(round(np.log2(np.sqrt(K) * 73.0 * 23170.0)))
+    s = r.integers(s0 - 1, s0 + 2, N).astype(np.int32)
+    b = r.integers(-20000, 20000, N).astype(np.int32)
+    items += [(base + ".w", w), (base + ".m", m), (base + ".s", s), (base + ".b", b)]
+
+
+def _norm(items, r, base, C):
+    items += [(base + ".g", r.integers(40000, 90000, C).astype(np.int32)),
+              (base + ".beta", r.integers(-6000, 6000, C).astype(np.int32)),
+              (base + ".eps", np.array([100000], np.int32))]
+
+
+def block_tensors():
+    r = np.random.default_rng(0x424C4B53)
+    items = []
+    _linear(items, r, "unet.conv_in", 64, 9 * 8)
+    _linear(items, r, "unet.conv_out", 8, 9 * 64)
+    items += [("te.tok.w", r.integers(-127, 128, (32, 16)).astype(np.int8)),
+              ("te.tok.m", r.integers(1 << 14, 1 << 15, 32).astype(np.int32)),
+              ("te.pos", r.integers(-1000, 1000, (4, 16)).astype(np.int32)),
+              ("lut.gauss", np.arange(257, dtype=np.int32) * 3),
+              ("lut.exp", exp_table32()),
+              ("lut.sigmoid", sigmoid_table()),
+              ("lut.phi", phi_table()),
+              ("c.sig", np.array([12345], np.int32)),
+              ("c.cin", np.array([-77], np.int32)),
+              ("tok.vocab", np.frombuffer(b"hello\nworld\n", np.uint8).copy()),
+              ("tok.merges", np.frombuffer(b"h e\nl o\n", np.uint8).copy())]
+    for base, ci, co, short in ((RESNET_A, 64, 128, True), (RESNET_B, 128, 128, False)):
+        _norm(items, r, base + ".norm1", ci)
+        _linear_scaled(items, r, base + ".conv1", co, 9 * ci)
+        _norm(items, r, base + ".norm2", co)
+        _linear_scaled(items, r, base + ".conv2", co, 9 * co)
+        if short:
+            _linear_scaled(items, r, base + ".conv_shortcut", co, ci)
+    C, F = XF_C, XF_F
+    b = XF + ".transformer_blocks.0"
+    _norm(items, r, XF + ".norm", C)
+    _linear_scaled(items, r, XF + ".proj_in", C, C)
+    for n in ("norm1", "norm2", "norm3"):
+        _norm(items, r, f"{b}.{n}", C)
+    for n in ("attn1.to_q", "attn1.to_k", "attn1.to_v", "attn1.to_out.0", "attn2.to_q", "attn2.to_out.0"):
+        _linear_scaled(items, r, f"{b}.{n}", C, C)
+    _linear_scaled(items, r, f"{b}.attn2.to_k", C, CTX_C)
+    _linear_scaled(items, r, f"{b}.attn2.to_v", C, CTX_C)
+    _linear_scaled(items, r, f"{b}.ff.net.0.proj.a", F, C)
+    _linear_scaled(items, r, f"{b}.ff.net.0.proj.g", F, C)
+    _linear_scaled(items, r, f"{b}.ff.net.2", C, F)
+    _linear_scaled(items, r, XF + ".proj_out", C, C)
     return items
 
 

@@ -1,5 +1,5 @@
 """The C ABI of libvgemm.so without a GPU: the library loads, exports every entry point that
-include/vgemm.h and include/vgemm_model.h declare, the ctypes mirror of VgemmASrc / VgemmAEpi / VgemmGnStat has the C layout (checked
+include/vgemm.h, include/vgemm_model.h and include/vgemm_engine.h declare, the ctypes mirror of VgemmASrc / VgemmAEpi / VgemmGnStat has the C layout (checked
 against a gcc-compiled probe of the header), and argument checks fail the way the reference throws
 (src/gemm_hl.cu:351,357; src/gemm.cu:41) before any device work."""
 import ctypes
@@ -12,7 +12,7 @@ import pytest
 from vela_amd import _lib
 
 ROOT = Path(__file__).resolve().parent.parent
-HEADERS = [ROOT / "include" / "vgemm.h", ROOT / "include" / "vgemm_model.h"]
+HEADERS = [ROOT / "include" / "vgemm.h", ROOT / "include" / "vgemm_model.h", ROOT / "include" / "vgemm_engine.h"]
 
 
 def declared():
@@ -41,12 +41,14 @@ PROBE = r"""
 #include <stddef.h>
 #include "vgemm.h"
 #include "vgemm_model.h"
+#include "vgemm_engine.h"
 #define F(T, f) printf(#T " " #f " %zu\n", offsetof(T, f));
 int main(void) {
     printf("VgemmASrc sizeof %zu\nVgemmAEpi sizeof %zu\nVgemmGnStat sizeof %zu\n", sizeof(VgemmASrc), sizeof(VgemmAEpi),
            sizeof(VgemmGnStat));
     printf("VgemmTensor sizeof %zu\nVgemmLin sizeof %zu\nVgemmNorm sizeof %zu\n", sizeof(VgemmTensor), sizeof(VgemmLin),
            sizeof(VgemmNorm));
+    printf("VgemmActivation sizeof %zu\n", sizeof(VgemmActivation));
     %FIELDS%
     return 0;
 }
@@ -54,7 +56,7 @@ int main(void) {
 
 
 STRUCTS = (("VgemmASrc", _lib.ASrc), ("VgemmAEpi", _lib.AEpi), ("VgemmGnStat", _lib.GnStat), ("VgemmTensor", _lib.Tensor),
-           ("VgemmLin", _lib.Lin), ("VgemmNorm", _lib.Norm))
+           ("VgemmLin", _lib.Lin), ("VgemmNorm", _lib.Norm), ("VgemmActivation", _lib.Activation))
 
 
 def test_struct_layout_matches_c(tmp_path):
@@ -257,3 +259,24 @@ def test_elementwise_errors():
     assert lib.vgemm_concat(None, fake, 8, fake, 8, 0, fake, None, 0) == 0
     assert lib.vgemm_upsample2(None, fake, 1, 2, 2, -4, fake) != 0
     assert lib.vgemm_upsample2(None, None, 0, 2, 2, 4, None) == 0
+
+
+def test_engine_argument_errors():
+    """The engine entry points' checks before any device work: a model and an arena size are needed,
+    a null engine or malformed activation fails, and destroy / arena_peak take a null engine."""
+    lib = _lib.load()
+    h = ctypes.c_void_p()
+    assert lib.vgemm_engine_create(None, 1 << 20, 0, ctypes.byref(h)) == -1 and not h.value
+    assert b"a model and an arena size" in lib.vgemm_last_error()
+    assert lib.vgemm_engine_create(None, 1 << 20, 0, None) == -1
+    lib.vgemm_engine_destroy(None)
+    assert lib.vgemm_engine_arena_peak(None) == 0
+    x = _lib.Activation(d=0x1000, B=2, T=64, C=64)
+    out = _lib.Activation(d=0x2000, B=2, T=64, C=128)
+    assert lib.vgemm_engine_resnet(None, None, ctypes.byref(x), 8, 8, b"p", ctypes.byref(out)) == -1
+    assert b"null engine" in lib.vgemm_last_error()
+    assert lib.vgemm_engine_resnet(None, None, ctypes.byref(x), 8, 7, b"p", ctypes.byref(out)) == -1   # T != H W
+    assert b"resnet: bad arguments" in lib.vgemm_last_error()
+    bad = _lib.Activation(d=0, B=2, T=64, C=64)
+    assert lib.vgemm_engine_transformer(None, None, ctypes.byref(bad), b"p", 2, ctypes.byref(out)) == -1
+    assert lib.vgemm_engine_set_context(None, None, ctypes.byref(x), b"b", 0) == -1

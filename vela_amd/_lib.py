@@ -91,7 +91,14 @@ class Norm(ctypes.Structure):
     _fields_ = [("C", I), ("den", LL), ("g_host", P), ("beta_host", P), ("g", P), ("beta", P)]
 
 
-# (name, restype, argtypes) of every entry point declared in include/vgemm.h and include/vgemm_model.h
+class Activation(ctypes.Structure):
+    """VgemmActivation (include/vgemm_engine.h) == meow::Tensor (src/engine.h:36)."""
+
+    _fields_ = [("d", P), ("B", I), ("T", I), ("C", I), ("rowmax", P), ("gnst", P)]
+
+
+# (name, restype, argtypes) of every entry point declared in include/vgemm.h, include/vgemm_model.h and
+# include/vgemm_engine.h
 SIGNATURES = [
     ("vgemm_asrc_init", None, [ctypes.POINTER(ASrc)]),
     ("vgemm_aepi_init", None, [ctypes.POINTER(AEpi)]),
@@ -153,6 +160,12 @@ SIGNATURES = [
     ("vgemm_add", I, [P, P, P, SZ]),
     ("vgemm_concat", I, [P, P, I, P, I, I, P, P, I]),
     ("vgemm_upsample2", I, [P, P, I, I, I, I, P]),
+    ("vgemm_engine_create", I, [P, SZ, I, ctypes.POINTER(P)]),
+    ("vgemm_engine_destroy", None, [P]),
+    ("vgemm_engine_arena_peak", SZ, [P]),
+    ("vgemm_engine_resnet", I, [P, P, ctypes.POINTER(Activation), I, I, ctypes.c_char_p, ctypes.POINTER(Activation)]),
+    ("vgemm_engine_set_context", I, [P, P, ctypes.POINTER(Activation), ctypes.c_char_p, I]),
+    ("vgemm_engine_transformer", I, [P, P, ctypes.POINTER(Activation), ctypes.c_char_p, I, ctypes.POINTER(Activation)]),
 ]
 
 _lib = None
