@@ -64,7 +64,9 @@ typedef struct VgemmGnStat {
 } VgemmGnStat;
 
 /* Epilogue description: meow::AEpi (src/gemm_hl.h:18-26) in the same order, plus an optional
- * split-K workspace (ws, ws_bytes; none = no split-K).
+ * split-K workspace (ws, ws_bytes; none = no split-K). Fields an epilogue does not read are ignored,
+ * as the reference ignores them (src/gemm_hl.cu:176-177, 279-296): gnstat outside EPI_PLAIN, the
+ * residual on EPI_GEGLU / EPI_SPLIT3 / EPI_QKV, rowmax on EPI_SPLIT3 / EPI_QKV.
  *   gnstat/gnT (EPI_PLAIN): add the sum, min and max of every output y (after the residual) to
  *     gnstat[(row / gnT) * 32 + col / (Nreal / 32)]; Nreal % 32 == 0, gnT % 64 == 0; the caller
  *     initialises the records (vgemm_gn_init). src/gemm_hl.cu:175-177, 285-287, 306-309.
@@ -150,7 +152,7 @@ void vgemm_set_tile_order(int order);
  * with src/kernels.cu:172-305,349-420: GroupNorm of X[B, T, C] (NHWC rows, `groups` groups of C /
  * groups channels) from VgemmGnStat records -- gathered by a GEMM epilogue (AEpi.gnstat, after
  * vgemm_gn_init) and finalised by vgemm_gn_fin1, or by vgemm_gn_stats1 -- and LayerNorm rows.
- * C % 4 == 0 and C <= 2560 throughout; groups <= 64 and C % groups == 0; X, Y, g and beta 16-byte
+ * C % 4 == 0 and C <= 2560 throughout; groups <= 64 (32 for gn_apply_row) and C % groups == 0; X, Y, g and beta 16-byte
  * aligned; int16-view planes hi/lo [rows x Kp] with Kp >= C, Kp % 4 == 0, 4-byte aligned. */
 int vgemm_gn_stats1(void* stream, const int32_t* X, int B, int T, int C, int groups, void* gs);   /* k_gn_stats1: init, sum/min/max, fin1 */
 int vgemm_gn_fin1(void* stream, void* gs, int cnt, int64_t n);                                   /* k_gn_fin1: mean, e (n = T * C / groups) */

@@ -130,9 +130,7 @@ def test_hl2_shape_errors(kw, code, msg):
     (dict(src=0, hi=FAKE, lo=FAKE, ld8=64), dict(epi=4, heads=1, C=64, T=8, TpQ=8, TpK=8), -1, "Nreal = 3C"),
     (dict(src=0, hi=FAKE, lo=FAKE, ld8=64), dict(gnstat=FAKE), -1, "GroupNorm statistics need"),
     (dict(src=0, hi=FAKE, lo=FAKE, ld8=64), dict(gnstat=FAKE, gnT=96), -1, "gnT % 64"),
-    (dict(src=0, hi=FAKE, lo=FAKE, ld8=64), dict(gnstat=FAKE, gnT=64, epi=3, Lphi=FAKE), -1, "need EPI_PLAIN"),
     (dict(src=0, hi=FAKE, lo=FAKE, ld8=64), dict(epi=2), -1, "Lphi"),
-    (dict(src=0, hi=FAKE, lo=FAKE, ld8=64), dict(epi=2, Lphi=FAKE, residual=FAKE), -1, "no residual"),
     (dict(src=0, hi=FAKE, lo=FAKE, ld8=64), dict(epi=1, Cs=30), -1, "SPLIT3"),
     (dict(src=0, hi=FAKE, lo=FAKE, ld8=64), dict(Y=None), -1, "null Y"),
 ])
@@ -154,8 +152,6 @@ QKV = dict(epi=4, heads=1, C=64, T=40, TpQ=128, TpK=64, Y2=FAKE, qhi=FAKE, qlo=F
     (dict(QKV, kts=None), "every q/k output"),
     (dict(QKV, Y2=FAKE + 4), "16-byte aligned Y2"),
     (dict(QKV, qlo=FAKE + 2), "4-byte aligned"),
-    (dict(QKV, residual=FAKE), "no residual"),
-    (dict(QKV, rowmax=FAKE), "no residual, rowmax"),
 ])
 def test_hl2_qkv_errors(aepi, msg):
     """EPI_QKV (src/gemm_hl.cu:179-241) needs N = 3C with C = 64 heads and every q/k output."""
@@ -280,3 +276,23 @@ def test_engine_argument_errors():
     bad = _lib.Activation(d=0, B=2, T=64, C=64)
     assert lib.vgemm_engine_transformer(None, None, ctypes.byref(bad), b"p", 2, ctypes.byref(out)) == -1
     assert lib.vgemm_engine_set_context(None, None, ctypes.byref(x), b"b", 0) == -1
+
+
+def test_norm_argument_errors():
+    """The integer norms' checks: groups divide C and are at most 64 (32 for the row kernel, whose
+    reference caches 32 records per row), C % 4 and C <= 2560, 16-byte aligned rows, the int16 view's
+    planes with Kp >= C and Kp % 4 == 0."""
+    lib = _lib.load()
+    ok_args = (None, FAKE, 2, 8, 128)
+    assert lib.vgemm_gn_stats1(*ok_args, 96, FAKE) == -1   # 128 % 96
+    assert b"groups must divide C" in lib.vgemm_last_error()
+    assert lib.vgemm_gn_stats1(None, FAKE, 2, 8, 256, 128, FAKE) == -1   # more than 64 groups
+    assert lib.vgemm_gn_stats2(None, FAKE, 2, 8, 128, 32, 0, FAKE) == -1   # den
+    assert lib.vgemm_gn_stats1(None, FAKE, 2, 8, 2564, 4, FAKE) == -1   # C > 2560
+    assert lib.vgemm_gn_stats1(None, FAKE + 4, 2, 8, 128, 32, FAKE) == -1   # alignment
+    rc = lib.vgemm_gn_apply_row(None, FAKE, 2, 8, 128, 64, FAKE, FAKE, FAKE, None, FAKE, None, None, None, None, 0)
+    assert rc == -1 and b"at most 32 groups" in lib.vgemm_last_error()
+    rc = lib.vgemm_gn_apply_row(None, FAKE, 2, 8, 128, 32, FAKE, FAKE, FAKE, None, None, None, FAKE, FAKE, FAKE, 126)
+    assert rc == -1 and b"Kp >= C" in lib.vgemm_last_error()
+    rc = lib.vgemm_lnorm_q(None, FAKE, 4, 128, FAKE, FAKE, 100000, FAKE, FAKE, FAKE, 130)
+    assert rc == -1 and b"Kp % 4 == 0" in lib.vgemm_last_error()

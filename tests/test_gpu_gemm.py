@@ -128,7 +128,7 @@ class Case:
             A.Ho, A.Wo, A.K = (H - 1) // stride + 1, (W - 1) // stride + 1, 9 * C
         return A
 
-    def run_gpu(self, ws_bytes=0):
+    def run_gpu(self, ws_bytes=0, extra=None):
         keep = {}
         A = self.asrc(keep)
         w, cst = dev(self.w), dev(self.cst)
@@ -148,14 +148,16 @@ class Case:
         if ws_bytes:
             ws = torch.empty(ws_bytes // 4 + 16, dtype=torch.int32, device="cuda")
             E.ws, E.ws_bytes = vg.ptr(ws), ws_bytes
+        for f, v in (extra or {}).items():
+            setattr(E, f, v)
         vg.k_gemm_hl2(A, self.Mp, self.M, w, self.Kp, self.Np, self.N, self.Kp, cst, E)
         torch.cuda.synchronize()
         if self.epi == vg.EPI_SPLIT3:
             return tuple(to_np(y) for y in Ys), None
         return to_np(Y), (to_np(rm).view(np.uint32) if rm is not None else None)
 
-    def check(self, ws_bytes=0, what=""):
-        got, grm = self.run_gpu(ws_bytes)
+    def check(self, ws_bytes=0, what="", extra=None):
+        got, grm = self.run_gpu(ws_bytes, extra)
         want, wrm = self.reference()
         if self.epi == vg.EPI_SPLIT3:
             for i in range(3):
@@ -386,6 +388,28 @@ def test_conv_splitk():
     vg.set_splitk(4)
     c = Case(vg.SRC_CONV16, 2 * 8 * 8, 128, 9 * 256, seed=17, conv=(2, 8, 8, 256, 1), residual=True)
     c.check(ws_bytes=vg.workspace_bytes(c.Mp, c.M, c.Np, c.N, c.Kp, 0), what="conv splitk")
+
+
+@pytest.mark.parametrize("epi,fields", [
+    (vg.EPI_GEGLU, ("residual", "gnstat")),
+    (vg.EPI_GELU, ("gnstat",)),
+    (vg.EPI_SPLIT3, ("residual", "rowmax", "gnstat")),
+])
+@pytest.mark.parametrize("variant", [-1, 0, 4])
+def test_unread_fields_are_ignored(epi, fields, variant):
+    """AEpi fields an epilogue does not read are accepted and ignored, as the reference's epilogue
+    ignores them (src/gemm_hl.cu:176-177, 279-296): the GroupNorm records outside EPI_PLAIN, the
+    residual on GEGLU / SPLIT3, the row maxima on SPLIT3. Results equal the call without them and
+    the buffers those fields point at are left untouched."""
+    vg.set_variant(variant)
+    sentinel = torch.full((3 * 4096,), 0x3C3C3C3C, dtype=torch.int32, device="cuda")
+    extra = {f: vg.ptr(sentinel[i * 4096:]) for i, f in enumerate(fields)}
+    if "gnstat" in fields:
+        extra["gnT"] = 64
+    c = Case(vg.SRC_I16, 128, 192, 320, epi=epi, seed=41 + epi, s_range=(16, 24), rowmax=epi != vg.EPI_SPLIT3,
+             Cs=64 if epi == vg.EPI_SPLIT3 else 0)
+    c.check(what=f"epi {epi} with {fields} v{variant}", extra=extra)
+    assert (to_np(sentinel) == 0x3C3C3C3C).all(), f"epi {epi}: a buffer of an unread field was written"
 
 
 def test_k_gemm_hl_wrapper():

@@ -44,7 +44,8 @@ def make_x(r, M, C, mode):
 
 
 @pytest.mark.parametrize("mode", [0, 1, 2])
-@pytest.mark.parametrize("B,T,C,groups", [(2, 5, 64, 32), (2, 300, 320, 32), (1, 64, 1280, 32), (2, 77, 2560, 32), (3, 129, 96, 8)])
+@pytest.mark.parametrize("B,T,C,groups", [(2, 5, 64, 32), (2, 300, 320, 32), (1, 64, 1280, 32), (2, 77, 2560, 32), (3, 129, 96, 8),
+                                          (2, 77, 1280, 64), (1, 64, 2560, 64), (2, 9, 128, 64)])
 def test_gn_stats(gpu, mode, B, T, C, groups):
     r = np.random.default_rng(mode + 3 * C + T)
     x = make_x(r, B * T, C, mode)
@@ -57,9 +58,13 @@ def test_gn_stats(gpu, mode, B, T, C, groups):
     den = 100000
     oracle.gn_stats2(x, B, T, C, groups, den, want)
     vn.k_gn_stats2(X, B, T, C, groups, den, gs)
-    vn.k_gn_stats2(X, B, T, C, groups, den, gs)   # assigns ss, as the reference's does: a repeat changes nothing
     torch.cuda.synchronize()
     check_records(records_np(gs), want, f"stats2 mode {mode} {B}x{T}x{C}")
+    # ss accumulates, as the reference's atomicAdd does (src/kernels.cu:201): a repeat adds it again
+    oracle.gn_stats2(x, B, T, C, groups, den, want)
+    vn.k_gn_stats2(X, B, T, C, groups, den, gs)
+    torch.cuda.synchronize()
+    check_records(records_np(gs), want, f"stats2 twice mode {mode} {B}x{T}x{C}")
 
 
 @pytest.mark.parametrize("C", [32, 64, 128, 320, 512, 640, 960, 1024, 1280, 1920, 2560])
@@ -104,6 +109,28 @@ def test_gn_apply_row_reference_cases(gpu, C, mode):
         vn.k_gn_apply(X, B, T, C, groups, S, dev(g.astype(np.int64)), dev(beta.astype(np.int64)), Y)
         torch.cuda.synchronize()
         assert_equal(to_np(Y), oracle.gn_apply(x, B, T, C, groups, st, g.astype(np.int64), beta.astype(np.int64)), f"gn_apply C={C} mode={mode}")
+
+
+@pytest.mark.parametrize("B,T,C,groups", [(2, 77, 1280, 64), (1, 64, 2560, 64), (2, 5, 64, 64), (3, 10, 96, 48)])
+def test_gn_apply_many_groups(gpu, B, T, C, groups):
+    """The elementwise k_gn_apply with more than 32 groups (up to 64): statistics from k_gn_stats1/2,
+    every element against the oracle. (The row kernel, like the reference's, takes at most 32.)"""
+    r = np.random.default_rng(B * T + C + groups)
+    x = make_x(r, B * T, C, 1)
+    den = 100000
+    st = oracle.gn_stats1(x, B, T, C, groups)
+    oracle.gn_stats2(x, B, T, C, groups, den, st)
+    g = r.integers(30000, 90000, C).astype(np.int64)
+    beta = r.integers(-20000, 20000, C).astype(np.int64)
+    X = dev(x)
+    gs = vg.gn_stats_alloc(B * groups)
+    vn.k_gn_stats1(X, B, T, C, groups, gs)
+    vn.k_gn_stats2(X, B, T, C, groups, den, gs)
+    Y = torch.zeros((B * T, C), dtype=torch.int32, device="cuda")
+    vn.k_gn_apply(X, B, T, C, groups, gs, dev(g), dev(beta), Y)
+    torch.cuda.synchronize()
+    check_records(records_np(gs), st, f"records {groups} groups C={C}")
+    assert_equal(to_np(Y), oracle.gn_apply(x, B, T, C, groups, st, g, beta), f"gn_apply {groups} groups C={C}")
 
 
 @pytest.mark.parametrize("C", [4, 12, 124, 128, 132, 320, 512, 640, 768, 1024, 1280, 2560])

@@ -37,7 +37,7 @@ def filled(shape, dtype):
     return t.view(getattr(torch, np.dtype(dtype).name)).view(*shape)
 
 
-def run_qkv(c: Case, heads, T, TpQ, TpK, ws_bytes=0):
+def run_qkv(c: Case, heads, T, TpQ, TpK, ws_bytes=0, extra=None):
     C = 64 * heads
     B = c.M // T
     keep = {}
@@ -53,6 +53,8 @@ def run_qkv(c: Case, heads, T, TpQ, TpK, ws_bytes=0):
     E = vg.AEpi(epi=vg.EPI_QKV, heads=heads, T=T, TpQ=TpQ, TpK=TpK, C=C, Y2=vg.ptr(V),
                 qhi=vg.ptr(q[0]), qlo=vg.ptr(q[1]), qe=vg.ptr(q[2]), qhs=vg.ptr(q[3]), qls=vg.ptr(q[4]), qts=vg.ptr(q[5]),
                 khi=vg.ptr(k[0]), klo=vg.ptr(k[1]), ke=vg.ptr(k[2]), khs=vg.ptr(k[3]), kls=vg.ptr(k[4]), kts=vg.ptr(k[5]))
+    for f, v in (extra or {}).items():
+        setattr(E, f, v)
     ws = None
     if ws_bytes:
         ws = torch.empty(ws_bytes // 4 + 16, dtype=torch.int32, device="cuda")
@@ -62,13 +64,13 @@ def run_qkv(c: Case, heads, T, TpQ, TpK, ws_bytes=0):
     return {p: tuple(to_np(x) for x in v) for p, v in out.items()} | {"v": to_np(V)}
 
 
-def check_qkv(src, heads, T, B=2, K=320, seed=0, variant=-1, ws_bytes=0, **kw):
+def check_qkv(src, heads, T, B=2, K=320, seed=0, variant=-1, ws_bytes=0, extra=None, **kw):
     C = 64 * heads
     M = B * T
     TpQ, TpK = cf.align(T, 128), cf.align(T, 64)
     vg.set_variant(variant)
     c = Case(src, M, 3 * C, K, seed=seed, **kw)
-    got = run_qkv(c, heads, T, TpQ, TpK, ws_bytes)
+    got = run_qkv(c, heads, T, TpQ, TpK, ws_bytes, extra)
     Y, _ = c.reference()
     want = oracle.qkv_heads(Y, M, C, heads, T, TpQ, TpK, fill=FILL)
     what = f"qkv src {src} heads {heads} T {T} K {K}"
@@ -94,6 +96,15 @@ def test_qkv_row_shifts_and_wide_range():
 def test_qkv_ignores_tile_override(variant):
     """QKV runs on the 128 x 128 tiles whatever variant is forced (src/gemm_hl.cu:358 forces 64 x 64)."""
     check_qkv(vg.SRC_I16, 2, 77, K=320, seed=20 + variant, variant=variant)
+
+
+def test_qkv_ignores_unread_fields():
+    """A residual, row maxima and GroupNorm records given to EPI_QKV are neither read nor written, as
+    the reference's QKV epilogue returns before it reaches them (src/gemm_hl.cu:179-241)."""
+    sentinel = torch.full((4096,), 0x3C3C3C3C, dtype=torch.int32, device="cuda")
+    extra = dict(residual=vg.ptr(sentinel), rowmax=vg.ptr(sentinel[1024:]), gnstat=vg.ptr(sentinel[2048:]), gnT=64)
+    check_qkv(vg.SRC_I8, 2, 64, seed=31, s_range=(12, 24), extra=extra)
+    assert (to_np(sentinel) == 0x3C3C3C3C).all()
 
 
 def test_qkv_with_workspace():

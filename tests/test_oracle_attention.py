@@ -62,6 +62,33 @@ def test_quant_heads_definition(T, Tp):
             assert hs[w] == qh.astype(np.int64).sum() and ls[w] == ql.astype(np.int64).sum() and ts[w] == q.sum()
 
 
+@pytest.mark.parametrize("T,Tp", [(5, 8), (77, 128), (64, 64), (1, 64)])
+def test_quant_heads_pad_definition(T, Tp):
+    """orc_quant_heads_pad (src/kernels.cu:799-805): rows t >= T of every group become the operand of
+    the value 0 -- the hi/lo split of 0 (pinned with split16), e 0, hs and ls the sums of those planes,
+    tsum the sum of the quantised zeros -- equal to the pad rows orc_quant_heads writes; rows t < T are
+    not touched."""
+    r = np.random.default_rng(T * 131 + Tp)
+    G = 5
+    bufs = [r.integers(-128, 128, (G * Tp, 64)).astype(np.int8), r.integers(-128, 128, (G * Tp, 64)).astype(np.int8),
+            r.integers(-1000, 1000, G * Tp).astype(np.int32)] + [r.integers(-(1 << 40), 1 << 40, G * Tp) for _ in range(3)]
+    before = [b.copy() for b in bufs]
+    oracle.quant_heads_pad(G, T, Tp, *bufs)
+    zh, zl = (x.astype(np.int64) for x in planes(np.zeros(64, np.int64)))
+    assert (zh == 0).all() and (zl == -128).all()
+    X = r.integers(-(2**31), 2**31, (G * T, 64), dtype=np.int64).astype(np.int32)
+    ref = oracle.quant_heads(X, G, T, 64, 1, Tp)
+    for g in range(G):
+        for t in range(Tp):
+            w = g * Tp + t
+            if t < T:
+                assert all(np.array_equal(a[w], b[w]) for a, b in zip(bufs, before))
+                continue
+            assert (bufs[0][w] == zh).all() and (bufs[1][w] == zl).all()
+            assert bufs[2][w] == 0 and bufs[3][w] == zh.sum() == 0 and bufs[4][w] == zl.sum() == -8192 and bufs[5][w] == 0
+            assert all(np.array_equal(a[w], b[w]) for a, b in zip(bufs, ref))
+
+
 def test_quant_v_definition():
     r = np.random.default_rng(3)
     B, heads, C, Tk, Tkp = 2, 2, 128, 77, 128

@@ -63,7 +63,7 @@ int g_variant = -1;   // meow::g_gemm_hl_variant: process-wide, written by tests
 int g_splitk = 0;
 int g_tile_order = -1;
 
-int fail(int code, const char* fmt, ...) {
+__attribute__((format(printf, 2, 3))) int fail(int code, const char* fmt, ...) {
     char buf[512];
     va_list ap;
     va_start(ap, fmt);
@@ -388,6 +388,14 @@ int view_impl(const VgemmASrc* A, const VgemmAEpi* E, vk::GemmParams& p, int Mre
 int hl2_impl(void* stream, const VgemmASrc* A, int Mp, int Mreal, const int8_t* W, int ldw, int Np, int Nreal, int Kp,
              const int32_t* cst, const VgemmAEpi* E, WsPolicy wsp) {
     if (!A || !E) return fail(VGEMM_ERR_ARG, "gemm_hl: null ASrc/AEpi");
+    // The fields an epilogue does not read are ignored, as the reference's epilogue ignores them
+    // (src/gemm_hl.cu:176-177, 279-296): the GroupNorm statistics outside EPI_PLAIN, the residual
+    // outside EPI_PLAIN / EPI_GELU, the row maxima on EPI_SPLIT3 and EPI_QKV.
+    VgemmAEpi Eu = *E;
+    if (Eu.epi != VGEMM_EPI_PLAIN) Eu.gnstat = nullptr;
+    if (Eu.epi == VGEMM_EPI_GEGLU || Eu.epi == VGEMM_EPI_SPLIT3 || Eu.epi == VGEMM_EPI_QKV) Eu.residual = nullptr;
+    if (Eu.epi == VGEMM_EPI_SPLIT3 || Eu.epi == VGEMM_EPI_QKV) Eu.rowmax = nullptr;
+    E = &Eu;
     if (!vgemm_supported(Mp, Np, Kp)) return fail(VGEMM_ERR_ARG, "gemm_hl: unsupported shape (Mp %d, Np %d, Kp %d)", Mp, Np, Kp);
     if (Mreal < 0 || Mreal > Mp || Nreal < 0 || Nreal > Np) return fail(VGEMM_ERR_ARG, "gemm_hl: Mreal/Nreal outside Mp/Np");
     if (!W || !cst || ldw < Kp || ldw % 16 || !aligned16(W)) return fail(VGEMM_ERR_ARG, "gemm_hl: W must be 16-byte aligned with ldw >= Kp, ldw %% 16 == 0");
@@ -395,8 +403,8 @@ int hl2_impl(void* stream, const VgemmASrc* A, int Mp, int Mreal, const int8_t* 
     if (E->epi != VGEMM_EPI_QKV && !E->Y && !E->vhi) return fail(VGEMM_ERR_ARG, "gemm_hl: null Y");
     // GroupNorm statistics (src/gemm_hl.h:22, src/engine.h:110): EPI_PLAIN, 32 groups of whole
     // columns, a block's rows in at most two samples
-    if (E->gnstat && (E->epi != VGEMM_EPI_PLAIN || Nreal % 32 || E->gnT <= 0 || E->gnT % 64))
-        return fail(VGEMM_ERR_ARG, "gemm_hl: GroupNorm statistics need EPI_PLAIN, Nreal %% 32 == 0 and gnT %% 64 == 0");
+    if (E->gnstat && (Nreal % 32 || E->gnT <= 0 || E->gnT % 64))
+        return fail(VGEMM_ERR_ARG, "gemm_hl: GroupNorm statistics need Nreal %% 32 == 0 and gnT %% 64 == 0");
     if (E->epi == VGEMM_EPI_QKV) {
         // src/engine.cu:318-326: N = 3C, C = 64 heads, rows = B*T, Tp >= T
         if (E->heads <= 0 || E->C != 64 * E->heads || Nreal != 3 * E->C || E->T <= 0 || E->TpQ < E->T || E->TpK < E->T)
@@ -406,7 +414,6 @@ int hl2_impl(void* stream, const VgemmASrc* A, int Mp, int Mreal, const int8_t* 
             if (!q) return fail(VGEMM_ERR_ARG, "gemm_hl: EPI_QKV needs Y2 and every q/k output");
         if (!aligned16(E->Y2) || ((uintptr_t)E->qhi | (uintptr_t)E->qlo | (uintptr_t)E->khi | (uintptr_t)E->klo) & 3)
             return fail(VGEMM_ERR_ARG, "gemm_hl: EPI_QKV needs a 16-byte aligned Y2 and 4-byte aligned hi/lo planes");
-        if (E->residual || E->rowmax || E->gnstat) return fail(VGEMM_ERR_ARG, "gemm_hl: EPI_QKV takes no residual, rowmax or statistics");
     }
     if (Mreal == 0 || Nreal == 0) return ok();
 
@@ -485,13 +492,11 @@ int hl2_impl(void* stream, const VgemmASrc* A, int Mp, int Mreal, const int8_t* 
         if (Nreal % 2) return fail(VGEMM_ERR_ARG, "gemm_hl: EPI_GEGLU needs an even Nreal (interleaved a/g columns)");
         if (!E->Lphi) return fail(VGEMM_ERR_ARG, "gemm_hl: EPI_GEGLU needs Lphi");
         if (E->ldy < Nreal / 2) return fail(VGEMM_ERR_ARG, "gemm_hl: ldy < Nreal/2");
-        if (E->residual) return fail(VGEMM_ERR_ARG, "gemm_hl: EPI_GEGLU takes no residual");
         vec = vec && E->ldy % 4 == 0;
         break;
     case VGEMM_EPI_SPLIT3:
         if (E->Cs <= 0 || E->Cs % 4 || Nreal > 3 * E->Cs) return fail(VGEMM_ERR_ARG, "gemm_hl: EPI_SPLIT3 needs Cs %% 4 == 0 and Nreal <= 3*Cs");
         if ((Nreal > E->Cs && !E->Y1) || (Nreal > 2 * E->Cs && !E->Y2)) return fail(VGEMM_ERR_ARG, "gemm_hl: EPI_SPLIT3 needs Y1/Y2");
-        if (E->rowmax || E->residual) return fail(VGEMM_ERR_ARG, "gemm_hl: EPI_SPLIT3 takes no residual or rowmax");
         vec = vec && (!E->Y1 || aligned16(E->Y1)) && (!E->Y2 || aligned16(E->Y2));
         break;
     case VGEMM_EPI_QKV:
@@ -871,6 +876,8 @@ int vgemm_gn_apply(void* stream, const int32_t* X, int B, int T, int C, int grou
 int vgemm_gn_apply_row(void* stream, const int32_t* X, int B, int T, int C, int groups, const void* gs, const int32_t* g, const int32_t* beta,
                        const int32_t* Lsig, int32_t* Y, uint32_t* pm, int8_t* hi, int8_t* lo, int32_t* e, int Kp) {
     if (int rc = gn_shape("gn_apply_row", X, B, T, C, groups, gs)) return rc;
+    // the reference's row kernel caches 32 records per row (src/kernels.cu:287-305)
+    if (groups > 32) return fail(VGEMM_ERR_ARG, "gn_apply_row: at most 32 groups");
     if (!g || !beta || !aligned16(g) || !aligned16(beta)) return fail(VGEMM_ERR_ARG, "gn_apply_row: g/beta must be 16-byte aligned");
     if (hi) {
         if (int rc = view_planes("gn_apply_row", C, hi, lo, e, Kp)) return rc;
@@ -921,7 +928,7 @@ int vgemm_quant_v(void* stream, const int32_t* X, int B, int Tk, int C, int head
     (void)scratch;   // the column maxima stay inside one block per group here
     if (!X || !vthi || !vtlo || !ev || !vsum || B <= 0 || heads <= 0 || Tk <= 0 || Tkp < Tk || C < 64 * heads)
         return fail(VGEMM_ERR_ARG, "quant_v: bad arguments");
-    if (Tkp % 64 || !aligned16(vthi) || !aligned16(vtlo)) return fail(VGEMM_ERR_ARG, "quant_v: Tkp % 64 and 16-byte aligned planes required");
+    if (Tkp % 64 || !aligned16(vthi) || !aligned16(vtlo)) return fail(VGEMM_ERR_ARG, "quant_v: Tkp %% 64 == 0 and 16-byte aligned planes required");
     return hip_status(vk::launch_quant_v(static_cast<hipStream_t>(stream), X, B, Tk, C, heads, Tkp, vthi, vtlo, ev, reinterpret_cast<long long*>(vsum)),
                       "quant_v launch");
 }

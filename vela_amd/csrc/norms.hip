@@ -162,12 +162,6 @@ __global__ void __launch_bounds__(256) gn_fin1_kernel(GnStat* __restrict__ gs, i
     gs[i].e = max(0, row_exp64(m) - 5);
 }
 
-// zero ss ahead of the squared-deviation atomics: k_gn_stats2 assigns ss (src/kernels.cu:201)
-__global__ void __launch_bounds__(256) gn_clear_ss_kernel(GnStat* __restrict__ gs, int cnt) {
-    const int i = blockIdx.x * 256 + threadIdx.x;
-    if (i < cnt) gs[i].ss = 0;
-}
-
 // src/kernels.cu:203-210
 __global__ void __launch_bounds__(256) gn_fin2_kernel(GnStat* __restrict__ gs, int cnt, i64 n, i64 den) {
     const int i = blockIdx.x * 256 + threadIdx.x;
@@ -681,7 +675,8 @@ hipError_t launch_gn_reduce(hipStream_t st, bool sq, const int32_t* X, int B, in
     const int runs = int(nblocks(T, size_t(R) * rpt));
     const dim3 grid(unsigned(B * runs), unsigned(nslab));
     if (sq) {
-        hipLaunchKernelGGL(gn_clear_ss_kernel, dim3(nblocks(size_t(B) * groups, 256)), dim3(256), 0, st, gs, B * groups);
+        // ss accumulates onto the records' value, as the reference's k_gn_stats2 does (src/kernels.cu:201):
+        // gn_init / k_gn_stats1 zero it
         hipLaunchKernelGGL(gn_reduce_kernel<true>, grid, dim3(GN_THREADS), 0, st, X, T, C, groups, qs, rpt, runs, gs);
     } else {
         hipLaunchKernelGGL(gn_reduce_kernel<false>, grid, dim3(GN_THREADS), 0, st, X, T, C, groups, qs, rpt, runs, gs);
