@@ -137,7 +137,7 @@ def vendor_planar_us(L, stream, steps=10, warmup=3):
 
 
 class ViewRun:
-    """C2 with the int16 view as its output (AEpi.vhi/vlo/ve): the row-maxima clear, the
+    """C2 with the int16 view as its output (vgemm_hl2_view): the row-maxima clear, the
     row-stationary kernel writing each chunk at its running exponent, and the fix-up pass; and, for
     comparison, the two-pass route (int32 Y + rowmax, then k_quant_rows)."""
 
@@ -153,8 +153,7 @@ class ViewRun:
         self.e = torch.empty(L.M, dtype=torch.int32, device="cuda")
         nb = vg.view_workspace_bytes(L.M, L.N, L.epi)
         self.ws = torch.empty(nb // 4 + 64, dtype=torch.int32, device="cuda")
-        self.E = vg.AEpi(epi=L.epi, Lphi=vg.ptr(prob.lphi), vhi=vg.ptr(self.hi), vlo=vg.ptr(self.lo), ve=vg.ptr(self.e), vld=F,
-                         ws=vg.ptr(self.ws), ws_bytes=nb)
+        self.E = vg.AEpi(epi=L.epi, Lphi=vg.ptr(prob.lphi), ws=vg.ptr(self.ws), ws_bytes=nb)
         # A + W + the int16 view + e + cst
         self.bytes = 2 * L.M * L.K + L.N * L.K + 2 * L.M * F + 4 * L.M + 16 * L.N
 
@@ -162,7 +161,8 @@ class ViewRun:
         from vela_amd import gemm as vg
 
         p, L = self.prob, self.L
-        vg.k_gemm_hl2(p.A, L.Mp, L.M, p.w, p.w.shape[1], L.Np, L.N, L.Kp, p.cst, self.E, stream=stream)
+        vg.k_gemm_hl2_view(p.A, L.Mp, L.M, p.w, p.w.shape[1], L.Np, L.N, L.Kp, p.cst, self.E, self.hi, self.lo, self.e, L.Nout,
+                           stream=stream)
 
     def two_pass(self, stream):
         from vela_amd import gemm as vg

@@ -50,7 +50,11 @@ struct AEpi {
     int8_t *qhi = nullptr, *qlo = nullptr, *khi = nullptr, *klo = nullptr; int32_t *qe = nullptr, *ke = nullptr;
     int64_t *qhs = nullptr, *qls = nullptr, *qts = nullptr, *khs = nullptr, *kls = nullptr, *kts = nullptr;
     void* ws = nullptr; size_t ws_bytes = 0;
-    int8_t *vhi = nullptr, *vlo = nullptr; int32_t* ve = nullptr; int vld = 0;   // int16 view (include/vgemm.h)
+};
+
+// The int16 view of the output (vgemm_hl2_view; no counterpart in the reference's fused GEMM).
+struct View {
+    int8_t* hi = nullptr; int8_t* lo = nullptr; int32_t* e = nullptr; int ld = 0;
 };
 
 namespace detail {
@@ -73,7 +77,6 @@ inline VgemmAEpi to_c(const AEpi& e) {
     c.qhi = e.qhi; c.qlo = e.qlo; c.khi = e.khi; c.klo = e.klo; c.qe = e.qe; c.ke = e.ke;
     c.qhs = e.qhs; c.qls = e.qls; c.qts = e.qts; c.khs = e.khs; c.kls = e.kls; c.kts = e.kts;
     c.ws = e.ws; c.ws_bytes = e.ws_bytes;
-    c.vhi = e.vhi; c.vlo = e.vlo; c.ve = e.ve; c.vld = e.vld;
     return c;
 }
 }  // namespace detail
@@ -84,6 +87,15 @@ inline void k_gemm_hl2(hipStream_t st, const ASrc& A, int Mp, int Mreal, const i
     const VgemmASrc a = detail::to_c(A);
     const VgemmAEpi e = detail::to_c(E);
     detail::check(vgemm_hl2(st, &a, Mp, Mreal, W, ldw, Np, Nreal, Kp, reinterpret_cast<const int32_t*>(cst), &e));
+}
+
+// k_gemm_hl2 writing the int16 view of its output instead of Y (this library's extension)
+inline void k_gemm_hl2_view(hipStream_t st, const ASrc& A, int Mp, int Mreal, const int8_t* W, int ldw, int Np, int Nreal, int Kp,
+                            const int4* cst, const AEpi& E, const View& V) {
+    const VgemmASrc a = detail::to_c(A);
+    const VgemmAEpi e = detail::to_c(E);
+    const VgemmView v{V.hi, V.lo, V.e, V.ld};
+    detail::check(vgemm_hl2_view(st, &a, Mp, Mreal, W, ldw, Np, Nreal, Kp, reinterpret_cast<const int32_t*>(cst), &e, &v));
 }
 
 // src/gemm_hl.h:29 / src/gemm_hl.cu:335-349

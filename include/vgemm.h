@@ -84,14 +84,6 @@ typedef struct VgemmAEpi {
     int8_t *qhi, *qlo, *khi, *klo; int32_t *qe, *ke;
     int64_t *qhs, *qls, *qts, *khs, *kls, *kts;
     void* ws; size_t ws_bytes;          /* optional split-K workspace (device memory) */
-    /* Optional int16 view of the output instead of Y (no counterpart in the reference's fused GEMM;
-     * the semantics of its quant_row_out, src/kernels.cu:317-331, as k_epilogue_geglu_q / k_quant_rows
-     * give them): per output row r < Mreal, e = row_exp(max |y|) into ve[r], q = quant16_32(y, e)
-     * into the planes vhi/vlo [Mreal x vld] (hi = q >> 8, lo = (q & 255) - 128), columns
-     * [nout, vld) padded with (0, -128). EPI_PLAIN / EPI_GEGLU / EPI_GELU with int16 rows or int8
-     * planes, Kp <= 320, no residual, rowmax or statistics; Y is not written (may be NULL); vld % 16
-     * == 0, planes 16-byte aligned. Needs vgemm_view_workspace_bytes() of workspace in ws. */
-    int8_t *vhi, *vlo; int32_t* ve; int vld;
 } VgemmAEpi;
 
 /* Fill an ASrc / AEpi with the reference's default member values (src = SRC_I8, stride = 1, rest 0). */
@@ -102,6 +94,19 @@ void vgemm_aepi_init(VgemmAEpi* e);
  * output column n; rows of A >= Mreal and columns >= Nreal are neither read as data nor written. */
 int vgemm_hl2(void* stream, const VgemmASrc* A, int Mp, int Mreal, const int8_t* W, int ldw, int Np, int Nreal,
               int Kp, const int32_t* cst, const VgemmAEpi* E);
+
+/* No counterpart in the reference's fused GEMM: the int16 view of the output instead of Y (the
+ * semantics of its quant_row_out, src/kernels.cu:317-331, as k_epilogue_geglu_q / k_quant_rows give
+ * them): per output row r < Mreal, e = row_exp(max |y|) into V->e[r], q = quant16_32(y, e) into the
+ * planes V->hi / V->lo [Mreal x V->ld] (hi = q >> 8, lo = (q & 255) - 128), columns [nout, ld) padded
+ * with (0, -128). EPI_PLAIN / EPI_GEGLU / EPI_GELU with int16 rows or int8 planes, Kp <= 320; E's
+ * residual, rowmax and statistics must be NULL and E->Y is not written; V->ld % 16 == 0, planes
+ * 16-byte aligned. Needs vgemm_view_workspace_bytes() of workspace in E->ws. */
+typedef struct VgemmView {
+    int8_t* hi; int8_t* lo; int32_t* e; int ld;
+} VgemmView;
+int vgemm_hl2_view(void* stream, const VgemmASrc* A, int Mp, int Mreal, const int8_t* W, int ldw, int Np, int Nreal,
+                   int Kp, const int32_t* cst, const VgemmAEpi* E, const VgemmView* V);
 
 /* No counterpart in the reference: vgemm_hl2 for callers that cannot allocate device memory (code
  * under stream capture, tight serving loops, harnesses that forbid hipMalloc). Same arguments, same
@@ -167,7 +172,7 @@ int vgemm_lnorm(void* stream, const int32_t* X, int M, int C, const int64_t* g, 
 int vgemm_lnorm_q(void* stream, const int32_t* X, int M, int C, const int32_t* g, const int32_t* beta, int64_t den, int8_t* hi,
                   int8_t* lo, int32_t* e, int Kp);                                                 /* k_lnorm_q: the int16 view of the row */
 
-/* Workspace bytes the int16 view (AEpi.vhi) of an Mreal x Nreal call with this epilogue needs:
+/* Workspace bytes the int16 view (vgemm_hl2_view) of an Mreal x Nreal call with this epilogue needs:
  * the row maxima, one exponent byte and one 32-bit mask per (row, 32 output columns). */
 size_t vgemm_view_workspace_bytes(int Mreal, int Nreal, int epi);
 /* Workspace bytes vgemm_hl2 uses for this shape at the current settings (0 = no split-K). */

@@ -48,7 +48,7 @@ int main(void) {
            sizeof(VgemmGnStat));
     printf("VgemmTensor sizeof %zu\nVgemmLin sizeof %zu\nVgemmNorm sizeof %zu\n", sizeof(VgemmTensor), sizeof(VgemmLin),
            sizeof(VgemmNorm));
-    printf("VgemmActivation sizeof %zu\n", sizeof(VgemmActivation));
+    printf("VgemmActivation sizeof %zu\nVgemmView sizeof %zu\n", sizeof(VgemmActivation), sizeof(VgemmView));
     %FIELDS%
     return 0;
 }
@@ -56,7 +56,8 @@ int main(void) {
 
 
 STRUCTS = (("VgemmASrc", _lib.ASrc), ("VgemmAEpi", _lib.AEpi), ("VgemmGnStat", _lib.GnStat), ("VgemmTensor", _lib.Tensor),
-           ("VgemmLin", _lib.Lin), ("VgemmNorm", _lib.Norm), ("VgemmActivation", _lib.Activation))
+           ("VgemmLin", _lib.Lin), ("VgemmNorm", _lib.Norm), ("VgemmActivation", _lib.Activation),
+           ("VgemmView", _lib.View))
 
 
 def test_struct_layout_matches_c(tmp_path):

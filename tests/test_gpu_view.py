@@ -1,4 +1,4 @@
-"""The int16 view of a GEMM's output (AEpi.vhi/vlo/ve): the row-stationary kernel's speculative
+"""The int16 view of a GEMM's output (vgemm_hl2_view): the row-stationary kernel's speculative
 per-chunk quantisation plus the fix-up pass must give exactly the reference's quant_row_out
 (src/kernels.cu:317-331) of the GEMM's int32 output -- e = row_exp(max |y|), q = quant16_32(y, e),
 hi = q >> 8, lo = (q & 255) - 128, pad columns (0, -128) -- checked against the oracle's
@@ -18,7 +18,7 @@ from vela_amd._lib import VgemmError
 pytestmark = pytest.mark.gpu
 
 
-def run_view(c: Case, vld: int, noalloc: bool = False):
+def run_view(c: Case, vld: int):
     """The view of Case c on the GPU: (hi, lo, e) as numpy arrays."""
     keep = {}
     A = c.asrc(keep)
@@ -28,11 +28,8 @@ def run_view(c: Case, vld: int, noalloc: bool = False):
     e = torch.full((c.M,), -7, dtype=torch.int32, device="cuda")
     nb = vg.view_workspace_bytes(c.M, c.N, c.epi)
     ws = torch.empty(nb // 4 + 64, dtype=torch.int32, device="cuda")
-    E = vg.AEpi(epi=c.epi, Lphi=vg.ptr(lut), vhi=vg.ptr(hi), vlo=vg.ptr(lo), ve=vg.ptr(e), vld=vld, ws=vg.ptr(ws), ws_bytes=nb)
-    if noalloc:
-        vg.k_gemm_hl2_noalloc(A, c.Mp, c.M, w, c.Kp, c.Np, c.N, c.Kp, cst, E)
-    else:
-        vg.k_gemm_hl2(A, c.Mp, c.M, w, c.Kp, c.Np, c.N, c.Kp, cst, E)
+    E = vg.AEpi(epi=c.epi, Lphi=vg.ptr(lut), ws=vg.ptr(ws), ws_bytes=nb)
+    vg.k_gemm_hl2_view(A, c.Mp, c.M, w, c.Kp, c.Np, c.N, c.Kp, cst, E, hi, lo, e, vld)
     torch.cuda.synchronize()
     return to_np(hi), to_np(lo), to_np(e)
 
@@ -43,8 +40,8 @@ def expect_view(c: Case, vld: int):
     return hi[:c.M], lo[:c.M], e[:c.M]
 
 
-def check(c: Case, vld: int, what: str, noalloc: bool = False):
-    got = run_view(c, vld, noalloc)
+def check(c: Case, vld: int, what: str):
+    got = run_view(c, vld)
     want = expect_view(c, vld)
     for g, w_, name in zip(got, want, ("hi", "lo", "e")):
         assert_equal(g, w_, f"{what} {name}")
@@ -118,8 +115,8 @@ def test_view_c2_full_rows_sampled():
     e = torch.empty(L.M, dtype=torch.int32, device="cuda")
     nb = vg.view_workspace_bytes(L.M, L.N, L.epi)
     ws = torch.empty(nb // 4 + 64, dtype=torch.int32, device="cuda")
-    E2 = vg.AEpi(epi=L.epi, Lphi=vg.ptr(p.lphi), vhi=vg.ptr(hi), vlo=vg.ptr(lo), ve=vg.ptr(e), vld=F, ws=vg.ptr(ws), ws_bytes=nb)
-    vg.k_gemm_hl2(p.A, L.Mp, L.M, p.w, p.w.shape[1], L.Np, L.N, L.Kp, p.cst, E2)
+    E2 = vg.AEpi(epi=L.epi, Lphi=vg.ptr(p.lphi), ws=vg.ptr(ws), ws_bytes=nb)
+    vg.k_gemm_hl2_view(p.A, L.Mp, L.M, p.w, p.w.shape[1], L.Np, L.N, L.Kp, p.cst, E2, hi, lo, e, F)
     torch.cuda.synchronize()
     # the view of the (separately oracle-checked) int32 output, all rows
     qh, ql, qe = oracle.quant_rows(y, L.M, F, F, F)
@@ -132,12 +129,15 @@ def test_view_c2_full_rows_sampled():
         assert_equal(y[r0:r0 + 64], want[r0:r0 + 64], f"C2 rows {r0}")
 
 
-def test_view_noalloc_matches():
+def test_view_and_plain_call_agree():
+    """The view call and a plain call of the same GEMM on the same inputs: Y of the plain call is
+    left untouched by the view call, and the view is the quantisation of that Y."""
     c = Case(vg.SRC_I16, 2048, 2560, 320, epi=vg.EPI_GEGLU, seed=31)
-    a = run_view(c, 1280)
-    b = run_view(c, 1280, noalloc=True)
-    for x, y_, name in zip(a, b, ("hi", "lo", "e")):
-        assert_equal(y_, x, f"noalloc view {name}")
+    y, _ = c.run_gpu()
+    hi, lo, e = run_view(c, 1280)
+    qh, ql, qe = oracle.quant_rows(y, c.M, c.nout, c.nout, 1280)
+    for g, w_, name in zip((hi, lo, e), (qh[:c.M], ql[:c.M], qe[:c.M]), ("hi", "lo", "e")):
+        assert_equal(g, w_, f"view of the plain call's Y {name}")
 
 
 def test_view_errors():
@@ -147,15 +147,16 @@ def test_view_errors():
     w, cst = dev(c.w), dev(c.cst)
     hi = torch.empty((256, 128), dtype=torch.int8, device="cuda")
     lo, e = torch.empty_like(hi), torch.empty(256, dtype=torch.int32, device="cuda")
-    base = dict(epi=vg.EPI_PLAIN, vhi=vg.ptr(hi), vlo=vg.ptr(lo), ve=vg.ptr(e), vld=128)
+    run = lambda E, ld=128, a=A, d=c: vg.k_gemm_hl2_view(a, d.Mp, d.M, w if d is c else dev(d.w), d.Kp, d.Np, d.N, d.Kp,
+                                                          cst if d is c else dev(d.cst), E, hi, lo, e, ld)
     with pytest.raises(VgemmError, match="needs a workspace"):
-        vg.k_gemm_hl2(A, c.Mp, c.M, w, c.Kp, c.Np, c.N, c.Kp, cst, vg.AEpi(**base))
+        run(vg.AEpi(epi=vg.EPI_PLAIN))
     ws = torch.empty(1 << 20, dtype=torch.int32, device="cuda")
     with pytest.raises(VgemmError, match="no residual"):
-        vg.k_gemm_hl2(A, c.Mp, c.M, w, c.Kp, c.Np, c.N, c.Kp, cst, vg.AEpi(**base, residual=vg.ptr(e), ws=vg.ptr(ws), ws_bytes=4 << 20))
-    with pytest.raises(VgemmError, match="vld"):
-        vg.k_gemm_hl2(A, c.Mp, c.M, w, c.Kp, c.Np, c.N, c.Kp, cst, vg.AEpi(**{**base, "vld": 120}, ws=vg.ptr(ws), ws_bytes=4 << 20))
+        run(vg.AEpi(epi=vg.EPI_PLAIN, residual=vg.ptr(e), ws=vg.ptr(ws), ws_bytes=4 << 20))
+    with pytest.raises(VgemmError, match="ld >= output columns"):
+        run(vg.AEpi(epi=vg.EPI_PLAIN, ws=vg.ptr(ws), ws_bytes=4 << 20), ld=120)
     d = Case(vg.SRC_I16, 256, 128, 640, epi=vg.EPI_PLAIN, seed=2)
     keep2 = {}
     with pytest.raises(VgemmError, match="Kp <= 320"):
-        vg.k_gemm_hl2(d.asrc(keep2), d.Mp, d.M, dev(d.w), d.Kp, d.Np, d.N, d.Kp, dev(d.cst), vg.AEpi(**base, ws=vg.ptr(ws), ws_bytes=4 << 20))
+        run(vg.AEpi(epi=vg.EPI_PLAIN, ws=vg.ptr(ws), ws_bytes=4 << 20), a=d.asrc(keep2), d=d)

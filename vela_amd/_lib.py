@@ -63,8 +63,18 @@ class AEpi(ctypes.Structure):
         ("qhi", P), ("qlo", P), ("khi", P), ("klo", P), ("qe", P), ("ke", P),
         ("qhs", P), ("qls", P), ("qts", P), ("khs", P), ("kls", P), ("kts", P),
         ("ws", P), ("ws_bytes", SZ),
-        ("vhi", P), ("vlo", P), ("ve", P), ("vld", I),
     ]
+
+    def __init__(self, **kw):
+        super().__init__()
+        for k, v in kw.items():
+            setattr(self, k, v)
+
+
+class View(ctypes.Structure):
+    """VgemmView (include/vgemm.h): the int16 view of a GEMM's output (vgemm_hl2_view)."""
+
+    _fields_ = [("hi", P), ("lo", P), ("e", P), ("ld", I)]
 
     def __init__(self, **kw):
         super().__init__()
@@ -104,6 +114,7 @@ SIGNATURES = [
     ("vgemm_aepi_init", None, [ctypes.POINTER(AEpi)]),
     ("vgemm_hl2", I, [P, ctypes.POINTER(ASrc), I, I, P, I, I, I, I, P, ctypes.POINTER(AEpi)]),
     ("vgemm_hl2_noalloc", I, [P, ctypes.POINTER(ASrc), I, I, P, I, I, I, I, P, ctypes.POINTER(AEpi)]),
+    ("vgemm_hl2_view", I, [P, ctypes.POINTER(ASrc), I, I, P, I, I, I, I, P, ctypes.POINTER(AEpi), ctypes.POINTER(View)]),
     ("vgemm_hl", I, [P, P, P, I, I, I, P, I, I, I, I, P, P, P, I, P, I, I, P, P, P]),
     ("vgemm_conv_e", I, [P, P, I, I, I, I, P]),
     ("vgemm_supported", I, [I, I, I]),

@@ -348,10 +348,11 @@ struct WsPolicy {
     bool strict;
 };
 
-// The int16 view of the output (AEpi.vhi/vlo/ve): the row-stationary kernel writes each chunk at its
+// The int16 view of the output (vgemm_hl2_view): the row-stationary kernel writes each chunk at its
 // running row exponent with correction bits and row maxima in the workspace, then the fix-up pass
 // settles every row at its final exponent (stripe_kernel.h, producers.hip: view_fix_kernel).
-int view_impl(const VgemmASrc* A, const VgemmAEpi* E, vk::GemmParams& p, int Mreal, int Nreal, const WsPolicy& wsp, hipStream_t st) {
+int view_impl(const VgemmASrc* A, const VgemmAEpi* E, const VgemmView* V, vk::GemmParams& p, int Mreal, int Nreal, const WsPolicy& wsp,
+              hipStream_t st) {
     const int epi = E->epi;
     if (epi != VGEMM_EPI_PLAIN && epi != VGEMM_EPI_GEGLU && epi != VGEMM_EPI_GELU)
         return fail(VGEMM_ERR_ARG, "gemm_hl int16 view: EPI_PLAIN, EPI_GEGLU or EPI_GELU only");
@@ -361,16 +362,16 @@ int view_impl(const VgemmASrc* A, const VgemmAEpi* E, vk::GemmParams& p, int Mre
     if (epi == VGEMM_EPI_GEGLU && Nreal % 2) return fail(VGEMM_ERR_ARG, "gemm_hl: EPI_GEGLU needs an even Nreal (interleaved a/g columns)");
     if (epi != VGEMM_EPI_PLAIN && !E->Lphi) return fail(VGEMM_ERR_ARG, "gemm_hl: EPI_GEGLU/EPI_GELU need Lphi");
     const int nout = epi == VGEMM_EPI_GEGLU ? Nreal / 2 : Nreal;
-    if (nout % 4 || !E->vlo || !E->ve || E->vld < nout || E->vld % 16 || !aligned16(E->vhi) || !aligned16(E->vlo))
-        return fail(VGEMM_ERR_ARG, "gemm_hl int16 view: output columns %% 4 == 0, vhi/vlo 16-byte aligned, vld >= output columns, vld %% 16 == 0, and ve");
-    if ((long long)Mreal * E->vld > MAX_EXTENT) return fail(VGEMM_ERR_UNSUPPORTED, "gemm_hl int16 view: planes larger than 2 GiB");
+    if (nout % 4 || !V->hi || !V->lo || !V->e || V->ld < nout || V->ld % 16 || !aligned16(V->hi) || !aligned16(V->lo))
+        return fail(VGEMM_ERR_ARG, "gemm_hl int16 view: output columns %% 4 == 0, hi/lo 16-byte aligned, ld >= output columns, ld %% 16 == 0, and e");
+    if ((long long)Mreal * V->ld > MAX_EXTENT) return fail(VGEMM_ERR_UNSUPPORTED, "gemm_hl int16 view: planes larger than 2 GiB");
     const ViewWs vw = view_ws(Mreal, nout);
     if (!wsp.ws || wsp.bytes < vw.bytes)
         return fail(wsp.strict ? VGEMM_ERR_UNSUPPORTED : VGEMM_ERR_ARG, "gemm_hl int16 view: needs a workspace of %zu bytes (AEpi.ws)", vw.bytes);
     if (!aligned16(wsp.ws)) return fail(VGEMM_ERR_ARG, "gemm_hl: workspace must be 16-byte aligned");
     char* ws = static_cast<char*>(wsp.ws);
-    p.vhi = E->vhi; p.vlo = E->vlo; p.vld = E->vld;
-    p.v_bytes = unsigned((long long)Mreal * E->vld);
+    p.vhi = V->hi; p.vlo = V->lo; p.vld = V->ld;
+    p.v_bytes = unsigned((long long)Mreal * V->ld);
     p.vgroups = cdiv(nout, 32);
     p.vmax = reinterpret_cast<uint32_t*>(ws + vw.max_off);
     p.vmask = reinterpret_cast<uint32_t*>(ws + vw.mask_off);
@@ -381,12 +382,12 @@ int view_impl(const VgemmASrc* A, const VgemmAEpi* E, vk::GemmParams& p, int Mre
     if (rc) return rc;
     rc = hip_status(vk::launch_stripe_view(A->src, epi, p, st), "gemm_hl int16 view launch");
     if (rc) return rc;
-    return hip_status(vk::launch_view_fix(st, p.vmax, p.vexp, p.vmask, Mreal, nout, p.vgroups, E->vhi, E->vlo, E->vld, E->ve),
+    return hip_status(vk::launch_view_fix(st, p.vmax, p.vexp, p.vmask, Mreal, nout, p.vgroups, V->hi, V->lo, V->ld, V->e),
                       "gemm_hl int16 view fix-up");
 }
 
 int hl2_impl(void* stream, const VgemmASrc* A, int Mp, int Mreal, const int8_t* W, int ldw, int Np, int Nreal, int Kp,
-             const int32_t* cst, const VgemmAEpi* E, WsPolicy wsp) {
+             const int32_t* cst, const VgemmAEpi* E, WsPolicy wsp, const VgemmView* V = nullptr) {
     if (!A || !E) return fail(VGEMM_ERR_ARG, "gemm_hl: null ASrc/AEpi");
     // The fields an epilogue does not read are ignored, as the reference's epilogue ignores them
     // (src/gemm_hl.cu:176-177, 279-296): the GroupNorm statistics outside EPI_PLAIN, the residual
@@ -400,7 +401,7 @@ int hl2_impl(void* stream, const VgemmASrc* A, int Mp, int Mreal, const int8_t* 
     if (Mreal < 0 || Mreal > Mp || Nreal < 0 || Nreal > Np) return fail(VGEMM_ERR_ARG, "gemm_hl: Mreal/Nreal outside Mp/Np");
     if (!W || !cst || ldw < Kp || ldw % 16 || !aligned16(W)) return fail(VGEMM_ERR_ARG, "gemm_hl: W must be 16-byte aligned with ldw >= Kp, ldw %% 16 == 0");
     if (E->epi < 0 || E->epi > VGEMM_EPI_QKV) return fail(VGEMM_ERR_ARG, "gemm_hl: unknown epilogue %d", E->epi);
-    if (E->epi != VGEMM_EPI_QKV && !E->Y && !E->vhi) return fail(VGEMM_ERR_ARG, "gemm_hl: null Y");
+    if (E->epi != VGEMM_EPI_QKV && !E->Y && !V) return fail(VGEMM_ERR_ARG, "gemm_hl: null Y");
     // GroupNorm statistics (src/gemm_hl.h:22, src/engine.h:110): EPI_PLAIN, 32 groups of whole
     // columns, a block's rows in at most two samples
     if (E->gnstat && (Nreal % 32 || E->gnT <= 0 || E->gnT % 64))
@@ -473,7 +474,7 @@ int hl2_impl(void* stream, const VgemmASrc* A, int Mp, int Mreal, const int8_t* 
 
     const int epi = E->epi;
     p.Y = E->Y; p.ldy = E->ldy; p.R = E->residual; p.Lphi = E->Lphi; p.rowmax = E->rowmax;
-    if (E->vhi) return view_impl(A, E, p, Mreal, Nreal, wsp, static_cast<hipStream_t>(stream));
+    if (V) return view_impl(A, E, V, p, Mreal, Nreal, wsp, static_cast<hipStream_t>(stream));
     p.Cs = E->Cs; p.Y1 = E->Y1; p.Y2 = E->Y2;
     p.gnstat = static_cast<vk::GnStat*>(E->gnstat); p.gnT = E->gnT;
     p.heads = E->heads; p.qT = E->T; p.TpQ = E->TpQ; p.TpK = E->TpK; p.qC = E->C;
@@ -630,6 +631,12 @@ extern "C" {
 int vgemm_hl2(void* stream, const VgemmASrc* A, int Mp, int Mreal, const int8_t* W, int ldw, int Np, int Nreal, int Kp,
               const int32_t* cst, const VgemmAEpi* E) {
     return hl2_impl(stream, A, Mp, Mreal, W, ldw, Np, Nreal, Kp, cst, E, WsPolicy{E ? E->ws : nullptr, E ? E->ws_bytes : 0, false});
+}
+
+int vgemm_hl2_view(void* stream, const VgemmASrc* A, int Mp, int Mreal, const int8_t* W, int ldw, int Np, int Nreal, int Kp,
+                   const int32_t* cst, const VgemmAEpi* E, const VgemmView* V) {
+    if (!V) return fail(VGEMM_ERR_ARG, "gemm_hl int16 view: null view");
+    return hl2_impl(stream, A, Mp, Mreal, W, ldw, Np, Nreal, Kp, cst, E, WsPolicy{E ? E->ws : nullptr, E ? E->ws_bytes : 0, false}, V);
 }
 
 int vgemm_hl2_noalloc(void* stream, const VgemmASrc* A, int Mp, int Mreal, const int8_t* W, int ldw, int Np, int Nreal, int Kp,

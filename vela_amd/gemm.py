@@ -11,13 +11,13 @@ import ctypes
 
 import torch
 
-from ._lib import GNSTAT_BYTES, GNSTAT_OFFSETS, AEpi, ASrc, VgemmError, check, load
+from ._lib import GNSTAT_BYTES, GNSTAT_OFFSETS, AEpi, ASrc, VgemmError, View, check, load
 
 EPI_PLAIN, EPI_SPLIT3, EPI_GEGLU, EPI_GELU, EPI_QKV = 0, 1, 2, 3, 4
 SRC_I8, SRC_X32, SRC_CONV32, SRC_I16, SRC_CONV16 = 0, 1, 2, 3, 4
 
 __all__ = [
-    "ASrc", "AEpi", "VgemmError", "EPI_PLAIN", "EPI_SPLIT3", "EPI_GEGLU", "EPI_GELU", "EPI_QKV",
+    "ASrc", "AEpi", "View", "VgemmError", "k_gemm_hl2_view", "EPI_PLAIN", "EPI_SPLIT3", "EPI_GEGLU", "EPI_GELU", "EPI_QKV",
     "SRC_I8", "SRC_X32", "SRC_CONV32", "SRC_I16", "SRC_CONV16", "k_gemm_hl2", "k_gemm_hl", "k_conv_e",
     "gemm_hl_supported", "set_variant", "get_variant", "set_splitk", "set_tile_order", "conv16_halo_rows", "workspace_bytes", "view_workspace_bytes", "Gemm",
     "k_quant_rows", "k_epilogue", "k_pixmax", "k_im2col3", "k_epilogue_split", "k_epilogue_geglu_q",
@@ -52,6 +52,15 @@ def k_gemm_hl2(A: ASrc, Mp: int, Mreal: int, W, ldw: int, Np: int, Nreal: int, K
 
 
 NOALLOC_WS_BYTES = 64 << 20
+
+
+def k_gemm_hl2_view(A: ASrc, Mp: int, Mreal: int, W, ldw: int, Np: int, Nreal: int, Kp: int, cst, E: AEpi, hi, lo, e, ld: int,
+                    stream=None) -> None:
+    """vgemm_hl2_view: the int16 view of the output (planes hi/lo [Mreal x ld], e per row) instead of Y;
+    E.ws must hold view_workspace_bytes()."""
+    V = View(hi=ptr(hi), lo=ptr(lo), e=ptr(e), ld=ld)
+    check(load().vgemm_hl2_view(stream_ptr(stream), ctypes.byref(A), Mp, Mreal, ptr(W), ldw, Np, Nreal, Kp, ptr(cst), ctypes.byref(E),
+                                ctypes.byref(V)))
 
 
 def k_gemm_hl2_noalloc(A: ASrc, Mp: int, Mreal: int, W, ldw: int, Np: int, Nreal: int, Kp: int, cst, E: AEpi, stream=None) -> None:
@@ -108,7 +117,7 @@ def workspace_bytes(Mp: int, Mreal: int, Np: int, Nreal: int, Kp: int, epi: int 
 
 
 def view_workspace_bytes(Mreal: int, Nreal: int, epi: int = EPI_PLAIN) -> int:
-    """Workspace bytes of the int16 view (AEpi.vhi/vlo/ve) for an Mreal x Nreal call."""
+    """Workspace bytes of the int16 view (k_gemm_hl2_view) for an Mreal x Nreal call."""
     return int(load().vgemm_view_workspace_bytes(Mreal, Nreal, epi))
 
 
