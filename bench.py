@@ -340,7 +340,7 @@ def dropin_sources(stream, steps, warmup):
     planes = torch.empty((2, L.Mp, L.Kp), dtype=torch.int8, device=dev)
     C = torch.empty((2 * L.Mp, L.Np), dtype=torch.int32, device=dev)
     ge = vg.Gemm()
-    ge.init(0)
+    ge.init(32 << 20)   # the reference engine's Gemm::init(cfg.gemmWorkspace), 32 MiB (src/engine.h:56)
     run = lambda: ge.run(planes, L.Kp, 0, w, L.Kp, 0, C, L.Np, 0, 2 * L.Mp, L.Np, L.Kp, stream=stream)   # noqa: E731
 
     def planar_route():

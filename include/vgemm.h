@@ -180,7 +180,11 @@ size_t vgemm_workspace_bytes(int Mp, int Mreal, int Np, int Nreal, int Kp, int e
 
 /* meow::Gemm (src/gemm.h:12-23, src/gemm.cu:7-70): C[M,N] = A[M,K] * W[N,K]^T, int8 x int8 -> int32,
  * row-major, optional strided batch. K % 16 == 0, N % 4 == 0, 16-byte aligned pointers.
- * The handle replaces the cuBLASLt plan cache; this library keeps no plans and needs no workspace. */
+ * The handle replaces the cuBLASLt plan cache (this library keeps no plans). vgemm_i8_create allocates
+ * ws_bytes of device memory on the current device, as the reference's Gemm::init allocates cuBLASLt's
+ * workspace (src/gemm.cu:7-11): a call with batch 1, deep K (>= 2048) and fewer output tiles than
+ * CUs splits K into it and sums the ranges in a second kernel. Calls on one handle share that
+ * workspace and must not overlap; 0 bytes disables the split. */
 int vgemm_i8_create(size_t ws_bytes, void** handle);
 int vgemm_i8_destroy(void* handle);
 int vgemm_i8_run(void* handle, void* stream, const int8_t* A, int lda, long long strideA, const int8_t* W, int ldw,

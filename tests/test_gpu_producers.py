@@ -165,6 +165,37 @@ def test_i8gemm(gpu, variant, M, N, K, batch):
         vg.set_variant(-1)
 
 
+@pytest.mark.parametrize("M,N,K,ws,splits", [
+    (1024, 1280, 11520, 32 << 20, 0),    # the 512-row C4 conv's stacked planes: split by the handle's workspace
+    (300, 200, 4096, 32 << 20, 0),       # partial tiles in both dimensions
+    (300, 200, 4096, 256 << 10, 0),      # a workspace too small for two K ranges: unsplit
+    (256, 256, 2048, 32 << 20, 5),       # forced splits (uneven K ranges)
+    (1024, 1280, 11520, 0, 0),           # no workspace: unsplit
+])
+def test_i8gemm_split_k(gpu, M, N, K, ws, splits):
+    """Gemm::run on deep K with few tiles splits K into the handle's workspace (the reference's
+    Gemm::init allocates it, src/gemm.cu:7-11) and sums the ranges: the same int32 C, rows and
+    columns beyond M and N untouched (ldc > N)."""
+    vg.set_splitk(splits)
+    try:
+        r = np.random.default_rng(M + N + K + splits)
+        lda, ldw, ldc = K, K, N + 8
+        A = r.integers(-128, 128, M * lda).astype(np.int8)
+        W = r.integers(-128, 128, N * ldw).astype(np.int8)
+        want = oracle.i8gemm(A, W, M, N, K, 1, 0, 0, 0, lda, ldw, ldc).reshape(M, ldc)
+        C = torch.full((M + 2, ldc), 0x5A5A5A5A, dtype=torch.int32, device="cuda")
+        g = vg.Gemm()
+        g.init(ws)
+        for _ in range(2):   # the workspace holds the last call's partials: a repeat gives the same C
+            g.run(dev(A), lda, 0, dev(W), ldw, 0, C, ldc, 0, M, N, K, 1)
+        torch.cuda.synchronize()
+        got = to_np(C)
+        assert_equal(got[:M, :N], want[:, :N], f"split-K Gemm::run {M}x{N}x{K} ws {ws} splits {splits}")
+        assert (got[:M, N:] == 0x5A5A5A5A).all() and (got[M:] == 0x5A5A5A5A).all(), "writes outside C"
+    finally:
+        vg.set_splitk(0)
+
+
 @pytest.mark.parametrize("order", [0, 1])
 @pytest.mark.parametrize("M,N,K,batch", [(257, 100, 320, 1), (77, 96, 64, 3), (192, 1280, 1024, 2)])
 def test_i8gemm_tile_orders(gpu, order, M, N, K, batch):

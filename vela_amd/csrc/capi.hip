@@ -22,6 +22,7 @@ hipError_t launch_gemm_conv16(int variant, int epi, const GemmParams& p, int bat
 int conv_halo_bm(int epi, int H, int W, int C, int stride, int Ho, int Wo);
 hipError_t launch_gemm_conv16_halo(int bm, int epi, const GemmParams& p, hipStream_t st);
 hipError_t launch_gemm_raw(int variant, const GemmParams& p, int batch, hipStream_t st);
+hipError_t launch_raw_reduce(const int32_t* ws, int splits, long long plane, int ldw, int M, int N, int32_t* C, int ldc, hipStream_t st);
 hipError_t launch_stripe(int src, int epi, const GemmParams& p, hipStream_t st);
 hipError_t launch_kwave(int src, int epi, const GemmParams& p, hipStream_t st);
 hipError_t launch_stripe_view(int src, int epi, const GemmParams& p, hipStream_t st);
@@ -205,6 +206,18 @@ int pick_variant(int M, int N, int Kp) {
     const long long tiles1 = (long long)cdiv(M, TILES[1].BM) * cdiv(N, TILES[1].BN);
     if (N >= 960 && Kp <= 1280 && tiles1 > 3LL * NCU) return 0;
     return 1;
+}
+
+// Tile of the single-plane int8 GEMM (Gemm::run). It has half the MFMA work per K step of the fused
+// two-plane kernel, so deep K wants the 128 x 128 tiles while they give every CU a block, else the
+// 128 x 64 ones (one MI355X, 200 launches each: the stacked planes of C3 [16384 x 5760] x 640 112.6 ->
+// 84.2 us, of the 2048-row C4 conv [4096 x 11520] x 1280 120.8 -> 79.6 us, of the 512-row one
+// [1024 x 11520] x 1280 69.1 -> 52.2 us, [4096 x 1280] x 1280 19.4 -> 17.0 us); shallow K keeps the
+// fused kernel's choice.
+int pick_variant_raw(int M, int N, int K) {
+    if (K < 1024) return pick_variant(M, N, K);
+    const long long tiles0 = (long long)cdiv(M, TILES[0].BM) * cdiv(N, TILES[0].BN);
+    return tiles0 >= NCU ? 0 : 2;
 }
 
 int pick_splitk(int variant, int M, int N, int Kp) {
@@ -665,16 +678,30 @@ int vgemm_conv_e(void* stream, const uint32_t* pm, int B, int H, int W, int stri
 }
 
 // ---- meow::Gemm replacement
-struct VgemmI8Handle { size_t ws; };
+// The handle owns the workspace its init asks for (the reference's Gemm::init allocates it for
+// cuBLASLt, src/gemm.cu:7-11): split-K partial sums of deep-K calls with few tiles. Calls on one
+// handle share it and must not overlap (as calls sharing a cuBLASLt workspace must not).
+struct VgemmI8Handle {
+    size_t ws_bytes;
+    void* ws;
+};
 
 int vgemm_i8_create(size_t ws_bytes, void** handle) {
     if (!handle) return fail(VGEMM_ERR_ARG, "i8gemm: null handle pointer");
-    *handle = new VgemmI8Handle{ws_bytes};
+    *handle = nullptr;
+    void* ws = nullptr;
+    if (ws_bytes) {
+        const hipError_t e = hipMalloc(&ws, ws_bytes);
+        if (e != hipSuccess) return fail(VGEMM_ERR_HIP, "i8gemm: workspace hipMalloc(%zu): %s", ws_bytes, hipGetErrorString(e));
+    }
+    *handle = new VgemmI8Handle{ws ? ws_bytes : 0, ws};
     return ok();
 }
 
 int vgemm_i8_destroy(void* handle) {
-    delete static_cast<VgemmI8Handle*>(handle);
+    VgemmI8Handle* h = static_cast<VgemmI8Handle*>(handle);
+    if (h && h->ws) (void)hipFree(h->ws);
+    delete h;
     return ok();
 }
 
@@ -697,13 +724,34 @@ int vgemm_i8_run(void* handle, void* stream, const int8_t* A, int lda, long long
     p.Y = C; p.ldy = ldc; p.vec_store = ldc % 4 == 0 ? 1 : 0;
     p.Mreal = M; p.Nreal = N; p.Kp = K; p.K = K;
     p.sA = strideA; p.sW = strideW; p.sC = strideC;
-    const int variant = g_variant >= 0 && g_variant < NVARIANT ? g_variant : pick_variant(M, N, K);
+    const int variant = g_variant >= 0 && g_variant < NVARIANT ? g_variant : pick_variant_raw(M, N, K);
     p.mtiles = cdiv(M, TILES[variant].BM);
     p.ntiles = cdiv(N, TILES[variant].BN);
-    p.ksplit = 1; p.kper = (K + 63) / 64;
-    p.colmajor = pick_tile_order(p, double(M) * K);
+    const int nK = (K + 63) / 64;
+    p.ksplit = 1; p.kper = nK;
     p.stride = 1;
-    return hip_status(vk::launch_gemm_raw(variant, p, batch, static_cast<hipStream_t>(stream)), "i8gemm launch");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    // deep K over fewer tiles than CUs: split K into the handle's workspace, then sum the ranges
+    const VgemmI8Handle* h = static_cast<const VgemmI8Handle*>(handle);
+    const long long tiles = (long long)p.mtiles * p.ntiles;
+    if (batch == 1 && h->ws && tiles < NCU && nK >= 32 && ldc % 4 == 0 && g_splitk != 1) {
+        const long long rows = (long long)p.mtiles * TILES[variant].BM, cols = (long long)p.ntiles * TILES[variant].BN;
+        const long long plane = rows * cols * 4;
+        long long s = g_splitk > 1 ? g_splitk : std::min<long long>(2LL * NCU / tiles, nK / 16);
+        s = std::min<long long>(s, (long long)(h->ws_bytes / size_t(plane)));
+        if (s * plane > MAX_EXTENT) s = MAX_EXTENT / plane;
+        if (s >= 2) {
+            p.kper = (nK + int(s) - 1) / int(s);
+            p.ksplit = (nK + p.kper - 1) / p.kper;
+            p.Y = static_cast<int32_t*>(h->ws); p.ldy = int(cols); p.sC = rows * cols; p.vec_store = 1;
+            p.colmajor = pick_tile_order(p, double(M) * K);
+            if (int rc = hip_status(vk::launch_gemm_raw(variant, p, 1, st), "i8gemm split launch")) return rc;
+            return hip_status(vk::launch_raw_reduce(static_cast<const int32_t*>(h->ws), p.ksplit, plane, int(cols), M, N, C, ldc, st),
+                              "i8gemm split reduce");
+        }
+    }
+    p.colmajor = pick_tile_order(p, double(M) * K);
+    return hip_status(vk::launch_gemm_raw(variant, p, batch, st), "i8gemm launch");
 }
 
 // ---- producers

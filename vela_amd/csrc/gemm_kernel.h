@@ -1212,7 +1212,8 @@ __global__ void __launch_bounds__(T::NT, (dma_waves_per_simd<T, EPI>())) gemm_dm
     if constexpr (EPI == EPI_PARTIAL) {
         store_partial<T>(p, acc_h, acc_l, rbase, n0 + wn * T::WTN, ti.ks);
     } else if constexpr (EPI == EPI_RAW) {
-        store_raw<T>(p, acc_h, rbase, n0 + wn * T::WTN, bt);
+        // split K: each K range's sums go to its own plane of the workspace (p.Y, stride p.sC)
+        store_raw<T>(p, acc_h, rbase, n0 + wn * T::WTN, p.ksplit > 1 ? ti.ks : bt);
     } else if constexpr (EPI == EPI_QKV) {
         qkv_epilogue<T>(p, acc_h, acc_l, rbase, n0, wn, er);
     } else {
@@ -1573,6 +1574,7 @@ hipError_t launch_gemm_conv32(int variant, int epi, const GemmParams& p, int bat
 hipError_t launch_gemm_i16(int variant, int epi, const GemmParams& p, int batch, hipStream_t st);
 hipError_t launch_gemm_conv16(int variant, int epi, const GemmParams& p, int batch, hipStream_t st);
 hipError_t launch_gemm_raw(int variant, const GemmParams& p, int batch, hipStream_t st);
+hipError_t launch_raw_reduce(const int32_t* ws, int splits, long long plane, int ldw, int M, int N, int32_t* C, int ldc, hipStream_t st);
 hipError_t launch_splitk_epilogue(int epi, const GemmParams& p, hipStream_t st);
 
 }  // namespace vk
