@@ -269,7 +269,8 @@ def dropin_sources(stream, steps, warmup):
       * Gemm::run on the stacked [hi; lo] planes [2M x K] (the cuBLASLt route, :271-277), C3 shape,
         alone and as im2col3 + Gemm::run + k_epilogue;
       * the C4 512-row convolution through AEpi without a split-K workspace (what a caller of the
-        reference's AEpi, which has none, runs)."""
+        reference's AEpi, which has none, runs), and through the route the reference engine itself
+        takes for that Kp (im2col3 + Gemm::run + k_epilogue)."""
     import torch
 
     from vela_amd import configs as cf
@@ -352,13 +353,34 @@ def dropin_sources(stream, steps, warmup):
     us, us_all = t_us(run), t_us(planar_route)
     out["Gemm::run planar [2x8192 x 5760] x [640 x 5760]^T (C3 via im2col3)"] = {
         "us": us, "tops": round(L.ops / (us * 1e-6) / 1e12, 1), "us_im2col3_run_epilogue": us_all}
-    del img, pm, e, y, planes, C, ge
+    del img, pm, e, y, planes, C
     # C4 512-row conv through AEpi without a workspace
     L = cf.c4()[1]
     p = cf.DeviceProblem(L, with_ws=False)
     p.reset()
     us = t_us(lambda: p.run(stream=stream))
-    out["C4 conv3x3 [8,8,8,1280]->1280, AEpi without workspace"] = {"us": us, "tops": round(L.ops / (us * 1e-6) / 1e12, 1)}
+    # ... and through the route the reference engine takes for it (Kp 11520 > customGemmMaxK 1536,
+    # src/engine.cu:176,279-288): k_pixmax, k_im2col3 of the int32 image, Gemm::run on the stacked
+    # planes with the engine's 32 MiB workspace, k_epilogue
+    img = rbits((L.B, L.H, L.W, L.C))
+    w, cst = wcst(L)
+    pm = torch.empty(L.B * L.H * L.W, dtype=torch.int32, device=dev)
+    e = torch.empty(L.Mp, dtype=torch.int32, device=dev)
+    y = torch.empty((L.M, L.N), dtype=torch.int32, device=dev)
+    planes = torch.empty((2, L.Mp, L.Kp), dtype=torch.int8, device=dev)
+    C = torch.empty((2 * L.Mp, L.Np), dtype=torch.int32, device=dev)
+
+    def engine_route():
+        vg.k_pixmax(img, L.B * L.H * L.W, L.C, pm, stream=stream)
+        vg.k_im2col3(img, pm, L.B, L.H, L.W, L.C, 1, planes[0], planes[1], e, L.Kp, stream=stream)
+        ge.run(planes, L.Kp, 0, w, L.Kp, 0, C, L.Np, 0, 2 * L.Mp, L.Np, L.Kp, stream=stream)
+        vg.k_epilogue(C[:L.Mp], C[L.Mp:], L.M, L.N, L.Np, cst, e, y, L.N, stream=stream)
+
+    us_route = t_us(engine_route)
+    out["C4 conv3x3 [8,8,8,1280]->1280, AEpi without workspace"] = {
+        "us": us, "tops": round(L.ops / (us * 1e-6) / 1e12, 1),
+        "us_engine_route_pixmax_im2col3_run_epilogue": us_route}
+    del img, pm, e, y, planes, C, ge
     return out
 
 
