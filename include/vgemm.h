@@ -147,8 +147,14 @@ int vgemm_get_variant(void);
  * epilogue. No counterpart in the reference; for tests and tuning. */
 int vgemm_conv16_halo_rows(int H, int W, int C, int stride, int epi);
 
-/* Split-K: force the number of K partitions for calls that pass a workspace (0 = automatic). */
+/* Split-K: force the number of K partitions (0 = automatic, 1 = never). */
 void vgemm_set_splitk(int s);
+/* No counterpart in the reference. A vgemm_hl2 call without AEpi.ws whose shape wants a K split
+ * (deep K over fewer tiles than CUs) uses a workspace the library allocates for its (device, stream)
+ * on the first such call outside stream capture, keeps until the process ends and enlarges (after
+ * synchronising that stream) when a later call needs more; under capture with none yet it runs
+ * unsplit. on = 0 turns this off (every call without AEpi.ws then runs unsplit); default on. */
+void vgemm_set_stream_workspaces(int on);
 /* Tile order over the XCDs: -1 automatic, 0 row stripes per XCD, 1 column groups per XCD. The order
  * changes which blocks share an L2, never a result bit. No counterpart in the reference (its tile
  * raster is CUDA's block order); a tuning and test knob like vgemm_set_splitk. */

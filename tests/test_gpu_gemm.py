@@ -412,6 +412,48 @@ def test_unread_fields_are_ignored(epi, fields, variant):
     assert (to_np(sentinel) == 0x3C3C3C3C).all(), f"epi {epi}: a buffer of an unread field was written"
 
 
+def test_stream_workspace_split():
+    """A call without AEpi.ws whose shape wants a K split (deep K, few tiles) splits K in its stream's
+    workspace: the same bytes as with a caller's workspace, with the stream workspaces off, captured
+    into a graph on a fresh stream before any eager call (no workspace yet: unsplit inside the graph)
+    and after one (the workspace exists: split inside the graph), every replay checked."""
+    c = Case(vg.SRC_I16, 256, 256, 8192, seed=61, residual=True, s_range=(22, 30))
+    want, _ = c.reference()
+    assert vg.workspace_bytes(c.Mp, c.M, c.Np, c.N, c.Kp, c.epi) > 0, "the shape must want a split"
+    got, _ = c.run_gpu()                       # no ws: the current stream's workspace
+    assert_equal(got, want, "stream workspace")
+    vg.set_stream_workspaces(False)
+    try:
+        got, _ = c.run_gpu()
+        assert_equal(got, want, "stream workspaces off")
+    finally:
+        vg.set_stream_workspaces(True)
+    keep = {}
+    A = c.asrc(keep)
+    w, cst, lut = dev(c.w), dev(c.cst), dev(c.lut)
+    for eager_first in (False, True):
+        s = torch.cuda.Stream()
+        Y = dev(c.res)
+        E = vg.AEpi(epi=c.epi, Lphi=vg.ptr(lut), Y=vg.ptr(Y), ldy=c.nout, residual=vg.ptr(Y))
+        if eager_first:
+            Y.copy_(dev(c.res))
+            vg.k_gemm_hl2(A, c.Mp, c.M, w, c.Kp, c.Np, c.N, c.Kp, cst, E, stream=s)
+            s.synchronize()
+            assert_equal(to_np(Y), want, "eager on the fresh stream")
+        g = vg.Graph(s)
+        torch.cuda.synchronize()
+        g.begin()
+        vg.k_gemm_hl2(A, c.Mp, c.M, w, c.Kp, c.Np, c.N, c.Kp, cst, E, stream=s)
+        g.end()
+        for rep in range(3):
+            Y.copy_(dev(c.res))   # the residual aliases Y: re-seed before each replay
+            torch.cuda.synchronize()
+            g.replay()
+            s.synchronize()
+            assert_equal(to_np(Y), want, f"graph replay {rep} (eager first: {eager_first})")
+        g.destroy()
+
+
 def test_k_gemm_hl_wrapper():
     """meow::k_gemm_hl: the SRC_I8 convenience entry point with default arguments."""
     c = Case(vg.SRC_I8, 130, 64, 96, seed=18, e_max=4)

@@ -171,6 +171,7 @@ SIGNATURES = [
     ("vgemm_add", I, [P, P, P, SZ]),
     ("vgemm_concat", I, [P, P, I, P, I, I, P, P, I]),
     ("vgemm_upsample2", I, [P, P, I, I, I, I, P]),
+    ("vgemm_set_stream_workspaces", None, [I]),
     ("vgemm_engine_create", I, [P, SZ, I, ctypes.POINTER(P)]),
     ("vgemm_engine_destroy", None, [P]),
     ("vgemm_engine_arena_peak", SZ, [P]),

@@ -6,6 +6,7 @@
 #include <algorithm>
 #include <atomic>
 #include <cstring>
+#include <map>
 #include <mutex>
 #include <string>
 
@@ -62,6 +63,7 @@ namespace {
 thread_local std::string g_err;
 int g_variant = -1;   // meow::g_gemm_hl_variant: process-wide, written by tests only
 int g_splitk = 0;
+std::atomic<bool> g_sws_on{true};   // split-K workspaces of calls that bring none (stream_workspace)
 int g_tile_order = -1;
 
 __attribute__((format(printf, 2, 3))) int fail(int code, const char* fmt, ...) {
@@ -327,6 +329,7 @@ int vgemm_supported(int Mp, int Np, int Kp) { return Mp > 0 && Np > 0 && Kp > 0 
 void vgemm_set_variant(int v) { g_variant = v; }
 int vgemm_get_variant(void) { return g_variant; }
 void vgemm_set_splitk(int s) { g_splitk = s < 0 ? 0 : s; }
+void vgemm_set_stream_workspaces(int on) { g_sws_on.store(on != 0, std::memory_order_relaxed); }
 void vgemm_set_tile_order(int order) { g_tile_order = order < 0 ? -1 : (order ? 1 : 0); }
 
 int vgemm_conv16_halo_rows(int H, int W, int C, int stride, int epi) {
@@ -353,13 +356,58 @@ size_t vgemm_workspace_bytes(int Mp, int Mreal, int Np, int Nreal, int Kp, int e
 namespace {
 
 // Where the split-K partials of a call go: the caller's workspace (AEpi.ws; a call whose split would
-// not fit runs unsplit), or the library's static scratch (the call is rejected if its split would
-// not fit).
+// not fit runs unsplit), the library's static scratch (vgemm_hl2_noalloc: the call is rejected if its
+// split would not fit), or, for a call that brings none, its stream's workspace (below).
 struct WsPolicy {
     void* ws;
     size_t bytes;
     bool strict;
 };
+
+// Split-K workspaces of calls that bring none. The reference's AEpi has no workspace, so its callers
+// never pass one; such a call whose shape wants a K split (deep K over fewer tiles than CUs) takes a
+// workspace that the library allocates for its (device, stream) on the first such call made outside
+// stream capture (the reference engine runs its forward eagerly once before it captures it), keeps
+// until the process ends, and replaces by a larger one (after synchronising that stream) when a later
+// call needs more. Calls on one stream run in order, so they never use it at the same time; calls on
+// other streams have their own. Under capture with no workspace yet, or with the workspaces turned
+// off (vgemm_set_stream_workspaces(0)), the call runs unsplit.
+struct StreamWs {
+    void* p = nullptr;
+    size_t bytes = 0;
+};
+std::mutex g_sws_mu;
+std::map<std::pair<int, uintptr_t>, StreamWs> g_sws;
+
+void* stream_workspace(hipStream_t st, size_t need, size_t* bytes) {
+    if (!g_sws_on.load(std::memory_order_relaxed)) return nullptr;
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+    std::lock_guard<std::mutex> lock(g_sws_mu);
+    StreamWs& w = g_sws[{dev, reinterpret_cast<uintptr_t>(st)}];
+    if (w.p && w.bytes >= need) {
+        *bytes = w.bytes;
+        return w.p;
+    }
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return nullptr;
+    if (w.p) {
+        if (hipStreamSynchronize(st) != hipSuccess) return nullptr;
+        (void)hipFree(w.p);
+        w.p = nullptr;
+        w.bytes = 0;
+    }
+    const size_t grain = size_t(4) << 20;
+    const size_t sz = (need + grain - 1) / grain * grain;
+    if (hipMalloc(&w.p, sz) != hipSuccess) {
+        (void)hipGetLastError();
+        w.p = nullptr;
+        return nullptr;
+    }
+    w.bytes = sz;
+    *bytes = sz;
+    return w.p;
+}
 
 // The int16 view of the output (vgemm_hl2_view): the row-stationary kernel writes each chunk at its
 // running row exponent with correction bits and row maxima in the workspace, then the fix-up pass
@@ -536,7 +584,7 @@ int hl2_impl(void* stream, const VgemmASrc* A, int Mp, int Mreal, const int8_t* 
         // the chip: the tile kernel (measured: 2048 x 5760 x 1280, C = 640 at 16 x 16, 72 -> 54 us)
         const int hv = halo_bm == 128 ? 0 : 1;
         const long long htiles = (long long)cdiv(Mreal, TILES[hv].BM) * cdiv(Nreal, TILES[hv].BN);
-        const int hsplits = wsp.ws && epi != VGEMM_EPI_QKV && !E->gnstat ? pick_splitk(hv, Mreal, Nreal, Kp) : 1;
+        const int hsplits = (wsp.ws || g_sws_on) && epi != VGEMM_EPI_QKV && !E->gnstat ? pick_splitk(hv, Mreal, Nreal, Kp) : 1;
         const long long tiles1 = (long long)cdiv(Mreal, TILES[1].BM) * cdiv(Nreal, TILES[1].BN);
         if (htiles * hsplits < NCU && tiles1 >= NCU) halo_bm = 0;
     }
@@ -561,7 +609,12 @@ int hl2_impl(void* stream, const VgemmASrc* A, int Mp, int Mreal, const int8_t* 
     p.ntiles = cdiv(Nreal, BN);
     const int nK = halo_bm ? p.C / 64 : (Kp + 63) / 64;
     // the split-K epilogue pass carries neither the QKV layout nor the GroupNorm statistics
-    int splits = wsp.ws && epi != VGEMM_EPI_QKV && !E->gnstat ? pick_splitk(variant, Mreal, Nreal, Kp) : 1;
+    int splits = epi != VGEMM_EPI_QKV && !E->gnstat ? pick_splitk(variant, Mreal, Nreal, Kp) : 1;
+    if (splits > 1 && !wsp.ws) {
+        size_t have = 0;
+        if (void* sw = stream_workspace(st, ws_bytes_for(variant, Mreal, Nreal, splits), &have)) wsp = WsPolicy{sw, have, false};
+    }
+    if (!wsp.ws) splits = 1;
     if (splits > 1 && ws_bytes_for(variant, Mreal, Nreal, splits) > wsp.bytes) {
         if (wsp.strict)
             return fail(VGEMM_ERR_UNSUPPORTED, "gemm_hl_noalloc: the split-K partials of this call need %zu bytes; the static workspace holds %zu",

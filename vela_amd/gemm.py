@@ -19,7 +19,7 @@ SRC_I8, SRC_X32, SRC_CONV32, SRC_I16, SRC_CONV16 = 0, 1, 2, 3, 4
 __all__ = [
     "ASrc", "AEpi", "View", "VgemmError", "k_gemm_hl2_view", "EPI_PLAIN", "EPI_SPLIT3", "EPI_GEGLU", "EPI_GELU", "EPI_QKV",
     "SRC_I8", "SRC_X32", "SRC_CONV32", "SRC_I16", "SRC_CONV16", "k_gemm_hl2", "k_gemm_hl", "k_conv_e",
-    "gemm_hl_supported", "set_variant", "get_variant", "set_splitk", "set_tile_order", "conv16_halo_rows", "workspace_bytes", "view_workspace_bytes", "Gemm",
+    "gemm_hl_supported", "set_variant", "get_variant", "set_splitk", "set_stream_workspaces", "set_tile_order", "conv16_halo_rows", "workspace_bytes", "view_workspace_bytes", "Gemm",
     "k_quant_rows", "k_epilogue", "k_pixmax", "k_im2col3", "k_epilogue_split", "k_epilogue_geglu_q",
     "fill_u32", "Graph", "ptr", "stream_ptr", "GNSTAT_BYTES", "gn_stats_alloc", "k_gn_init", "gn_stats_read",
 ]
@@ -52,6 +52,11 @@ def k_gemm_hl2(A: ASrc, Mp: int, Mreal: int, W, ldw: int, Np: int, Nreal: int, K
 
 
 NOALLOC_WS_BYTES = 64 << 20
+
+
+def set_stream_workspaces(on: bool) -> None:
+    """vgemm_set_stream_workspaces: split-K workspaces for calls without AEpi.ws (default on)."""
+    load().vgemm_set_stream_workspaces(1 if on else 0)
 
 
 def k_gemm_hl2_view(A: ASrc, Mp: int, Mreal: int, W, ldw: int, Np: int, Nreal: int, Kp: int, cst, E: AEpi, hi, lo, e, ld: int,
