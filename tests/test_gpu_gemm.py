@@ -412,6 +412,22 @@ def test_unread_fields_are_ignored(epi, fields, variant):
     assert (to_np(sentinel) == 0x3C3C3C3C).all(), f"epi {epi}: a buffer of an unread field was written"
 
 
+@pytest.mark.parametrize("variant", [-1, 0, 1])
+def test_x32_rowmax_understated(variant):
+    """SRC_X32 with row maxima below the rows' true maxima (a caller's stale maxima): the shift comes
+    from the given maximum and values beyond it saturate in quant16_32 exactly as the reference's
+    formula has them, INT_MAX and INT_MIN with e = 1 included."""
+    vg.set_variant(variant)
+    c = Case(vg.SRC_X32, 192, 128, 256, seed=71)
+    r = rng(72)
+    c.x[:, :8] = np.array([2**31 - 1, -(2**31), 2**31 - 2, -(2**31) + 1, 65535, -65536, 32767, -32768], np.int32)
+    c.xrm = r.integers(0, 1 << 18, c.M).astype(np.uint32)      # e from 0 to 4, far below the true maxima
+    c.xrm[:16] = 40000                                          # e = 1
+    c.xrm[16:32] = 0                                            # e = 0
+    c.kw = dict(x=c.x, xrowmax=c.xrm, K=c.K)
+    c.check(what=f"X32 understated rowmax v{variant}")
+
+
 def test_stream_workspace_split():
     """A call without AEpi.ws whose shape wants a K split (deep K, few tiles) splits K in its stream's
     workspace: the same bytes as with a caller's workspace, with the stream workspaces off, captured

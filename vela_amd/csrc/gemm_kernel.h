@@ -108,12 +108,23 @@ __device__ __forceinline__ void split16x16(const unsigned* d, v4i& h, v4i& l) {
     }
 }
 
+// quant16_32(v, e) for e in [0, 17] in four VALU instructions, from sh1 = max(e - 1, 0) and
+// c1 = (e > 0): the rounding shift as ((v >> (e - 1)) + 1) >> 1, which equals (v >> e) +
+// ((v >> (e - 1)) & 1) for e >= 1 because floor shifts compose (v >> e = (v >> (e - 1)) >> 1); the
+// add saturates, so that its one overflowing case (e = 1, v = INT_MAX) still clamps to 32767 as the
+// reference's form does; e = 0 leaves v as it is.
+__device__ __forceinline__ int quant16_sh(int v, int sh1, int c1) {
+    const int t = __builtin_elementwise_add_sat(v >> sh1, c1);
+    return min(max(t >> c1, -32767), 32767);
+}
+
 // 16 int32 values quantised with shift e (quant16_32), packed to int16 pairs
 __device__ __forceinline__ void quant_pack16(const v4i* x, int e, unsigned* d) {
+    const int sh1 = e > 0 ? e - 1 : 0, c1 = e > 0 ? 1 : 0;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-        const int q0 = quant16_32(x[j >> 1][(2 * j) & 3], e);
-        const int q1 = quant16_32(x[j >> 1][(2 * j + 1) & 3], e);
+        const int q0 = quant16_sh(x[j >> 1][(2 * j) & 3], sh1, c1);
+        const int q1 = quant16_sh(x[j >> 1][(2 * j + 1) & 3], sh1, c1);
         d[j] = __builtin_amdgcn_perm(unsigned(q1), unsigned(q0), 0x05040100u);
     }
 }
@@ -142,11 +153,12 @@ __device__ __forceinline__ void clamp16_pairs(unsigned* d) {
 
 // the same with any shift e in [0, 17] (quant16_32)
 __device__ __forceinline__ void quant16_pairs(unsigned* d, int e) {
+    const int sh1 = e > 0 ? e - 1 : 0, c1 = e > 0 ? 1 : 0;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
         const int w = int(d[j]);
-        const int q0 = quant16_32(int(short(w & 0xffff)), e);
-        const int q1 = quant16_32(w >> 16, e);
+        const int q0 = quant16_sh(int(short(w & 0xffff)), sh1, c1);
+        const int q1 = quant16_sh(w >> 16, sh1, c1);
         d[j] = __builtin_amdgcn_perm(unsigned(q1), unsigned(q0), 0x05040100u);
     }
 }
