@@ -151,9 +151,11 @@ int vgemm_conv16_halo_rows(int H, int W, int C, int stride, int epi);
 void vgemm_set_splitk(int s);
 /* No counterpart in the reference. A vgemm_hl2 call without AEpi.ws whose shape wants a K split
  * (deep K over fewer tiles than CUs) uses a workspace the library allocates for its (device, stream)
- * on the first such call outside stream capture, keeps until the process ends and enlarges (after
- * synchronising that stream) when a later call needs more; under capture with none yet it runs
- * unsplit. on = 0 turns this off (every call without AEpi.ws then runs unsplit); default on. */
+ * on the first such call outside stream capture and keeps until the process ends (a later call that
+ * needs more gets a larger one; none is freed, as captured graphs may refer to them); under capture
+ * with none yet it runs unsplit. A graph captured with such calls uses its capture stream's
+ * workspace: replay it on that stream. on = 0 turns this off (every call without AEpi.ws then runs
+ * unsplit); default on. */
 void vgemm_set_stream_workspaces(int on);
 /* Tile order over the XCDs: -1 automatic, 0 row stripes per XCD, 1 column groups per XCD. The order
  * changes which blocks share an L2, never a result bit. No counterpart in the reference (its tile

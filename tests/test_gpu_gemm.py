@@ -432,10 +432,16 @@ def test_stream_workspace_split():
     """A call without AEpi.ws whose shape wants a K split (deep K, few tiles) splits K in its stream's
     workspace: the same bytes as with a caller's workspace, with the stream workspaces off, captured
     into a graph on a fresh stream before any eager call (no workspace yet: unsplit inside the graph)
-    and after one (the workspace exists: split inside the graph), every replay checked."""
+    and after one (the workspace exists: split inside the graph), every replay checked; replays
+    after a larger call on the same stream replaced the workspace still use the one they captured."""
     c = Case(vg.SRC_I16, 256, 256, 8192, seed=61, residual=True, s_range=(22, 30))
     want, _ = c.reference()
     assert vg.workspace_bytes(c.Mp, c.M, c.Np, c.N, c.Kp, c.epi) > 0, "the shape must want a split"
+    big = Case(vg.SRC_I16, 512, 1024, 8192, seed=62, s_range=(22, 30))
+    big_need = vg.workspace_bytes(big.Mp, big.M, big.Np, big.N, big.Kp, big.epi)
+    grain = 4 << 20
+    assert big_need > -(-vg.workspace_bytes(c.Mp, c.M, c.Np, c.N, c.Kp, c.epi) // grain) * grain, \
+        "the larger call must need a larger workspace"
     got, _ = c.run_gpu()                       # no ws: the current stream's workspace
     assert_equal(got, want, "stream workspace")
     vg.set_stream_workspaces(False)
@@ -467,6 +473,21 @@ def test_stream_workspace_split():
             g.replay()
             s.synchronize()
             assert_equal(to_np(Y), want, f"graph replay {rep} (eager first: {eager_first})")
+        if eager_first:
+            # a larger call on the same stream: a new workspace for it, the graph keeps the old one
+            bkeep = {}
+            bA = big.asrc(bkeep)
+            bw, bcst, blut = dev(big.w), dev(big.cst), dev(big.lut)
+            bY = torch.zeros((big.M, big.nout), dtype=torch.int32, device="cuda")
+            bE = vg.AEpi(epi=big.epi, Lphi=vg.ptr(blut), Y=vg.ptr(bY), ldy=big.nout)
+            vg.k_gemm_hl2(bA, big.Mp, big.M, bw, big.Kp, big.Np, big.N, big.Kp, bcst, bE, stream=s)
+            Y.copy_(dev(c.res))
+            torch.cuda.synchronize()
+            g.replay()
+            s.synchronize()
+            bwant, _ = big.reference()
+            assert_equal(to_np(bY), bwant, "the larger call")
+            assert_equal(to_np(Y), want, "graph replay after the workspace was replaced")
         g.destroy()
 
 

@@ -367,11 +367,13 @@ struct WsPolicy {
 // Split-K workspaces of calls that bring none. The reference's AEpi has no workspace, so its callers
 // never pass one; such a call whose shape wants a K split (deep K over fewer tiles than CUs) takes a
 // workspace that the library allocates for its (device, stream) on the first such call made outside
-// stream capture (the reference engine runs its forward eagerly once before it captures it), keeps
-// until the process ends, and replaces by a larger one (after synchronising that stream) when a later
-// call needs more. Calls on one stream run in order, so they never use it at the same time; calls on
-// other streams have their own. Under capture with no workspace yet, or with the workspaces turned
-// off (vgemm_set_stream_workspaces(0)), the call runs unsplit.
+// stream capture (the reference engine runs its forward eagerly once before it captures it). When a
+// later call needs more, a larger one replaces it for new calls; none is ever freed before the
+// process ends, since a graph captured earlier may still refer to it. Calls on one stream run in
+// order, so they never use it at the same time; calls on other streams have their own (a graph
+// captured with such calls uses its capture stream's workspace, so it is replayed on that stream, as
+// the reference replays its forward). Under capture with no workspace yet, or with the workspaces
+// turned off (vgemm_set_stream_workspaces(0)), the call runs unsplit.
 struct StreamWs {
     void* p = nullptr;
     size_t bytes = 0;
@@ -391,19 +393,14 @@ void* stream_workspace(hipStream_t st, size_t need, size_t* bytes) {
     }
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return nullptr;
-    if (w.p) {
-        if (hipStreamSynchronize(st) != hipSuccess) return nullptr;
-        (void)hipFree(w.p);
-        w.p = nullptr;
-        w.bytes = 0;
-    }
     const size_t grain = size_t(4) << 20;
     const size_t sz = (need + grain - 1) / grain * grain;
-    if (hipMalloc(&w.p, sz) != hipSuccess) {
+    void* np = nullptr;
+    if (hipMalloc(&np, sz) != hipSuccess) {
         (void)hipGetLastError();
-        w.p = nullptr;
         return nullptr;
     }
+    w.p = np;   // a smaller one it replaces stays allocated (graphs may refer to it)
     w.bytes = sz;
     *bytes = sz;
     return w.p;
