@@ -1,13 +1,15 @@
 """GPU parity of the row-stationary kernel (shallow K, many rows: the C2 GEGLU up-projection path)
 against the CPU oracle, byte for byte.
 
-The kernel is forced with variant 4 on shapes where it applies (int16 rows or int8 planes, Kp <= 320,
-output columns a multiple of four); shapes with a deeper K run the tile kernels under the same
-setting, which these cases then cover as well. Cases follow src/test_gemm_hl.cu:53-86 (random
-operands, e shifts, residual) and cover what is particular to this kernel: K not a multiple of 64,
-partial row stripes and W chunks, blocks that stream many chunks (large M) or one chunk (small M),
-and its two epilogue forms (the integer form, and the int64 formula for blocks with row shifts,
-shifts outside [0, 31], possible saturation or a table outside [0, 65536]).
+The kernel is forced with variant 4 (stripe_kernel.h, 32 rows per wave) and variant 6
+(stripe16_kernel.h, 16 rows per wave; calls with a residual stay on the former) on shapes where it
+applies (int16 rows or int8 planes, Kp <= 320, output columns a multiple of four); shapes with a
+deeper K run the tile kernels under the same setting, which these cases then cover as well. Cases
+follow src/test_gemm_hl.cu:53-86 (random operands, e shifts, residual) and cover what is particular
+to these kernels: K not a multiple of 64, partial row stripes and W chunks, blocks that stream many
+chunks (large M) or one chunk (small M), and the two epilogue forms (the integer form, and the
+int64 formula for blocks with row shifts, shifts outside [0, 31], possible saturation or a table
+outside [0, 65536]).
 """
 import numpy as np
 import pytest
@@ -17,12 +19,10 @@ from vela_amd import gemm as vg
 
 pytestmark = pytest.mark.gpu
 
-STRIPE = 4
 
-
-@pytest.fixture(autouse=True)
-def _stripe(gpu):
-    vg.set_variant(STRIPE)
+@pytest.fixture(autouse=True, params=[4, 6], ids=["stripe", "stripe16"])
+def _stripe(gpu, request):
+    vg.set_variant(request.param)
     vg.set_splitk(0)
     yield
     vg.set_variant(-1)
@@ -39,6 +39,17 @@ SHAPES = [(300, 200, 320), (257, 136, 64), (130, 96, 200), (200, 128, 328), (129
 def test_stripe_plain_residual(src, shape):
     M, N, K = shape
     Case(src, M, N, K, seed=60 + K % 97, residual=True, rowmax=True, s_range=(16, 24)).check(what=f"stripe {src} {shape}")
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+@pytest.mark.parametrize("src", [vg.SRC_I16, vg.SRC_I8])
+@pytest.mark.parametrize("epi", [vg.EPI_PLAIN, vg.EPI_GEGLU, vg.EPI_GELU])
+def test_stripe_no_residual(src, shape, epi):
+    """Calls without a residual (the ones both kernels serve), with and without the row maximum, in
+    the integer form and (e != 0 on odd M) the int64 form."""
+    M, N, K = shape
+    kw = dict(e_max=7) if M % 2 else dict(s_range=(16, 24))
+    Case(src, M, N, K, epi=epi, seed=100 + K % 83 + epi, rowmax=M % 3 != 0, **kw).check(what=f"stripe epi {epi} {src} {shape}")
 
 
 @pytest.mark.parametrize("shape", SHAPES)
@@ -65,6 +76,8 @@ def test_stripe_epilogues(epi, K):
     ]
     for i, (name, kw) in enumerate(forms):
         Case(vg.SRC_I16, 384, 256, K, epi=epi, seed=80 + i, rowmax=True, residual=epi == vg.EPI_PLAIN, **kw).check(what=f"{name} epi {epi} K {K}")
+        if epi == vg.EPI_PLAIN:
+            Case(vg.SRC_I16, 384, 256, K, epi=epi, seed=80 + i, rowmax=True, **kw).check(what=f"{name} epi {epi} K {K}, no residual")
 
 
 def test_stripe_lut_outside_range():

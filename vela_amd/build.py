@@ -34,7 +34,7 @@ HIP_FLAGS = [
 C_FLAGS = ["-O3", "-march=x86-64-v3", "-fPIC", "-fopenmp", "-Wall", "-Wextra", "-Wno-unused-parameter", "-std=gnu11"]
 
 HIP_SOURCES = ["gemm_src_i8.hip", "gemm_src_i16.hip", "gemm_src_x32.hip", "gemm_src_conv32.hip",
-               "gemm_src_conv16.hip", "gemm_stripe.hip", "gemm_kwave.hip", "gemm_raw.hip", "producers.hip", "elementwise.hip", "norms.hip", "attn.hip", "capi.hip", "model.cpp", "engine.cpp"]
+               "gemm_src_conv16.hip", "gemm_stripe.hip", "gemm_stripe16.hip", "gemm_kwave.hip", "gemm_raw.hip", "producers.hip", "elementwise.hip", "norms.hip", "attn.hip", "capi.hip", "model.cpp", "engine.cpp"]
 
 
 def _run(cmd: list[str]) -> None:

@@ -27,6 +27,7 @@ hipError_t launch_raw_reduce(const int32_t* ws, int splits, long long plane, int
 hipError_t launch_stripe(int src, int epi, const GemmParams& p, hipStream_t st);
 hipError_t launch_kwave(int src, int epi, const GemmParams& p, hipStream_t st);
 hipError_t launch_stripe_view(int src, int epi, const GemmParams& p, hipStream_t st);
+hipError_t launch_stripe16(int src, int epi, const GemmParams& p, hipStream_t st);
 hipError_t launch_view_fix(hipStream_t st, const uint32_t* vmax, const uint8_t* vexp, const uint32_t* vmask, int M, int F, int G, int8_t* hi,
                            int8_t* lo, int ld, int32_t* e);
 hipError_t launch_splitk_epilogue(int epi, const GemmParams& p, hipStream_t st);
@@ -123,6 +124,15 @@ constexpr int VARIANT_STRIPE = 4;
 // planes or int16 images with C % 64 == 0, epilogue PLAIN (with or without a residual) / SPLIT3 /
 // GEGLU / GELU, no GroupNorm statistics. 64 x 64 tiles, the four waves of a block splitting K.
 constexpr int VARIANT_KWAVE = 5;
+// Variant 6 forces the sixteen-rows-per-wave row-stationary kernel (stripe16_kernel.h) where the
+// row-stationary kernel applies without a residual; variant 4 forces stripe_kernel.h.
+constexpr int VARIANT_STRIPE16 = 6;
+// Automatic choice between the two: the table epilogues (GEGLU, GELU) on stripe16, whose four waves
+// per SIMD hide their per-output dependency chains better (C2 GEGLU 75.3 -> 73.2 us, 32768 x 320 x
+// 1280 GELU 46.6 -> 44.3 us, same box); PLAIN on stripe_kernel, whose 32-row waves read each W
+// fragment for twice the rows (16-row waves double the LDS reads: 32768 x 320 x 2560 PLAIN 78.9 ->
+// 83.8 us on stripe16).
+bool stripe16_auto(int epi) { return epi == VGEMM_EPI_GEGLU || epi == VGEMM_EPI_GELU; }
 constexpr int STRIPE_BM = 128, STRIPE_CH = 64;
 constexpr int STRIPE_NCOLS = 1280;   // W rows per block, at most
 
@@ -566,10 +576,13 @@ int hl2_impl(void* stream, const VgemmASrc* A, int Mp, int Mreal, const int8_t* 
     hipStream_t st = static_cast<hipStream_t>(stream);
 
     // shallow GEMMs with many rows: the row-stationary kernel (forced by variant 4 where it applies)
-    if (stripe_applies(A->src, epi, p) && !p.gnstat && (g_variant == VARIANT_STRIPE || (g_variant < 0 && stripe_auto(p)))) {
+    if (stripe_applies(A->src, epi, p) && !p.gnstat &&
+        (g_variant == VARIANT_STRIPE || g_variant == VARIANT_STRIPE16 || (g_variant < 0 && stripe_auto(p)))) {
         const int nout = epi == VGEMM_EPI_GEGLU ? Nreal / 2 : Nreal;
         p.y_bytes = unsigned(((long long)(Mreal - 1) * E->ldy + nout) * 4);
         stripe_grid(p);
+        const bool s16 = !p.R && (g_variant == VARIANT_STRIPE16 || (g_variant < 0 && stripe16_auto(epi)));
+        if (s16) return hip_status(vk::launch_stripe16(A->src, epi, p, st), "gemm_hl stripe launch");
         return hip_status(vk::launch_stripe(A->src, epi, p, st), "gemm_hl stripe launch");
     }
 

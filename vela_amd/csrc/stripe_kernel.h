@@ -82,6 +82,234 @@ constexpr unsigned STRIPE_LUT_RAW = 8192;
 
 enum { FORM_INT = 0, FORM_EXACT = 1 };
 
+// ---- block set-up shared by the row-stationary kernels (NT threads per block, at least BM)
+
+// column constants cst[n] of the block's chunks [cb, cb + ncols / CH): thread column j = tid + NT q.
+// Issued first, so that their latency passes under the row loads rather than in the set-up.
+template <int EPI, int NT>
+__device__ __forceinline__ void stripe_load_cols(const GemmParams& p, int tid, int cb, int ncols, v4i* craw) {
+    constexpr int CH = StripeCfg::CH, CPT = (StripeCfg::NCOLS + NT - 1) / NT;
+    const __amdgpu_buffer_rsrc_t rC = make_rsrc(p.cst, unsigned(p.Nreal) * 16u);
+#pragma unroll
+    for (int q = 0; q < CPT; ++q) {
+        const int j = tid + NT * q;
+        const int n = cb * CH + (j / CH) * CH + wrow_of_lds<EPI, CH>(j % CH);
+        craw[q] = bload16(rC, j < ncols && n < p.Nreal ? unsigned(n) * 16u : OOB);
+    }
+}
+
+// the row shift of row m0 + tid (0 without per-row shifts: a null buffer reads zeros)
+__device__ __forceinline__ int stripe_load_erow(const GemmParams& p, int tid, int m0) {
+    const __amdgpu_buffer_rsrc_t rE = make_rsrc(p.e, p.e ? unsigned(p.Mreal) * 4u : 0u);
+    const bool ok = tid < StripeCfg::BM && m0 + tid < p.Mreal;
+    return int(__builtin_amdgcn_raw_buffer_load_b32(rE, int(ok ? unsigned(m0 + tid) * 4u : OOB), 0, 0));
+}
+
+// DMA of the raw GELU table (entries 0..2047, 8 KB) into sh.lut + STRIPE_LUT_RAW by waves 0..3
+template <bool LUT>
+__device__ __forceinline__ void stripe_lut_dma(const GemmParams& p, StripeShared<LUT>& sh, int wave, int lane) {
+    const v4i rL = make_rsrc_words(p.Lphi, 2049u * 4u);
+    const unsigned lbase = lds_addr(sh.lut) + STRIPE_LUT_RAW;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const unsigned c = unsigned(wave * 2 + j) * 1024u;
+        dma16(rL, unsigned(lane) * 16u, c, lbase + c);
+    }
+}
+
+// Once the column constants, the raw table and the row shifts are in: the expanded GELU table, the
+// integer form's column table and the block's flags; returns the block's epilogue form (uniform).
+// Ends with a block-wide barrier after the tables are written.
+template <int EPI, int NT>
+__device__ __forceinline__ int stripe_setup(const GemmParams& p, StripeShared<EPI == EPI_GEGLU || EPI == EPI_GELU>& sh, int tid,
+                                            int m0, int cb, int ncols, const v4i* craw, int erv, int L2048) {
+    constexpr bool NEEDLUT = EPI == EPI_GEGLU || EPI == EPI_GELU;
+    constexpr int CH = StripeCfg::CH, BM = StripeCfg::BM, CPT = (StripeCfg::NCOLS + NT - 1) / NT;
+    constexpr int LPT = NEEDLUT ? (2050 + NT - 1) / NT : 1;
+    int2 lv[LPT];
+    int lbad = 0;
+    if constexpr (NEEDLUT) {
+        const int* raw = reinterpret_cast<const int*>(reinterpret_cast<const char*>(sh.lut) + STRIPE_LUT_RAW);
+#pragma unroll
+        for (int q = 0; q < LPT; ++q) {
+            const int i = tid + NT * q;
+            int2 v = make_int2(0, 0);
+            if (i == 2049) v = make_int2(65536 << 10, 0);
+            else if (i >= 1 && i < 2049) {
+                const int a = raw[i - 1], nx = i - 1 == 2047 ? L2048 : raw[i];
+                if (a < 0 || a > 65536 || nx < 0 || nx > 65536) lbad = 1;
+                // the entry's offset taken at x = 0 instead of at its first x, 1024 (i - 1025)
+                v = make_int2(int((unsigned(a) << 10) - unsigned(nx - a) * unsigned(1024 * (i - 1025))), nx - a);
+            }
+            lv[q] = v;
+        }
+    }
+    int4 cc[CPT];
+    int smn = INT_MAX, smx = INT_MIN, bad = 0, bmx = 0, wbad = 0;
+    double um = 0.0;
+#pragma unroll
+    for (int q = 0; q < CPT; ++q) {
+        const int j = tid + NT * q;
+        cc[q] = make_int4(0, 0, 0, 0);
+        if (j < ncols) {
+            const int n = cb * CH + (j / CH) * CH + wrow_of_lds<EPI, CH>(j % CH);
+            if (n < p.Nreal) {
+                const int4 c = make_int4(craw[q][0], craw[q][1], craw[q][2], craw[q][3]);
+                cc[q] = c;
+                const i64 mag = (c.x < 0 ? -i64(c.x) : i64(c.x)) * i64(p.Kp);
+                if (mag >= (1LL << 30) || c.y < -1000 || c.y > 1000) bad = 1;
+                // the bounds below take |acc| <= 2^22 Kp, which needs |wsum| <= 128 Kp
+                if (uabs(c.w) > 128u * unsigned(p.Kp)) wbad = 1;
+                smn = min(smn, c.y);
+                smx = max(smx, c.y);
+                // |acc m 2^-s| <= 2^22 Kp |m| 2^-s, since |acc| <= 32768 * 128 * Kp
+                if (c.y >= -1000 && c.y <= 1000) um = max(um, ldexp(4194304.0 * double(p.Kp) * fabs(double(c.x)), -c.y));
+                else um = 1e300;
+                bmx = max(bmx, int(min(uabs(c.z), 0x7fffffffu)));
+            }
+        }
+    }
+    int emn = INT_MAX, emx = INT_MIN;
+    if (tid < BM) {
+        const int er = erv;
+        sh.erow[tid] = er;
+        if (m0 + tid < p.Mreal) emn = emx = er;
+    }
+#pragma unroll
+    for (int o = 32; o; o >>= 1) {
+        emn = min(emn, __shfl_xor(emn, o));
+        emx = max(emx, __shfl_xor(emx, o));
+        smn = min(smn, __shfl_xor(smn, o));
+        smx = max(smx, __shfl_xor(smx, o));
+        bad |= __shfl_xor(bad, o);
+        wbad |= __shfl_xor(wbad, o);
+        bmx = max(bmx, __shfl_xor(bmx, o));
+        um = max(um, __shfl_xor(um, o));
+        if constexpr (NEEDLUT) lbad |= __shfl_xor(lbad, o);
+    }
+    if ((tid & 63) == 0) {
+        if (emn <= emx) { atomicMin(&sh.flag[0], emn); atomicMax(&sh.flag[1], emx); }
+        if (smn <= smx) { atomicMin(&sh.flag[2], smn); atomicMax(&sh.flag[3], smx); }
+        if (bad) atomicOr(&sh.flag[4], 1);
+        if (wbad) atomicOr(&sh.flag[7], 1);
+        if (lbad) atomicOr(&sh.flag[5], 1);
+        atomicMax(&sh.flag[6], bmx);
+        atomicMax(&sh.umax, __double_as_longlong(um));
+    }
+    __syncthreads();   // raw table read by everyone, all flags in
+    if constexpr (NEEDLUT) {
+#pragma unroll
+        for (int q = 0; q < LPT; ++q) {
+            const int i = tid + NT * q;
+            if (i < 2050) sh.lut[i] = lv[q];
+        }
+    }
+    const i64 emin = sh.flag[0], emax = sh.flag[1], smin = sh.flag[2], smax = sh.flag[3];
+    const bool lut_ok = !NEEDLUT || !sh.flag[5];
+    const bool ezero = emin > emax || (emin == 0 && emax == 0);
+    // no element saturates: |y| <= max 2^22 Kp |m| 2^-s + 1 + max |b| < 2^31
+    const bool nosat = __longlong_as_double(sh.umax) + double(sh.flag[6]) + 2.0 < 2147483647.0;
+    int form = ezero && smin >= 0 && smax <= 31 && nosat && lut_ok && !sh.flag[7] ? FORM_INT : FORM_EXACT;
+    form = __builtin_amdgcn_readfirstlane(form);
+#pragma unroll
+    for (int q = 0; q < CPT; ++q) {
+        const int j = tid + NT * q;
+        if (j < ncols) {
+            const int4 c = cc[q];
+            if (form == FORM_INT) {
+                // C = 128 wsum m + 2^(s-1) + b 2^s (|C| < 2^63: |wsum| <= 128 Kp, s <= 31)
+                const i64 C = 128LL * i64(c.w) * i64(c.x) + (c.y ? (1LL << (c.y - 1)) : 0) + i64(c.z) * (1LL << c.y);
+                sh.tab[j] = make_int4(c.x, c.y, int(unsigned(u64(C))), int(unsigned(u64(C) >> 32)));
+            }
+        }
+    }
+    __syncthreads();
+    return form;
+}
+
+// W chunk DMA of the row-stationary kernels: waves 0..3 fill a chunk (64 W rows x Kp) of the LDS
+// ring, five 1 KB instructions each. W rows of a K step sit in pairs in 128-byte LDS rows (pswz).
+// Instruction j of wave w fills K step ks = q / 4, LDS rows 8 rg .. 8 rg + 7 (rg = q % 4, the W rows
+// 16 rg .. 16 rg + 15) of a chunk, q = 5 w + j; lane l holds the 16-byte piece that swz16 puts at
+// position l % 8 of LDS row R = 8 rg + l / 8: piece pc = (l % 8) ^ (l / 8) ^ (rg % 2) (the swz16 key
+// of R), which is K chunk pc % 4 of W row 16 rg + x, x = 2 (l / 8) + pc / 4. So wrow(16 rg + x) =
+// wrow(x) + a constant of rg, and three per-lane values cover every instruction.
+template <int EPI>
+struct StripeDma {
+    static constexpr int RG = StripeCfg::CH / 16;
+    static_assert(RG == 4 && StripeCfg::DMA_INS * 4 == (StripeCfg::NKS / 2) * RG, "DMA mapping");
+    v4i rW;
+    int wb, wk0, wk1;
+    unsigned wlane;
+    __device__ __forceinline__ void init(const GemmParams& p, int lane) {
+        rW = make_rsrc_words(p.w, p.w_bytes);
+        const int pce = (lane & 7) ^ (lane >> 3);                 // piece, rg even
+        const int lx = 2 * (lane >> 3) + (pce >> 2);
+        wb = EPI == EPI_GEGLU ? 2 * lx : lx;                      // wrow(x)
+        wk0 = 16 * (pce & 3);                                     // K offset, rg even
+        wk1 = 16 * ((pce ^ 1) & 3);                               // K offset, rg odd
+        wlane = unsigned(wb) * unsigned(p.ldw);
+    }
+    // chunk c into ring stage `stage` (the instructions of wave `wave` < 4)
+    template <bool LUT>
+    __device__ __forceinline__ void issue(const GemmParams& p, StripeShared<LUT>& sh, int wave, int c, int stage) const {
+        constexpr int CH = StripeCfg::CH;
+        const int n0 = c * CH;
+        const unsigned sbase = lds_addr(sh.w[stage]);
+        const bool rows_in = n0 + CH <= p.Nreal;   // the whole chunk lies inside W (uniform)
+#pragma unroll
+        for (int j = 0; j < StripeCfg::DMA_INS; ++j) {
+            const int q = wave * StripeCfg::DMA_INS + j, ks = q / RG, rg = q - ks * RG;
+            // wrow(16 rg + l4) - wrow(l4): GEGLU rows 2 lr (lr < 32) and 2 (lr - 32) + 1
+            const int rgo = EPI == EPI_GEGLU ? (rg < 2 ? 32 * rg : 32 * (rg - 2) + 1) : 16 * rg;
+            const int wk = ks * 64 + ((rg & 1) ? wk1 : wk0);
+            unsigned off = wlane + unsigned(wk) + unsigned(rgo) * unsigned(p.ldw);
+            if (ks * 64 + 64 > p.Kp && wk >= p.Kp) off = OOB;
+            if (!rows_in && n0 + wb + rgo >= p.Nreal) off = OOB;
+            dma16(rW, off, unsigned(n0) * unsigned(p.ldw), sbase + unsigned(ks * StripeCfg::KSTEP + rg * 1024));
+        }
+    }
+};
+
+// ---- integer epilogue pieces shared by the row-stationary kernels
+
+// phi(x) for tables with 0 <= L <= 65536 (lut: the expanded table in LDS): x clamped to
+// [-2^20 - 1, 2^20], entry (x >> 10) + 1025, (1024 L[i] + d (x - 1024 (i - 1025))) >> 10 as one 24-bit
+// multiply-add mod 2^32: the exact value lies in [0, 2^26] and |d| <= 65536, |xc| <= 2^20 + 1 fit the
+// 24-bit operands
+__device__ __forceinline__ int stripe_phi(const int2* lut, int x) {
+    const int xc = min(max(x, -1048577), 1048576);
+    const int2 t = lut[(xc >> 10) + 1025];
+    return int(unsigned(t.x) + unsigned(__mul24(t.y, xc))) >> 10;
+}
+// (a b + 2^15) >> 16 as a 64-bit product: the high word and the 32-bit result
+__device__ __forceinline__ int stripe_mulsh16(int a, int b, unsigned& hi) {
+    const i64 t = i64(a) * i64(b) + 32768;
+    hi = unsigned(u64(t) >> 32);
+    return int(__builtin_amdgcn_alignbit(hi, unsigned(u64(t)), 16));
+}
+// the same with 2^47 added to the rounding constant: returns y ^ 2^31 (y biased to unsigned order)
+// and hi = (high word of a b + 2^15) + 2^15, which is <= 65535 exactly when y fits in int32
+__device__ __forceinline__ unsigned stripe_mulsh16b(int a, int b, unsigned& hi) {
+    const i64 t = i64(a) * i64(b) + (32768 + (1LL << 47));
+    hi = unsigned(u64(t) >> 32);
+    return __builtin_amdgcn_alignbit(hi, unsigned(u64(t)), 16);
+}
+// the integer requantisation (A m + C) >> s of an element with table entry k = {m, s, C lo, C hi},
+// exact when it fits in int32
+__device__ __forceinline__ int stripe_req(int A, const int4& k) {
+    const i64 t = i64(A) * i64(k.x) + i64((u64(unsigned(k.w)) << 32) | unsigned(k.z));
+    return int(__builtin_amdgcn_alignbit(unsigned(u64(t) >> 32), unsigned(u64(t)), unsigned(k.y)));
+}
+
+// flags of the block set-up, cleared by thread 0 before the set-up reads them
+template <bool LUT>
+__device__ __forceinline__ void stripe_clear_flags(StripeShared<LUT>& sh) {
+    sh.flag[0] = INT_MAX; sh.flag[1] = INT_MIN; sh.flag[2] = INT_MAX; sh.flag[3] = INT_MIN;
+    sh.flag[4] = 0; sh.flag[5] = 0; sh.flag[6] = 0; sh.flag[7] = 0;
+    sh.umax = 0;
+}
+
 // RES: the PLAIN instantiation for calls with a residual (its own kernel, so that the residual
 // loads do not shape the code of the others). VIEW: the int16-view instantiation (no Y; see the
 // view loop below).
@@ -120,75 +348,18 @@ __global__ void __launch_bounds__(256, 2) stripe_kernel(const GemmParams p) {
     const int nlim = GEGLU ? (p.Nreal >> 1) : p.Nreal;
     if (cb >= ce) return;   // (the host sizes the grid so that every block has a chunk)
 
-    if (tid == 0) {
-        sh.flag[0] = INT_MAX; sh.flag[1] = INT_MIN; sh.flag[2] = INT_MAX; sh.flag[3] = INT_MIN;
-        sh.flag[4] = 0; sh.flag[5] = 0; sh.flag[6] = 0; sh.flag[7] = 0;
-        sh.umax = 0;
-    }
+    if (tid == 0) stripe_clear_flags(sh);
 
-    // ---- the block's column constants (cst[n] for thread column j = tid + 256 q), loaded first so that
-    // their latency passes under the row loads below rather than in the block set-up
+    // ---- the block's column constants, the row shift of row m0 + tid, the GELU table (DMA)
     const int ncols = (ce - cb) * CH;
     v4i craw[S::CPT];
-    {
-        const __amdgpu_buffer_rsrc_t rC = make_rsrc(p.cst, unsigned(p.Nreal) * 16u);
-#pragma unroll
-        for (int q = 0; q < S::CPT; ++q) {
-            const int j = tid + 256 * q;
-            const int n = cb * CH + (j / CH) * CH + wrow_of_lds<EPI, CH>(j % CH);
-            craw[q] = bload16(rC, j < ncols && n < p.Nreal ? unsigned(n) * 16u : OOB);
-        }
-    }
-    // and the row shift of row m0 + tid (0 without per-row shifts: a null buffer reads zeros)
-    int erv;
-    {
-        const __amdgpu_buffer_rsrc_t rE = make_rsrc(p.e, p.e ? unsigned(p.Mreal) * 4u : 0u);
-        const bool ok = tid < BM && m0 + tid < p.Mreal;
-        erv = int(__builtin_amdgcn_raw_buffer_load_b32(rE, int(ok ? unsigned(m0 + tid) * 4u : OOB), 0, 0));
-    }
-
-    // ---- DMA: the GELU table (raw), then W chunk cb
-    if constexpr (NEEDLUT) {
-        const v4i rL = make_rsrc_words(p.Lphi, 2049u * 4u);
-        const unsigned lbase = lds_addr(sh.lut) + STRIPE_LUT_RAW;
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const unsigned c = unsigned(wave * 2 + j) * 1024u;
-            dma16(rL, unsigned(lane) * 16u, c, lbase + c);
-        }
-    }
+    stripe_load_cols<EPI, 256>(p, tid, cb, ncols, craw);
+    const int erv = stripe_load_erow(p, tid, m0);
+    if constexpr (NEEDLUT) stripe_lut_dma(p, sh, wave, lane);
     const int L2048 = NEEDLUT ? p.Lphi[2048] : 0;
-    const v4i rW = make_rsrc_words(p.w, p.w_bytes);
-    // W rows of a K step sit in pairs in 128-byte LDS rows (pswz). Instruction j of this wave fills K
-    // step ks = q / 4, LDS rows 8 rg .. 8 rg + 7 (rg = q % 4, the W rows 16 rg .. 16 rg + 15) of a
-    // chunk, q = 5 wave + j; lane l holds the 16-byte piece that swz16 puts at position l % 8 of LDS
-    // row R = 8 rg + l / 8: piece pc = (l % 8) ^ (l / 8) ^ (rg % 2) (the swz16 key of R), which is K
-    // chunk pc % 4 of W row 16 rg + x, x = 2 (l / 8) + pc / 4. So wrow(16 rg + x) = wrow(x) + a
-    // constant of rg, and three per-lane values cover every instruction.
-    constexpr int RG = CH / 16;
-    static_assert(RG == 4 && S::DMA_INS * 4 == (NKS / 2) * RG, "DMA mapping");
-    const int pce = (lane & 7) ^ (lane >> 3);                             // piece, rg even
-    const int lx = 2 * (lane >> 3) + (pce >> 2);
-    const int wb = GEGLU ? 2 * lx : lx;                                   // wrow(x)
-    const int wk0 = 16 * (pce & 3);                                       // K offset, rg even
-    const int wk1 = 16 * ((pce ^ 1) & 3);                                 // K offset, rg odd
-    const unsigned wlane = unsigned(wb) * unsigned(p.ldw);
-    auto issue = [&](int c, int stage) {
-        const int n0 = c * CH;
-        const unsigned sbase = lds_addr(sh.w[stage]);
-        const bool rows_in = n0 + CH <= p.Nreal;   // the whole chunk lies inside W (uniform)
-#pragma unroll
-        for (int j = 0; j < S::DMA_INS; ++j) {
-            const int q = wave * S::DMA_INS + j, ks = q / RG, rg = q - ks * RG;
-            // wrow(16 rg + l4) - wrow(l4): GEGLU rows 2 lr (lr < 32) and 2 (lr - 32) + 1
-            const int rgo = GEGLU ? (rg < 2 ? 32 * rg : 32 * (rg - 2) + 1) : 16 * rg;
-            const int wk = ks * 64 + ((rg & 1) ? wk1 : wk0);
-            unsigned off = wlane + unsigned(wk) + unsigned(rgo) * unsigned(p.ldw);
-            if (ks * 64 + 64 > p.Kp && wk >= p.Kp) off = OOB;
-            if (!rows_in && n0 + wb + rgo >= p.Nreal) off = OOB;
-            dma16(rW, off, unsigned(n0) * unsigned(p.ldw), sbase + unsigned(ks * S::KSTEP + rg * 1024));
-        }
-    };
+    StripeDma<EPI> dma;
+    dma.init(p, lane);
+    auto issue = [&](int c, int stage) { dma.issue(p, sh, wave, c, stage); };
     issue(cb, 0);
 
     // ---- the wave's activation rows (A operand: lane row lc, K bytes [32t + 16lh, +16) of substep t).
@@ -223,108 +394,7 @@ __global__ void __launch_bounds__(256, 2) stripe_kernel(const GemmParams p) {
     // ---- block set-up: column constants of chunks [cb, ce), the expanded GELU table, flags
     vm_wait<AL>();   // the column constants, the table and chunk cb's W (older than the row loads)
     block_barrier();
-    int form;
-    {
-        constexpr int LPT = NEEDLUT ? (2050 + 255) / 256 : 1;
-        int2 lv[LPT];
-        int lbad = 0;
-        if constexpr (NEEDLUT) {
-            const int* raw = reinterpret_cast<const int*>(reinterpret_cast<const char*>(sh.lut) + STRIPE_LUT_RAW);
-#pragma unroll
-            for (int q = 0; q < LPT; ++q) {
-                const int i = tid + 256 * q;
-                int2 v = make_int2(0, 0);
-                if (i == 2049) v = make_int2(65536 << 10, 0);
-                else if (i >= 1 && i < 2049) {
-                    const int a = raw[i - 1], nx = i - 1 == 2047 ? L2048 : raw[i];
-                    if (a < 0 || a > 65536 || nx < 0 || nx > 65536) lbad = 1;
-                    // the entry's offset taken at x = 0 instead of at its first x, 1024 (i - 1025)
-                    v = make_int2(int((unsigned(a) << 10) - unsigned(nx - a) * unsigned(1024 * (i - 1025))), nx - a);
-                }
-                lv[q] = v;
-            }
-        }
-        int4 cc[S::CPT];
-        int smn = INT_MAX, smx = INT_MIN, bad = 0, bmx = 0, wbad = 0;
-        double um = 0.0;
-#pragma unroll
-        for (int q = 0; q < S::CPT; ++q) {
-            const int j = tid + 256 * q;
-            cc[q] = make_int4(0, 0, 0, 0);
-            if (j < ncols) {
-                const int n = cb * CH + (j / CH) * CH + wrow_of_lds<EPI, CH>(j % CH);
-                if (n < p.Nreal) {
-                    const int4 c = make_int4(craw[q][0], craw[q][1], craw[q][2], craw[q][3]);
-                    cc[q] = c;
-                    const i64 mag = (c.x < 0 ? -i64(c.x) : i64(c.x)) * i64(p.Kp);
-                    if (mag >= (1LL << 30) || c.y < -1000 || c.y > 1000) bad = 1;
-                    // the bounds below take |acc| <= 2^22 Kp, which needs |wsum| <= 128 Kp
-                    if (uabs(c.w) > 128u * unsigned(p.Kp)) wbad = 1;
-                    smn = min(smn, c.y);
-                    smx = max(smx, c.y);
-                    // |acc m 2^-s| <= 2^22 Kp |m| 2^-s, since |acc| <= 32768 * 128 * Kp
-                    if (c.y >= -1000 && c.y <= 1000) um = max(um, ldexp(4194304.0 * double(p.Kp) * fabs(double(c.x)), -c.y));
-                    else um = 1e300;
-                    bmx = max(bmx, int(min(uabs(c.z), 0x7fffffffu)));
-                }
-            }
-        }
-        int emn = INT_MAX, emx = INT_MIN;
-        if (tid < BM) {
-            const int er = erv;
-            sh.erow[tid] = er;
-            if (m0 + tid < p.Mreal) emn = emx = er;
-        }
-#pragma unroll
-        for (int o = 32; o; o >>= 1) {
-            emn = min(emn, __shfl_xor(emn, o));
-            emx = max(emx, __shfl_xor(emx, o));
-            smn = min(smn, __shfl_xor(smn, o));
-            smx = max(smx, __shfl_xor(smx, o));
-            bad |= __shfl_xor(bad, o);
-            wbad |= __shfl_xor(wbad, o);
-            bmx = max(bmx, __shfl_xor(bmx, o));
-            um = max(um, __shfl_xor(um, o));
-            if constexpr (NEEDLUT) lbad |= __shfl_xor(lbad, o);
-        }
-        if (lane == 0) {
-            if (emn <= emx) { atomicMin(&sh.flag[0], emn); atomicMax(&sh.flag[1], emx); }
-            if (smn <= smx) { atomicMin(&sh.flag[2], smn); atomicMax(&sh.flag[3], smx); }
-            if (bad) atomicOr(&sh.flag[4], 1);
-            if (wbad) atomicOr(&sh.flag[7], 1);
-            if (lbad) atomicOr(&sh.flag[5], 1);
-            atomicMax(&sh.flag[6], bmx);
-            atomicMax(&sh.umax, __double_as_longlong(um));
-        }
-        __syncthreads();   // raw table read by everyone, all flags in
-        if constexpr (NEEDLUT) {
-#pragma unroll
-            for (int q = 0; q < LPT; ++q) {
-                const int i = tid + 256 * q;
-                if (i < 2050) sh.lut[i] = lv[q];
-            }
-        }
-        const i64 emin = sh.flag[0], emax = sh.flag[1], smin = sh.flag[2], smax = sh.flag[3];
-        const bool lut_ok = !NEEDLUT || !sh.flag[5];
-        const bool ezero = emin > emax || (emin == 0 && emax == 0);
-        // no element saturates: |y| <= max 2^22 Kp |m| 2^-s + 1 + max |b| < 2^31
-        const bool nosat = __longlong_as_double(sh.umax) + double(sh.flag[6]) + 2.0 < 2147483647.0;
-        form = ezero && smin >= 0 && smax <= 31 && nosat && lut_ok && !sh.flag[7] ? FORM_INT : FORM_EXACT;
-        form = __builtin_amdgcn_readfirstlane(form);
-#pragma unroll
-        for (int q = 0; q < S::CPT; ++q) {
-            const int j = tid + 256 * q;
-            if (j < ncols) {
-                const int4 c = cc[q];
-                if (form == FORM_INT) {
-                    // C = 128 wsum m + 2^(s-1) + b 2^s (|C| < 2^63: |wsum| <= 128 Kp, s <= 31)
-                    const i64 C = 128LL * i64(c.w) * i64(c.x) + (c.y ? (1LL << (c.y - 1)) : 0) + i64(c.z) * (1LL << c.y);
-                    sh.tab[j] = make_int4(c.x, c.y, int(unsigned(u64(C))), int(unsigned(u64(C) >> 32)));
-                }
-            }
-        }
-        __syncthreads();
-    }
+    const int form = stripe_setup<EPI, 256>(p, sh, tid, m0, cb, ncols, craw, erv, L2048);
 
     // ---- the rows' hi/lo split (int16 rows), once they have arrived
     if constexpr (SRC == SRC_I16) {
@@ -351,32 +421,10 @@ __global__ void __launch_bounds__(256, 2) stripe_kernel(const GemmParams p) {
     const bool lean = form == FORM_INT && (RES || !p.R);
     const bool lut_lds = NEEDLUT && !sh.flag[5];  // the expanded table in LDS is valid (0 <= L <= 65536)
 
-    // phi(x) for tables with 0 <= L <= 65536: x clamped to [-2^20 - 1, 2^20], entry (x >> 10) + 1025
-    // (1024 L[i] + d (x - 1024 (i - 1025))) >> 10 as one 24-bit multiply-add mod 2^32: the exact value
-    // lies in [0, 2^26] and |d| <= 65536, |xc| <= 2^20 + 1 fit the 24-bit operands
-    auto phi = [&](int x) -> int {
-        const int xc = min(max(x, -1048577), 1048576);
-        const int2 t = sh.lut[(xc >> 10) + 1025];
-        return int(unsigned(t.x) + unsigned(__mul24(t.y, xc))) >> 10;
-    };
-    // (a b + 2^15) >> 16 as a 64-bit product: the high word and the 32-bit result
-    auto mulsh16 = [&](int a, int b, unsigned& hi) -> int {
-        const i64 t = i64(a) * i64(b) + 32768;
-        hi = unsigned(u64(t) >> 32);
-        return int(__builtin_amdgcn_alignbit(hi, unsigned(u64(t)), 16));
-    };
-    // the same with 2^47 added to the rounding constant: returns y ^ 2^31 (y biased to unsigned order)
-    // and hi = (high word of a b + 2^15) + 2^15, which is <= 65535 exactly when y fits in int32
-    auto mulsh16b = [&](int a, int b, unsigned& hi) -> unsigned {
-        const i64 t = i64(a) * i64(b) + (32768 + (1LL << 47));
-        hi = unsigned(u64(t) >> 32);
-        return __builtin_amdgcn_alignbit(hi, unsigned(u64(t)), 16);
-    };
-    // the integer requantisation (A m + C) >> s of an element, exact when it fits in int32
-    auto req = [&](int A, const int4& k) -> int {
-        const i64 t = i64(A) * i64(k.x) + i64((u64(unsigned(k.w)) << 32) | unsigned(k.z));
-        return int(__builtin_amdgcn_alignbit(unsigned(u64(t) >> 32), unsigned(u64(t)), unsigned(k.y)));
-    };
+    auto phi = [&](int x) -> int { return stripe_phi(sh.lut, x); };
+    auto mulsh16 = [&](int a, int b, unsigned& hi) -> int { return stripe_mulsh16(a, b, hi); };
+    auto mulsh16b = [&](int a, int b, unsigned& hi) -> unsigned { return stripe_mulsh16b(a, b, hi); };
+    auto req = [&](int A, const int4& k) -> int { return stripe_req(A, k); };
 
     bool pipelined = false;
     if constexpr (!RES && !VIEW) {
