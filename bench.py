@@ -151,7 +151,7 @@ class ViewRun:
         self.hi = torch.empty((L.M, F), dtype=torch.int8, device="cuda")
         self.lo = torch.empty_like(self.hi)
         self.e = torch.empty(L.M, dtype=torch.int32, device="cuda")
-        nb = vg.view_workspace_bytes(L.M, L.N, L.epi)
+        nb = vg.view_workspace_bytes(L.M, L.N, L.Kp, L.epi)
         self.ws = torch.empty(nb // 4 + 64, dtype=torch.int32, device="cuda")
         self.E = vg.AEpi(epi=L.epi, Lphi=vg.ptr(prob.lphi), ws=vg.ptr(self.ws), ws_bytes=nb)
         # A + W + the int16 view + e + cst

@@ -99,9 +99,11 @@ int vgemm_hl2(void* stream, const VgemmASrc* A, int Mp, int Mreal, const int8_t*
  * semantics of its quant_row_out, src/kernels.cu:317-331, as k_epilogue_geglu_q / k_quant_rows give
  * them): per output row r < Mreal, e = row_exp(max |y|) into V->e[r], q = quant16_32(y, e) into the
  * planes V->hi / V->lo [Mreal x V->ld] (hi = q >> 8, lo = (q & 255) - 128), columns [nout, ld) padded
- * with (0, -128). EPI_PLAIN / EPI_GEGLU / EPI_GELU with int16 rows or int8 planes, Kp <= 320; E's
- * residual, rowmax and statistics must be NULL and E->Y is not written; V->ld % 16 == 0, planes
- * 16-byte aligned. Needs vgemm_view_workspace_bytes() of workspace in E->ws. */
+ * with (0, -128). EPI_PLAIN / EPI_GEGLU / EPI_GELU with int16 rows or int8 planes; E's residual,
+ * rowmax and statistics must be NULL and E->Y is not written; V->ld % 16 == 0, planes 16-byte
+ * aligned. Needs vgemm_view_workspace_bytes() of workspace in E->ws. Kp <= 320 runs the fused
+ * row-stationary form (three kernels); deeper K writes the GEMM's int32 rows into the workspace and
+ * quantises them (the tile kernels, then k_quant_rows). */
 typedef struct VgemmView {
     int8_t* hi; int8_t* lo; int32_t* e; int ld;
 } VgemmView;
@@ -180,9 +182,10 @@ int vgemm_lnorm(void* stream, const int32_t* X, int M, int C, const int64_t* g, 
 int vgemm_lnorm_q(void* stream, const int32_t* X, int M, int C, const int32_t* g, const int32_t* beta, int64_t den, int8_t* hi,
                   int8_t* lo, int32_t* e, int Kp);                                                 /* k_lnorm_q: the int16 view of the row */
 
-/* Workspace bytes the int16 view (vgemm_hl2_view) of an Mreal x Nreal call with this epilogue needs:
- * the row maxima, one exponent byte and one 32-bit mask per (row, 32 output columns). */
-size_t vgemm_view_workspace_bytes(int Mreal, int Nreal, int epi);
+/* Workspace bytes the int16 view (vgemm_hl2_view) of an Mreal x Nreal x Kp call with this epilogue
+ * needs: for Kp <= 320 the row maxima, one exponent byte and one 32-bit mask per (row, 32 output
+ * columns); deeper, the int32 output rows and the GEMM's split-K workspace at the current settings. */
+size_t vgemm_view_workspace_bytes(int Mreal, int Nreal, int Kp, int epi);
 /* Workspace bytes vgemm_hl2 uses for this shape at the current settings (0 = no split-K). */
 size_t vgemm_workspace_bytes(int Mp, int Mreal, int Np, int Nreal, int Kp, int epi);
 

@@ -26,7 +26,7 @@ def run_view(c: Case, vld: int):
     hi = torch.full((c.M, vld), 0x55, dtype=torch.int8, device="cuda")
     lo = torch.full((c.M, vld), 0x55, dtype=torch.int8, device="cuda")
     e = torch.full((c.M,), -7, dtype=torch.int32, device="cuda")
-    nb = vg.view_workspace_bytes(c.M, c.N, c.epi)
+    nb = vg.view_workspace_bytes(c.M, c.N, c.Kp, c.epi)
     ws = torch.empty(nb // 4 + 64, dtype=torch.int32, device="cuda")
     E = vg.AEpi(epi=c.epi, Lphi=vg.ptr(lut), ws=vg.ptr(ws), ws_bytes=nb)
     vg.k_gemm_hl2_view(A, c.Mp, c.M, w, c.Kp, c.Np, c.N, c.Kp, cst, E, hi, lo, e, vld)
@@ -59,6 +59,19 @@ def check(c: Case, vld: int, what: str):
 def test_view_matches_quant_rows(src, epi, M, N, K, vld):
     c = Case(src, M, N, K, epi=epi, seed=M + N + K + src)
     check(c, vld, f"view src {src} epi {epi} {M}x{N}x{K}")
+
+
+@pytest.mark.parametrize("src", [vg.SRC_I16, vg.SRC_I8])
+@pytest.mark.parametrize("epi,M,N,K,vld", [
+    (vg.EPI_GEGLU, 600, 5120, 640, 2560),      # the UNet's GEGLU up-projection at 640 channels (Kp 640)
+    (vg.EPI_GEGLU, 256, 10240, 1280, 5120),    # at 1280 channels (Kp 1280)
+    (vg.EPI_PLAIN, 300, 640, 1280, 656),       # padded view
+    (vg.EPI_GELU, 130, 256, 4096, 256),        # deep K over few tiles: split-K in the workspace's tail
+])
+def test_view_deep_k(src, epi, M, N, K, vld):
+    """Kp > 320: the GEMM's int32 rows in the workspace, then their quantisation."""
+    c = Case(src, M, N, K, epi=epi, seed=M + K + src, s_range=(18, 26))
+    check(c, vld, f"deep-K view src {src} epi {epi} {M}x{N}x{K}")
 
 
 def test_view_exponent_grows_across_chunks():
@@ -113,7 +126,7 @@ def test_view_c2_full_rows_sampled():
     hi = torch.empty((L.M, F), dtype=torch.int8, device="cuda")
     lo = torch.empty_like(hi)
     e = torch.empty(L.M, dtype=torch.int32, device="cuda")
-    nb = vg.view_workspace_bytes(L.M, L.N, L.epi)
+    nb = vg.view_workspace_bytes(L.M, L.N, L.Kp, L.epi)
     ws = torch.empty(nb // 4 + 64, dtype=torch.int32, device="cuda")
     E2 = vg.AEpi(epi=L.epi, Lphi=vg.ptr(p.lphi), ws=vg.ptr(ws), ws_bytes=nb)
     vg.k_gemm_hl2_view(p.A, L.Mp, L.M, p.w, p.w.shape[1], L.Np, L.N, L.Kp, p.cst, E2, hi, lo, e, F)
@@ -158,5 +171,6 @@ def test_view_errors():
         run(vg.AEpi(epi=vg.EPI_PLAIN, ws=vg.ptr(ws), ws_bytes=4 << 20), ld=120)
     d = Case(vg.SRC_I16, 256, 128, 640, epi=vg.EPI_PLAIN, seed=2)
     keep2 = {}
-    with pytest.raises(VgemmError, match="Kp <= 320"):
-        run(vg.AEpi(epi=vg.EPI_PLAIN, ws=vg.ptr(ws), ws_bytes=4 << 20), a=d.asrc(keep2), d=d)
+    need = vg.view_workspace_bytes(256, 128, d.Kp, vg.EPI_PLAIN)
+    with pytest.raises(VgemmError, match="needs a workspace"):
+        run(vg.AEpi(epi=vg.EPI_PLAIN, ws=vg.ptr(ws), ws_bytes=need - 16), a=d.asrc(keep2), d=d)

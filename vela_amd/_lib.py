@@ -124,7 +124,7 @@ SIGNATURES = [
     ("vgemm_set_tile_order", None, [I]),
     ("vgemm_conv16_halo_rows", I, [I, I, I, I, I]),
     ("vgemm_workspace_bytes", SZ, [I, I, I, I, I, I]),
-    ("vgemm_view_workspace_bytes", SZ, [I, I, I]),
+    ("vgemm_view_workspace_bytes", SZ, [I, I, I, I]),
     ("vgemm_i8_create", I, [SZ, ctypes.POINTER(P)]),
     ("vgemm_i8_destroy", I, [P]),
     ("vgemm_i8_run", I, [P, P, P, I, LL, P, I, LL, P, I, LL, I, I, I, I]),

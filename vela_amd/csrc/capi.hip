@@ -31,7 +31,7 @@ hipError_t launch_stripe16(int src, int epi, const GemmParams& p, hipStream_t st
 hipError_t launch_view_fix(hipStream_t st, const uint32_t* vmax, const uint8_t* vexp, const uint32_t* vmask, int M, int F, int G, int8_t* hi,
                            int8_t* lo, int ld, int32_t* e);
 hipError_t launch_splitk_epilogue(int epi, const GemmParams& p, hipStream_t st);
-hipError_t launch_quant_rows(hipStream_t st, const int32_t* X, int M, int K, int ldx, int8_t* hi, int8_t* lo, int32_t* e, int Kp);
+hipError_t launch_quant_rows(hipStream_t st, const int32_t* X, int M, int K, int ldx, int8_t* hi, int8_t* lo, int32_t* e, int Kp, int rows);
 hipError_t launch_pixmax(hipStream_t st, const int32_t* X, int rows, int C, uint32_t* pm);
 hipError_t launch_conv_e(hipStream_t st, const uint32_t* pm, int B, int H, int W, int stride, int32_t* e);
 hipError_t launch_im2col3(hipStream_t st, const int32_t* X, const uint32_t* pm, int B, int H, int W, int C, int stride, int8_t* hi, int8_t* lo,
@@ -287,6 +287,17 @@ ViewWs view_ws(int M, int nout) {
     return w;
 }
 
+// Deeper K (the tile kernels): the GEMM's int32 output rows [M x align4(nout)] in the workspace, then
+// k_quant_rows' quantisation of them into the view; the GEMM's split-K workspace follows.
+constexpr int VIEW_FUSED_KP = 320;
+struct ViewWs2 { int ld; size_t bytes; };
+ViewWs2 view_ws2(int M, int nout) {
+    ViewWs2 w;
+    w.ld = (nout + 3) / 4 * 4;
+    w.bytes = (size_t(M) * w.ld * 4 + 255) / 256 * 256;
+    return w;
+}
+
 size_t ws_bytes_for(int variant, int M, int N, int splits) {
     if (splits <= 1) return 0;
     const size_t rows = size_t(cdiv(M, TILES[variant].BM)) * TILES[variant].BM;
@@ -347,9 +358,11 @@ int vgemm_conv16_halo_rows(int H, int W, int C, int stride, int epi) {
     return vk::conv_halo_bm(epi, H, W, C, stride, (H - 1) / stride + 1, (W - 1) / stride + 1);
 }
 
-size_t vgemm_view_workspace_bytes(int Mreal, int Nreal, int epi) {
-    if (Mreal <= 0 || Nreal <= 0) return 0;
-    return view_ws(Mreal, epi == VGEMM_EPI_GEGLU ? Nreal / 2 : Nreal).bytes;
+size_t vgemm_view_workspace_bytes(int Mreal, int Nreal, int Kp, int epi) {
+    if (Mreal <= 0 || Nreal <= 0 || Kp <= 0) return 0;
+    const int nout = epi == VGEMM_EPI_GEGLU ? Nreal / 2 : Nreal;
+    if (Kp <= VIEW_FUSED_KP) return view_ws(Mreal, nout).bytes;
+    return view_ws2(Mreal, nout).bytes + vgemm_workspace_bytes(Mreal, Mreal, Nreal, Nreal, Kp, epi);
 }
 
 size_t vgemm_workspace_bytes(int Mp, int Mreal, int Np, int Nreal, int Kp, int epi) {
@@ -419,20 +432,41 @@ void* stream_workspace(hipStream_t st, size_t need, size_t* bytes) {
 // The int16 view of the output (vgemm_hl2_view): the row-stationary kernel writes each chunk at its
 // running row exponent with correction bits and row maxima in the workspace, then the fix-up pass
 // settles every row at its final exponent (stripe_kernel.h, producers.hip: view_fix_kernel).
-int view_impl(const VgemmASrc* A, const VgemmAEpi* E, const VgemmView* V, vk::GemmParams& p, int Mreal, int Nreal, const WsPolicy& wsp,
-              hipStream_t st) {
+int hl2_impl(void* stream, const VgemmASrc* A, int Mp, int Mreal, const int8_t* W, int ldw, int Np, int Nreal, int Kp,
+             const int32_t* cst, const VgemmAEpi* E, WsPolicy wsp, const VgemmView* V = nullptr);
+
+int view_impl(void* stream, const VgemmASrc* A, int Mp, int Mreal, const int8_t* W, int ldw, int Np, int Nreal, int Kp, const int32_t* cst,
+              const VgemmAEpi* E, const VgemmView* V, vk::GemmParams& p, const WsPolicy& wsp) {
+    hipStream_t st = static_cast<hipStream_t>(stream);
     const int epi = E->epi;
     if (epi != VGEMM_EPI_PLAIN && epi != VGEMM_EPI_GEGLU && epi != VGEMM_EPI_GELU)
         return fail(VGEMM_ERR_ARG, "gemm_hl int16 view: EPI_PLAIN, EPI_GEGLU or EPI_GELU only");
     if (E->residual || E->rowmax || E->gnstat) return fail(VGEMM_ERR_ARG, "gemm_hl int16 view: no residual, rowmax or statistics");
     if (A->src != VGEMM_SRC_I16 && A->src != VGEMM_SRC_I8) return fail(VGEMM_ERR_UNSUPPORTED, "gemm_hl int16 view: int16 rows or int8 planes only");
-    if (p.Kp > 320) return fail(VGEMM_ERR_UNSUPPORTED, "gemm_hl int16 view: Kp <= 320 only (the row-stationary kernel)");
     if (epi == VGEMM_EPI_GEGLU && Nreal % 2) return fail(VGEMM_ERR_ARG, "gemm_hl: EPI_GEGLU needs an even Nreal (interleaved a/g columns)");
     if (epi != VGEMM_EPI_PLAIN && !E->Lphi) return fail(VGEMM_ERR_ARG, "gemm_hl: EPI_GEGLU/EPI_GELU need Lphi");
     const int nout = epi == VGEMM_EPI_GEGLU ? Nreal / 2 : Nreal;
     if (nout % 4 || !V->hi || !V->lo || !V->e || V->ld < nout || V->ld % 16 || !aligned16(V->hi) || !aligned16(V->lo))
         return fail(VGEMM_ERR_ARG, "gemm_hl int16 view: output columns %% 4 == 0, hi/lo 16-byte aligned, ld >= output columns, ld %% 16 == 0, and e");
     if ((long long)Mreal * V->ld > MAX_EXTENT) return fail(VGEMM_ERR_UNSUPPORTED, "gemm_hl int16 view: planes larger than 2 GiB");
+    if (Kp > VIEW_FUSED_KP) {
+        // the GEMM's int32 rows into the workspace (the tile kernels, split-K in the workspace's
+        // tail), then their quantisation (k_quant_rows, Mreal rows)
+        const ViewWs2 vw = view_ws2(Mreal, nout);
+        const size_t need = vgemm_view_workspace_bytes(Mreal, Nreal, Kp, epi);
+        if (!wsp.ws || wsp.bytes < need)
+            return fail(wsp.strict ? VGEMM_ERR_UNSUPPORTED : VGEMM_ERR_ARG, "gemm_hl int16 view: needs a workspace of %zu bytes (AEpi.ws)", need);
+        if (!aligned16(wsp.ws)) return fail(VGEMM_ERR_ARG, "gemm_hl: workspace must be 16-byte aligned");
+        int32_t* Yw = static_cast<int32_t*>(wsp.ws);
+        VgemmAEpi E2 = *E;
+        E2.Y = Yw;
+        E2.ldy = vw.ld;
+        E2.ws_bytes = wsp.bytes - vw.bytes;
+        E2.ws = E2.ws_bytes ? static_cast<char*>(wsp.ws) + vw.bytes : nullptr;
+        const int rc = hl2_impl(stream, A, Mp, Mreal, W, ldw, Np, Nreal, Kp, cst, &E2, WsPolicy{E2.ws, E2.ws_bytes, wsp.strict});
+        if (rc) return rc;
+        return hip_status(vk::launch_quant_rows(st, Yw, Mreal, nout, vw.ld, V->hi, V->lo, V->e, V->ld, Mreal), "gemm_hl int16 view: quantisation");
+    }
     const ViewWs vw = view_ws(Mreal, nout);
     if (!wsp.ws || wsp.bytes < vw.bytes)
         return fail(wsp.strict ? VGEMM_ERR_UNSUPPORTED : VGEMM_ERR_ARG, "gemm_hl int16 view: needs a workspace of %zu bytes (AEpi.ws)", vw.bytes);
@@ -455,7 +489,7 @@ int view_impl(const VgemmASrc* A, const VgemmAEpi* E, const VgemmView* V, vk::Ge
 }
 
 int hl2_impl(void* stream, const VgemmASrc* A, int Mp, int Mreal, const int8_t* W, int ldw, int Np, int Nreal, int Kp,
-             const int32_t* cst, const VgemmAEpi* E, WsPolicy wsp, const VgemmView* V = nullptr) {
+             const int32_t* cst, const VgemmAEpi* E, WsPolicy wsp, const VgemmView* V) {
     if (!A || !E) return fail(VGEMM_ERR_ARG, "gemm_hl: null ASrc/AEpi");
     // The fields an epilogue does not read are ignored, as the reference's epilogue ignores them
     // (src/gemm_hl.cu:176-177, 279-296): the GroupNorm statistics outside EPI_PLAIN, the residual
@@ -542,7 +576,7 @@ int hl2_impl(void* stream, const VgemmASrc* A, int Mp, int Mreal, const int8_t* 
 
     const int epi = E->epi;
     p.Y = E->Y; p.ldy = E->ldy; p.R = E->residual; p.Lphi = E->Lphi; p.rowmax = E->rowmax;
-    if (V) return view_impl(A, E, V, p, Mreal, Nreal, wsp, static_cast<hipStream_t>(stream));
+    if (V) return view_impl(stream, A, Mp, Mreal, W, ldw, Np, Nreal, Kp, cst, E, V, p, wsp);
     p.Cs = E->Cs; p.Y1 = E->Y1; p.Y2 = E->Y2;
     p.gnstat = static_cast<vk::GnStat*>(E->gnstat); p.gnT = E->gnT;
     p.heads = E->heads; p.qT = E->T; p.TpQ = E->TpQ; p.TpK = E->TpK; p.qC = E->C;
@@ -820,7 +854,7 @@ int vgemm_i8_run(void* handle, void* stream, const int8_t* A, int lda, long long
 // ---- producers
 int vgemm_quant_rows(void* stream, const int32_t* X, int M, int K, int ldx, int8_t* hi, int8_t* lo, int32_t* e, int Kp) {
     if (!X || !hi || !lo || !e || M <= 0 || K <= 0 || Kp < K || Kp % 4 || ldx < K) return fail(VGEMM_ERR_ARG, "quant_rows: bad arguments");
-    return hip_status(vk::launch_quant_rows(static_cast<hipStream_t>(stream), X, M, K, ldx, hi, lo, e, Kp), "quant_rows launch");
+    return hip_status(vk::launch_quant_rows(static_cast<hipStream_t>(stream), X, M, K, ldx, hi, lo, e, Kp, (M + 31) / 32 * 32), "quant_rows launch");
 }
 
 int vgemm_epilogue(void* stream, const int32_t* Chi, const int32_t* Clo, int M, int N, int ldc, const int32_t* cst, const int32_t* e, int32_t* Y,

@@ -313,8 +313,9 @@ __global__ void __launch_bounds__(256) fill_u32_kernel(uint32_t* __restrict__ p,
 
 static inline unsigned blocks_for(size_t n, size_t per) { return unsigned((n + per - 1) / per); }
 
-hipError_t launch_quant_rows(hipStream_t st, const int32_t* X, int M, int K, int ldx, int8_t* hi, int8_t* lo, int32_t* e, int Kp) {
-    const int Mp = (M + 31) / 32 * 32;
+// rows: the rows written, M and the pad rows [M, rows) (k_quant_rows: align32(M))
+hipError_t launch_quant_rows(hipStream_t st, const int32_t* X, int M, int K, int ldx, int8_t* hi, int8_t* lo, int32_t* e, int Kp, int rows) {
+    const int Mp = rows;
     const dim3 grid(blocks_for(Mp, 4));
     const int words = (Kp / 4 + 63) / 64;   // int4 words per lane
     if (ldx % 4 == 0 && (reinterpret_cast<uintptr_t>(X) & 15) == 0 && words <= 8) {

@@ -121,9 +121,9 @@ def workspace_bytes(Mp: int, Mreal: int, Np: int, Nreal: int, Kp: int, epi: int 
     return int(load().vgemm_workspace_bytes(Mp, Mreal, Np, Nreal, Kp, epi))
 
 
-def view_workspace_bytes(Mreal: int, Nreal: int, epi: int = EPI_PLAIN) -> int:
-    """Workspace bytes of the int16 view (k_gemm_hl2_view) for an Mreal x Nreal call."""
-    return int(load().vgemm_view_workspace_bytes(Mreal, Nreal, epi))
+def view_workspace_bytes(Mreal: int, Nreal: int, Kp: int, epi: int = EPI_PLAIN) -> int:
+    """Workspace bytes of the int16 view (k_gemm_hl2_view) for an Mreal x Nreal x Kp call."""
+    return int(load().vgemm_view_workspace_bytes(Mreal, Nreal, Kp, epi))
 
 
 class Gemm:
