@@ -75,8 +75,6 @@ __global__ void __launch_bounds__(512, 4) stripe16_kernel(const GemmParams p) {
     if (cb >= ce) return;   // (the host sizes the grid so that every block has a chunk)
     const bool dma_wave = wave < 4;   // waves 0..3 issue the W and table DMA
 
-    if (tid == 0) stripe_clear_flags(sh);
-
     // ---- the block's column constants, the row shift of row m0 + tid, the GELU table (DMA), chunk cb
     const int ncols = (ce - cb) * CH;
     v4i craw[G::CPT];
@@ -124,7 +122,8 @@ __global__ void __launch_bounds__(512, 4) stripe16_kernel(const GemmParams p) {
     // ---- block set-up (column table, expanded GELU table, flags, form)
     vm_wait<AL>();   // the column constants, the table and chunk cb's W (older than the row loads)
     block_barrier();
-    const int form = stripe_setup<EPI, NT>(p, sh, tid, m0, cb, ncols, craw, erv, L2048);
+    bool lut_ok;
+    const int form = stripe_setup<EPI, NT>(p, sh, tid, m0, cb, ncols, craw, erv, L2048, lut_ok);
 
     // ---- the rows' hi/lo split (int16 rows), once they have arrived
     if constexpr (SRC == SRC_I16) {
@@ -142,7 +141,7 @@ __global__ void __launch_bounds__(512, 4) stripe16_kernel(const GemmParams p) {
     // this lane's rows are rbase + 4 fg + v
     const unsigned rowoff = unsigned(rbase + 4 * fg) * ldy4;
     unsigned yabs[4] = {0u, 0u, 0u, 0u};   // running max |y| of the lane's four rows
-    const bool lut_lds = NEEDLUT && !sh.flag[5];
+    const bool lut_lds = NEEDLUT && lut_ok;
     const v4i vzero = {0, 0, 0, 0};
     // W fragment of K step t, subtile u of the chunk in LDS stage sW (B operand: lane column fr)
     auto wfrag = [&](const unsigned char* sW, int t, int u) __attribute__((always_inline)) {

@@ -73,8 +73,7 @@ struct StripeShared {
     // above the table: 1024 phi(x) = lut[j].x + lut[j].y x (mod 2^32) for x in entry j's range
     int2 lut[LUT ? 2050 : 1];
     int erow[StripeCfg::BM];    // per-row shifts of the block (int64 form)
-    unsigned long long umax;
-    int flag[8];                // emin, emax, smin, smax, column bound failed, table range failed, max |b|, |wsum| > 128 Kp
+    int wflag[8];               // per wave of the set-up: bit 0 the integer form cannot hold, bit 1 a table entry lies outside [0, 65536]
 };
 
 // byte offset inside sh.lut of the raw table as the DMA delivers it (entries 0..2047)
@@ -118,16 +117,23 @@ __device__ __forceinline__ void stripe_lut_dma(const GemmParams& p, StripeShared
 }
 
 // Once the column constants, the raw table and the row shifts are in: the expanded GELU table, the
-// integer form's column table and the block's flags; returns the block's epilogue form (uniform).
-// Ends with a block-wide barrier after the tables are written.
+// integer form's column table and the block's epilogue form (uniform), which is the integer form
+// when every row has e = 0 and every column satisfies, with 32-bit tests: 0 <= s <= 31, |m| Kp <
+// 2^30, |wsum| <= 128 Kp, |b| < 2^30 and 2^22 Kp |m| 2^-s < 2^30 (so that no element saturates:
+// |y| <= 2^22 Kp |m| 2^-s + 1 + |b| < 2^31, as |acc| <= 32768 * 128 * Kp), and the table lies in
+// [0, 65536]. Each thread tests its own columns, rows and table entries; a ballot per wave and one
+// LDS word per wave carry the result through the barrier that the table expansion needs anyway.
+// lut_ok: the table lies in [0, 65536] (the expanded table in LDS is then valid). Ends with a
+// block-wide barrier after the tables are written.
 template <int EPI, int NT>
 __device__ __forceinline__ int stripe_setup(const GemmParams& p, StripeShared<EPI == EPI_GEGLU || EPI == EPI_GELU>& sh, int tid,
-                                            int m0, int cb, int ncols, const v4i* craw, int erv, int L2048) {
+                                            int m0, int cb, int ncols, const v4i* craw, int erv, int L2048, bool& lut_ok) {
     constexpr bool NEEDLUT = EPI == EPI_GEGLU || EPI == EPI_GELU;
     constexpr int CH = StripeCfg::CH, BM = StripeCfg::BM, CPT = (StripeCfg::NCOLS + NT - 1) / NT;
     constexpr int LPT = NEEDLUT ? (2050 + NT - 1) / NT : 1;
+    static_assert(NT / 64 <= 8, "one set-up word per wave");
     int2 lv[LPT];
-    int lbad = 0;
+    bool lbad = false;
     if constexpr (NEEDLUT) {
         const int* raw = reinterpret_cast<const int*>(reinterpret_cast<const char*>(sh.lut) + STRIPE_LUT_RAW);
 #pragma unroll
@@ -137,66 +143,41 @@ __device__ __forceinline__ int stripe_setup(const GemmParams& p, StripeShared<EP
             if (i == 2049) v = make_int2(65536 << 10, 0);
             else if (i >= 1 && i < 2049) {
                 const int a = raw[i - 1], nx = i - 1 == 2047 ? L2048 : raw[i];
-                if (a < 0 || a > 65536 || nx < 0 || nx > 65536) lbad = 1;
+                lbad |= unsigned(a) > 65536u || unsigned(nx) > 65536u;
                 // the entry's offset taken at x = 0 instead of at its first x, 1024 (i - 1025)
                 v = make_int2(int((unsigned(a) << 10) - unsigned(nx - a) * unsigned(1024 * (i - 1025))), nx - a);
             }
             lv[q] = v;
         }
     }
+    const unsigned mlim = (1u << 30) / unsigned(p.Kp);   // |m| < mlim  <=>  |m| Kp < 2^30
     int4 cc[CPT];
-    int smn = INT_MAX, smx = INT_MIN, bad = 0, bmx = 0, wbad = 0;
-    double um = 0.0;
+    bool bad = false;
 #pragma unroll
     for (int q = 0; q < CPT; ++q) {
         const int j = tid + NT * q;
-        cc[q] = make_int4(0, 0, 0, 0);
-        if (j < ncols) {
-            const int n = cb * CH + (j / CH) * CH + wrow_of_lds<EPI, CH>(j % CH);
-            if (n < p.Nreal) {
-                const int4 c = make_int4(craw[q][0], craw[q][1], craw[q][2], craw[q][3]);
-                cc[q] = c;
-                const i64 mag = (c.x < 0 ? -i64(c.x) : i64(c.x)) * i64(p.Kp);
-                if (mag >= (1LL << 30) || c.y < -1000 || c.y > 1000) bad = 1;
-                // the bounds below take |acc| <= 2^22 Kp, which needs |wsum| <= 128 Kp
-                if (uabs(c.w) > 128u * unsigned(p.Kp)) wbad = 1;
-                smn = min(smn, c.y);
-                smx = max(smx, c.y);
-                // |acc m 2^-s| <= 2^22 Kp |m| 2^-s, since |acc| <= 32768 * 128 * Kp
-                if (c.y >= -1000 && c.y <= 1000) um = max(um, ldexp(4194304.0 * double(p.Kp) * fabs(double(c.x)), -c.y));
-                else um = 1e300;
-                bmx = max(bmx, int(min(uabs(c.z), 0x7fffffffu)));
-            }
-        }
+        const int n = cb * CH + (j / CH) * CH + wrow_of_lds<EPI, CH>(j % CH);
+        const bool live = j < ncols && n < p.Nreal;
+        const int4 c = live ? make_int4(craw[q][0], craw[q][1], craw[q][2], craw[q][3]) : make_int4(0, 0, 0, 0);
+        cc[q] = c;
+        const unsigned am = uabs(c.x);
+        const bool sok = unsigned(c.y) <= 31u;
+        // 2^22 Kp |m| 2^-s < 2^30  <=>  Kp |m| < 2^(8 + s), with Kp |m| < 2^30
+        // (for s >= 23 the shift by 31 holds too, as Kp |m| < 2^30)
+        const bool umok = am < mlim && ((am * unsigned(p.Kp)) >> (sok ? min(8 + c.y, 31) : 0)) == 0u;
+        bad |= !(sok && umok && uabs(c.w) <= 128u * unsigned(p.Kp) && uabs(c.z) < (1u << 30));
     }
-    int emn = INT_MAX, emx = INT_MIN;
     if (tid < BM) {
-        const int er = erv;
-        sh.erow[tid] = er;
-        if (m0 + tid < p.Mreal) emn = emx = er;
+        sh.erow[tid] = erv;
+        bad |= m0 + tid < p.Mreal && erv != 0;
     }
+    const bool anybad = __builtin_amdgcn_ballot_w64(bad) != 0, anylbad = __builtin_amdgcn_ballot_w64(lbad) != 0;
+    if ((tid & 63) == 0) sh.wflag[tid >> 6] = (anybad ? 1 : 0) | (anylbad ? 2 : 0);
+    __syncthreads();   // raw table read by everyone, every wave's word in
+    int f = 0;
 #pragma unroll
-    for (int o = 32; o; o >>= 1) {
-        emn = min(emn, __shfl_xor(emn, o));
-        emx = max(emx, __shfl_xor(emx, o));
-        smn = min(smn, __shfl_xor(smn, o));
-        smx = max(smx, __shfl_xor(smx, o));
-        bad |= __shfl_xor(bad, o);
-        wbad |= __shfl_xor(wbad, o);
-        bmx = max(bmx, __shfl_xor(bmx, o));
-        um = max(um, __shfl_xor(um, o));
-        if constexpr (NEEDLUT) lbad |= __shfl_xor(lbad, o);
-    }
-    if ((tid & 63) == 0) {
-        if (emn <= emx) { atomicMin(&sh.flag[0], emn); atomicMax(&sh.flag[1], emx); }
-        if (smn <= smx) { atomicMin(&sh.flag[2], smn); atomicMax(&sh.flag[3], smx); }
-        if (bad) atomicOr(&sh.flag[4], 1);
-        if (wbad) atomicOr(&sh.flag[7], 1);
-        if (lbad) atomicOr(&sh.flag[5], 1);
-        atomicMax(&sh.flag[6], bmx);
-        atomicMax(&sh.umax, __double_as_longlong(um));
-    }
-    __syncthreads();   // raw table read by everyone, all flags in
+    for (int w = 0; w < NT / 64; ++w) f |= sh.wflag[w];
+    lut_ok = !NEEDLUT || !(f & 2);
     if constexpr (NEEDLUT) {
 #pragma unroll
         for (int q = 0; q < LPT; ++q) {
@@ -204,19 +185,13 @@ __device__ __forceinline__ int stripe_setup(const GemmParams& p, StripeShared<EP
             if (i < 2050) sh.lut[i] = lv[q];
         }
     }
-    const i64 emin = sh.flag[0], emax = sh.flag[1], smin = sh.flag[2], smax = sh.flag[3];
-    const bool lut_ok = !NEEDLUT || !sh.flag[5];
-    const bool ezero = emin > emax || (emin == 0 && emax == 0);
-    // no element saturates: |y| <= max 2^22 Kp |m| 2^-s + 1 + max |b| < 2^31
-    const bool nosat = __longlong_as_double(sh.umax) + double(sh.flag[6]) + 2.0 < 2147483647.0;
-    int form = ezero && smin >= 0 && smax <= 31 && nosat && lut_ok && !sh.flag[7] ? FORM_INT : FORM_EXACT;
-    form = __builtin_amdgcn_readfirstlane(form);
+    const int form = __builtin_amdgcn_readfirstlane(f == 0 ? FORM_INT : FORM_EXACT);
+    if (form == FORM_INT) {
 #pragma unroll
-    for (int q = 0; q < CPT; ++q) {
-        const int j = tid + NT * q;
-        if (j < ncols) {
-            const int4 c = cc[q];
-            if (form == FORM_INT) {
+        for (int q = 0; q < CPT; ++q) {
+            const int j = tid + NT * q;
+            if (j < ncols) {
+                const int4 c = cc[q];
                 // C = 128 wsum m + 2^(s-1) + b 2^s (|C| < 2^63: |wsum| <= 128 Kp, s <= 31)
                 const i64 C = 128LL * i64(c.w) * i64(c.x) + (c.y ? (1LL << (c.y - 1)) : 0) + i64(c.z) * (1LL << c.y);
                 sh.tab[j] = make_int4(c.x, c.y, int(unsigned(u64(C))), int(unsigned(u64(C) >> 32)));
@@ -302,14 +277,6 @@ __device__ __forceinline__ int stripe_req(int A, const int4& k) {
     return int(__builtin_amdgcn_alignbit(unsigned(u64(t) >> 32), unsigned(u64(t)), unsigned(k.y)));
 }
 
-// flags of the block set-up, cleared by thread 0 before the set-up reads them
-template <bool LUT>
-__device__ __forceinline__ void stripe_clear_flags(StripeShared<LUT>& sh) {
-    sh.flag[0] = INT_MAX; sh.flag[1] = INT_MIN; sh.flag[2] = INT_MAX; sh.flag[3] = INT_MIN;
-    sh.flag[4] = 0; sh.flag[5] = 0; sh.flag[6] = 0; sh.flag[7] = 0;
-    sh.umax = 0;
-}
-
 // RES: the PLAIN instantiation for calls with a residual (its own kernel, so that the residual
 // loads do not shape the code of the others). VIEW: the int16-view instantiation (no Y; see the
 // view loop below).
@@ -348,7 +315,6 @@ __global__ void __launch_bounds__(256, 2) stripe_kernel(const GemmParams p) {
     const int nlim = GEGLU ? (p.Nreal >> 1) : p.Nreal;
     if (cb >= ce) return;   // (the host sizes the grid so that every block has a chunk)
 
-    if (tid == 0) stripe_clear_flags(sh);
 
     // ---- the block's column constants, the row shift of row m0 + tid, the GELU table (DMA)
     const int ncols = (ce - cb) * CH;
@@ -394,7 +360,8 @@ __global__ void __launch_bounds__(256, 2) stripe_kernel(const GemmParams p) {
     // ---- block set-up: column constants of chunks [cb, ce), the expanded GELU table, flags
     vm_wait<AL>();   // the column constants, the table and chunk cb's W (older than the row loads)
     block_barrier();
-    const int form = stripe_setup<EPI, 256>(p, sh, tid, m0, cb, ncols, craw, erv, L2048);
+    bool lut_ok;
+    const int form = stripe_setup<EPI, 256>(p, sh, tid, m0, cb, ncols, craw, erv, L2048, lut_ok);
 
     // ---- the rows' hi/lo split (int16 rows), once they have arrived
     if constexpr (SRC == SRC_I16) {
@@ -419,7 +386,7 @@ __global__ void __launch_bounds__(256, 2) stripe_kernel(const GemmParams p) {
     // the integer form's epilogue issues a fixed number of stores per chunk, and residual loads that
     // it consumes before the chunk's last stores
     const bool lean = form == FORM_INT && (RES || !p.R);
-    const bool lut_lds = NEEDLUT && !sh.flag[5];  // the expanded table in LDS is valid (0 <= L <= 65536)
+    const bool lut_lds = NEEDLUT && lut_ok;  // the expanded table in LDS is valid (0 <= L <= 65536)
 
     auto phi = [&](int x) -> int { return stripe_phi(sh.lut, x); };
     auto mulsh16 = [&](int a, int b, unsigned& hi) -> int { return stripe_mulsh16(a, b, hi); };
