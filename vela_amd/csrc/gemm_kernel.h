@@ -185,8 +185,8 @@ struct EpiShared : GnShared<GN> {
     double wm[BN];      // 128 * wsum * m * 2^-s; + 1/2 when e == 0, and + b as well when the block folds b
     int b[BN];
     int2 lut[LUT ? 2050 : 1];   // lut[i + 1] = (L[i], L[i+1] - L[i]); lut[0] below the table, lut[2049] above
-    unsigned long long umax;    // bits of max over columns of 2^22*Kp*|m|*2^-s (a positive double)
-    int flag[8];        // emin, emax, smin, smax, column bound failed, table range failed, max |b|, b not foldable
+    int4 wslot[8];      // per wave of the set-up: min e, max e, min s, max s over its rows / columns
+    int wbits[8];       // per wave: bit 0 a column bound failed, bit 1 a table entry lies outside [0, 65536], bit 2 b not foldable
 };
 
 // GroupNorm statistics of a block (src/gemm_hl.cu:175-177, 285-287, 306-309). The reference gathers
@@ -259,88 +259,115 @@ __device__ __forceinline__ int row_shift(const GemmParams& p, int r) {
     return p.e ? p.e[r] : 0;
 }
 
+// Wave-wide minimum / maximum (every lane active): within each 16-lane row by DPP (xor 1, xor 2, the
+// half-row mirror, the row mirror), then over the four rows by readlane.
+template <int CTRL>
+__device__ __forceinline__ int dpp_i32(int v) { return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false); }
+__device__ __forceinline__ int wave_min_i32(int v) {
+    v = min(v, dpp_i32<0xB1>(v));
+    v = min(v, dpp_i32<0x4E>(v));
+    v = min(v, dpp_i32<0x141>(v));
+    v = min(v, dpp_i32<0x140>(v));
+    return min(min(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
+               min(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
+}
+__device__ __forceinline__ int wave_max_i32(int v) {
+    v = max(v, dpp_i32<0xB1>(v));
+    v = max(v, dpp_i32<0x4E>(v));
+    v = max(v, dpp_i32<0x141>(v));
+    v = max(v, dpp_i32<0x140>(v));
+    return max(max(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
+               max(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
+}
+
+// A thread's share of the block's exactness test: the shift range of its rows and columns and the
+// failed tests of its columns and table entries. Each wave reduces its threads' shares and writes
+// one slot; after a barrier every thread combines the slots (setup_flags).
+struct SetupPart {
+    int emn = INT_MAX, emx = INT_MIN, smn = INT_MAX, smx = INT_MIN;
+    bool bad = false, lbad = false, nofold = false;
+};
+template <class S>
+__device__ __forceinline__ void setup_publish(S& sh, const SetupPart& v) {
+    const int emn = wave_min_i32(v.emn), emx = wave_max_i32(v.emx), smn = wave_min_i32(v.smn), smx = wave_max_i32(v.smx);
+    const int bits = (__builtin_amdgcn_ballot_w64(v.bad) ? 1 : 0) | (__builtin_amdgcn_ballot_w64(v.lbad) ? 2 : 0) |
+                     (__builtin_amdgcn_ballot_w64(v.nofold) ? 4 : 0);
+    if ((threadIdx.x & 63) == 0) {
+        sh.wslot[threadIdx.x >> 6] = make_int4(emn, emx, smn, smx);
+        sh.wbits[threadIdx.x >> 6] = bits;
+    }
+}
+// The block's forms from the waves' slots. fast: the FP64 form is exact for every element (columns
+// with |m| Kp < 2^30 and |s| <= 1000, 1 <= s - e <= 52 for every row and column, the table in
+// [0, 65536]); ezero: every row has e = 0; fold: also no element can saturate and b folds exactly
+// into the FMA constant (every column with 2^22 Kp |m| 2^-s < 2^30, |b| < 2^30 and |b| 2^s < 2^51).
+template <bool NEEDLUT, int NW, class S>
+__device__ __forceinline__ EpiFlags setup_flags(const S& sh) {
+    int emin = INT_MAX, emax = INT_MIN, smin = INT_MAX, smax = INT_MIN, bits = 0;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+        const int4 q = sh.wslot[w];
+        emin = min(emin, q.x); emax = max(emax, q.y); smin = min(smin, q.z); smax = max(smax, q.w);
+        bits |= sh.wbits[w];
+    }
+    EpiFlags f;
+    f.fast = !(bits & 1) && (i64(smin) - emax >= 1) && (i64(smax) - emin <= 52) && emin >= -1000 && emax <= 1000;
+    if (NEEDLUT && (bits & 2)) f.fast = false;
+    f.ezero = emin > emax || (emin == 0 && emax == 0);
+    f.fold = f.fast && f.ezero && !(bits & 4);
+    return f;
+}
+
+// a column's FP64 constants m 2^-s, 128 wsum m 2^-s and its share of the exactness test
+__device__ __forceinline__ void setup_column(const GemmParams& p, const int4& c, double& ms, double& wmv, SetupPart& sp) {
+    const i64 mag = (c.x < 0 ? -i64(c.x) : i64(c.x)) * i64(p.Kp);
+    sp.bad |= mag >= (1LL << 30) || c.y < -1000 || c.y > 1000;
+    sp.smn = min(sp.smn, c.y);
+    sp.smx = max(sp.smx, c.y);
+    if (c.y >= -1000 && c.y <= 1000) {
+        ms = ldexp(double(c.x), -c.y);
+        wmv = ldexp(128.0 * (double(c.w) * double(c.x)), -c.y);
+        // |acc*m*2^-s| <= 2^22*Kp*|m|*2^-s, since |acc| <= 32768*128*Kp; with that below 2^30 and
+        // |b| < 2^30 no element saturates; wm + 1/2 + b is exact when |b|*2^s < 2^51
+        const double um = ldexp(4194304.0 * double(p.Kp) * fabs(double(c.x)), -c.y);
+        sp.nofold |= !(um < 1073741824.0) || uabs(c.z) >= (1u << 30) || ldexp(fabs(double(c.z)), c.y) >= 2251799813685248.0;
+    } else {
+        ms = 0.0;
+        wmv = 0.0;
+    }
+}
+
 // Fill the epilogue constants of columns [n0, n0 + BN) (in LDS-row order) and decide whether the
 // FP64 epilogue is exact for every element of this block.
 template <int EPI, int SRC, int BM, int BN, class S>
 __device__ __forceinline__ EpiFlags block_prologue(const GemmParams& p, int m0, int n0, S& sh) {
     constexpr bool NEEDLUT = EPI == EPI_GEGLU || EPI == EPI_GELU;
-    const int tid = threadIdx.x, lane = tid & 63;
-    if (tid == 0) {
-        sh.flag[0] = INT_MAX; sh.flag[1] = INT_MIN; sh.flag[2] = INT_MAX; sh.flag[3] = INT_MIN;
-        sh.flag[4] = 0; sh.flag[5] = 0; sh.flag[6] = 0; sh.flag[7] = 0;
-        sh.umax = 0;
+    const int tid = threadIdx.x;
+    if constexpr (EPI == EPI_PLAIN_GN) {
+        gn_clear(p, m0, sh);
+        __syncthreads();
     }
-    if constexpr (EPI == EPI_PLAIN_GN) gn_clear(p, m0, sh);
-    __syncthreads();
-    // per-row shift range (one LDS atomic per wave)
-    {
-        int emn = INT_MAX, emx = INT_MIN;
-        for (int i = tid; i < BM; i += 256) {
-            const int r = m0 + i;
-            if (r < p.Mreal) {
-                const int er = row_shift<SRC>(p, r);
-                emn = min(emn, er);
-                emx = max(emx, er);
-            }
-        }
-#pragma unroll
-        for (int o = 32; o; o >>= 1) {
-            emn = min(emn, __shfl_xor(emn, o));
-            emx = max(emx, __shfl_xor(emx, o));
-        }
-        if (lane == 0 && emn <= emx) {
-            atomicMin(&sh.flag[0], emn);
-            atomicMax(&sh.flag[1], emx);
+    SetupPart sp;
+    for (int i = tid; i < BM; i += 256) {
+        const int r = m0 + i;
+        if (r < p.Mreal) {
+            const int er = row_shift<SRC>(p, r);
+            sp.emn = min(sp.emn, er);
+            sp.emx = max(sp.emx, er);
         }
     }
-    {
-        int smn = INT_MAX, smx = INT_MIN, bad = 0, bmx = 0, nofold = 0;
-        double um = 0.0;
-        for (int j = tid; j < BN; j += 256) {
-            const int n = n0 + wrow_of_lds<EPI, BN>(j);
-            double ms = 0.0, wmv = 0.0;
-            int bb = 0;
-            if (n < p.Nreal) {
-                const int4 c = p.cst[n];
-                const i64 mag = (c.x < 0 ? -i64(c.x) : i64(c.x)) * i64(p.Kp);
-                if (mag >= (1LL << 30) || c.y < -1000 || c.y > 1000) bad = 1;
-                smn = min(smn, c.y);
-                smx = max(smx, c.y);
-                if (c.y >= -1000 && c.y <= 1000) {
-                    ms = ldexp(double(c.x), -c.y);
-                    wmv = ldexp(128.0 * (double(c.w) * double(c.x)), -c.y);
-                    // |acc*m*2^-s| <= 2^22*Kp*|m|*2^-s, since |acc| <= 32768*128*Kp
-                    um = max(um, ldexp(4194304.0 * double(p.Kp) * fabs(double(c.x)), -c.y));
-                    // wm + 1/2 + b is exact when |b|*2^s < 2^51 (numerator below 2^53)
-                    if (ldexp(fabs(double(c.z)), c.y) >= 2251799813685248.0) nofold = 1;
-                }
-                bb = c.z;
-                bmx = max(bmx, int(min(uabs(c.z), 0x7fffffffu)));
-            }
-            sh.ms[j] = ms; sh.wm[j] = wmv; sh.b[j] = bb;
+    for (int j = tid; j < BN; j += 256) {
+        const int n = n0 + wrow_of_lds<EPI, BN>(j);
+        double ms = 0.0, wmv = 0.0;
+        int bb = 0;
+        if (n < p.Nreal) {
+            const int4 c = p.cst[n];
+            setup_column(p, c, ms, wmv, sp);
+            bb = c.z;
         }
-#pragma unroll
-        for (int o = 32; o; o >>= 1) {
-            smn = min(smn, __shfl_xor(smn, o));
-            smx = max(smx, __shfl_xor(smx, o));
-            bad |= __shfl_xor(bad, o);
-            bmx = max(bmx, __shfl_xor(bmx, o));
-            nofold |= __shfl_xor(nofold, o);
-            um = max(um, __shfl_xor(um, o));
-        }
-        if (lane == 0) {
-            if (smn <= smx) {
-                atomicMin(&sh.flag[2], smn);
-                atomicMax(&sh.flag[3], smx);
-            }
-            if (bad) atomicOr(&sh.flag[4], 1);
-            atomicMax(&sh.flag[6], bmx);
-            if (nofold) atomicOr(&sh.flag[7], 1);
-            atomicMax(&sh.umax, __double_as_longlong(um));
-        }
+        sh.ms[j] = ms; sh.wm[j] = wmv; sh.b[j] = bb;
     }
     if constexpr (NEEDLUT) {
-        int bad = 0;
         for (int i = tid; i < 2050; i += 256) {
             int2 v;
             if (i == 0) v = make_int2(0, 0);
@@ -348,23 +375,14 @@ __device__ __forceinline__ EpiFlags block_prologue(const GemmParams& p, int m0, 
             else {
                 const int a = p.Lphi[i - 1], nx = p.Lphi[i];
                 v = make_int2(a, nx - a);
-                if (a < 0 || a > 65536 || nx < 0 || nx > 65536) bad = 1;
+                sp.lbad |= unsigned(a) > 65536u || unsigned(nx) > 65536u;
             }
             sh.lut[i] = v;
         }
-#pragma unroll
-        for (int o = 32; o; o >>= 1) bad |= __shfl_xor(bad, o);
-        if (lane == 0 && bad) atomicOr(&sh.flag[5], 1);
     }
+    setup_publish(sh, sp);
     __syncthreads();
-    const i64 emin = sh.flag[0], emax = sh.flag[1], smin = sh.flag[2], smax = sh.flag[3];
-    EpiFlags f;
-    f.fast = !sh.flag[4] && (smin - emax >= 1) && (smax - emin <= 52) && emin >= -1000 && emax <= 1000;
-    if (NEEDLUT && sh.flag[5]) f.fast = false;
-    f.ezero = emin > emax || (emin == 0 && emax == 0);
-    // fold: e == 0 and no element can saturate (|floor(X)| + |b| < 2^31), so y = floor(X + b) with b
-    // folded into the FMA constant and no saturating int steps
-    f.fold = f.fast && f.ezero && !sh.flag[7] && __longlong_as_double(sh.umax) + double(sh.flag[6]) + 2.0 < 2147483647.0;
+    const EpiFlags f = setup_flags<NEEDLUT, 4>(sh);
     if (f.ezero) {
         // the FMA constant of the e == 0 forms: wm + 1/2, and + b when folded (exact, see above)
         for (int j = tid; j < BN; j += 256) sh.wm[j] = (sh.wm[j] + 0.5) + (f.fold ? double(sh.b[j]) : 0.0);
@@ -407,11 +425,11 @@ template <int EPI, int SRC, int BM, int BN, int NT, class S>
 __device__ __forceinline__ EpiFlags epi_setup(const GemmParams& p, const TilePre& t, int L2048, S& sh) {
     constexpr bool NEEDLUT = EPI == EPI_GEGLU || EPI == EPI_GELU;
     static_assert(NT >= BM && NT >= BN, "one table row and column per thread");
-    const int tid = threadIdx.x, lane = tid & 63;
+    const int tid = threadIdx.x;
     // ---- phase 1: everything that reads LDS or needs no LDS (the raw table is still in place)
     constexpr int LPT = NEEDLUT ? (2050 + NT - 1) / NT : 1;   // table entries per thread
+    SetupPart sp;
     int2 lv[LPT];
-    int lbad = 0;
     if constexpr (NEEDLUT) {
         const int* raw = reinterpret_cast<const int*>(reinterpret_cast<const char*>(sh.lut) + LUT_RAW_OFF);
 #pragma unroll
@@ -422,52 +440,26 @@ __device__ __forceinline__ EpiFlags epi_setup(const GemmParams& p, const TilePre
             else if (i >= 1 && i <= 2049) {
                 const int a = raw[i - 1], nx = i - 1 == 2047 ? L2048 : raw[i];
                 v = make_int2(a, nx - a);
-                if (a < 0 || a > 65536 || nx < 0 || nx > 65536) lbad = 1;
+                sp.lbad |= unsigned(a) > 65536u || unsigned(nx) > 65536u;
             }
             lv[q] = v;
         }
     }
-    double ms = 0.0, wmv = 0.0, um = 0.0;
-    int bb = 0, smn = INT_MAX, smx = INT_MIN, bad = 0, bmx = 0, nofold = 0;
-    if (t.cok) {
-        const int4 c = t.c;
-        const i64 mag = (c.x < 0 ? -i64(c.x) : i64(c.x)) * i64(p.Kp);
-        if (mag >= (1LL << 30) || c.y < -1000 || c.y > 1000) bad = 1;
-        smn = c.y;
-        smx = c.y;
-        if (c.y >= -1000 && c.y <= 1000) {
-            ms = ldexp(double(c.x), -c.y);
-            wmv = ldexp(128.0 * (double(c.w) * double(c.x)), -c.y);
-            // |acc*m*2^-s| <= 2^22*Kp*|m|*2^-s, since |acc| <= 32768*128*Kp
-            um = ldexp(4194304.0 * double(p.Kp) * fabs(double(c.x)), -c.y);
-            // wm + 1/2 + b is exact when |b|*2^s < 2^51 (numerator below 2^53)
-            if (ldexp(fabs(double(c.z)), c.y) >= 2251799813685248.0) nofold = 1;
-        }
-        bb = c.z;
-        bmx = int(min(uabs(c.z), 0x7fffffffu));
-    }
-    int emn = t.eok ? t.e : INT_MAX, emx = t.eok ? t.e : INT_MIN;
-#pragma unroll
-    for (int o = 32; o; o >>= 1) {
-        emn = min(emn, __shfl_xor(emn, o));
-        emx = max(emx, __shfl_xor(emx, o));
-        smn = min(smn, __shfl_xor(smn, o));
-        smx = max(smx, __shfl_xor(smx, o));
-        bad |= __shfl_xor(bad, o);
-        bmx = max(bmx, __shfl_xor(bmx, o));
-        nofold |= __shfl_xor(nofold, o);
-        um = max(um, __shfl_xor(um, o));
-        if constexpr (NEEDLUT) lbad |= __shfl_xor(lbad, o);
-    }
-    if (tid == 0) {
-        sh.flag[0] = INT_MAX; sh.flag[1] = INT_MIN; sh.flag[2] = INT_MAX; sh.flag[3] = INT_MIN;
-        sh.flag[4] = 0; sh.flag[5] = 0; sh.flag[6] = 0; sh.flag[7] = 0;
-        sh.umax = 0;
-    }
+    double ms = 0.0, wmv = 0.0;
+    const int bb = t.cok ? t.c.z : 0;
+    if (t.cok) setup_column(p, t.c, ms, wmv, sp);
+    if (t.eok) { sp.emn = t.e; sp.emx = t.e; }
+    setup_publish(sh, sp);
     if constexpr (EPI == EPI_PLAIN_GN) gn_clear(p, t.m0, sh);
-    __syncthreads();   // raw table read by everyone, flags reset
-    // ---- phase 2: tables, expanded GELU table, flags
-    if (tid < BN) { sh.ms[tid] = ms; sh.wm[tid] = wmv; sh.b[tid] = bb; }
+    __syncthreads();   // raw table read by everyone, every wave's slot in
+    // ---- phase 2: the block's forms, the column tables (with the e == 0 FMA constant: wm + 1/2, and
+    // + b when folded, exact as above) and the expanded GELU table
+    const EpiFlags f = setup_flags<NEEDLUT, NT / 64>(sh);
+    if (tid < BN) {
+        sh.ms[tid] = ms;
+        sh.wm[tid] = f.ezero ? (wmv + 0.5) + (f.fold ? double(bb) : 0.0) : wmv;
+        sh.b[tid] = bb;
+    }
     if constexpr (NEEDLUT) {
 #pragma unroll
         for (int q = 0; q < LPT; ++q) {
@@ -475,27 +467,7 @@ __device__ __forceinline__ EpiFlags epi_setup(const GemmParams& p, const TilePre
             if (i < 2050) sh.lut[i] = lv[q];
         }
     }
-    if (lane == 0) {
-        if (emn <= emx) { atomicMin(&sh.flag[0], emn); atomicMax(&sh.flag[1], emx); }
-        if (smn <= smx) { atomicMin(&sh.flag[2], smn); atomicMax(&sh.flag[3], smx); }
-        if (bad) atomicOr(&sh.flag[4], 1);
-        if (lbad) atomicOr(&sh.flag[5], 1);
-        atomicMax(&sh.flag[6], bmx);
-        if (nofold) atomicOr(&sh.flag[7], 1);
-        atomicMax(&sh.umax, __double_as_longlong(um));
-    }
     __syncthreads();
-    const i64 emin = sh.flag[0], emax = sh.flag[1], smin = sh.flag[2], smax = sh.flag[3];
-    EpiFlags f;
-    f.fast = !sh.flag[4] && (smin - emax >= 1) && (smax - emin <= 52) && emin >= -1000 && emax <= 1000;
-    if (NEEDLUT && sh.flag[5]) f.fast = false;
-    f.ezero = emin > emax || (emin == 0 && emax == 0);
-    f.fold = f.fast && f.ezero && !sh.flag[7] && __longlong_as_double(sh.umax) + double(sh.flag[6]) + 2.0 < 2147483647.0;
-    if (f.ezero) {
-        // the FMA constant of the e == 0 forms: wm + 1/2, and + b when folded (exact, see above)
-        if (tid < BN) sh.wm[tid] = (sh.wm[tid] + 0.5) + (f.fold ? double(sh.b[tid]) : 0.0);
-        __syncthreads();
-    }
     return f;
 }
 
