@@ -96,7 +96,7 @@ def time_graphed(fn, stream, reps, replays):
 
 def pmc_traffic():
     """HBM bytes per launch of the C2 kernel from the committed rocprofv3 counter summary, if present."""
-    p = ROOT / "profiles" / "stripe_kernel_c2_geglu_pmc.json"
+    p = ROOT / "profiles" / "stripe16_kernel_c2_geglu_pmc.json"
     if p.exists():
         try:
             d = json.loads(p.read_text())
@@ -541,7 +541,7 @@ def main():
     vendor_c2 = vendor_planar_us(L, stream, args.steps, args.warmup)
     roof = roofline(L.ops, L.hbm_bytes, ms * 1e-3)
     roof["traffic"] = traffic
-    roof.update({"traffic_source": traffic_src, "kernel": "vk::stripe_kernel<SRC_I16, EPI_GEGLU>",
+    roof.update({"traffic_source": traffic_src, "kernel": "vk::stripe16_kernel<SRC_I16, EPI_GEGLU>",
                  "algorithmic_ops_per_launch": L.ops, "algorithmic_bytes_per_launch": L.hbm_bytes,
                  "mfma_frac": round(tops / PEAK_INT8_TOPS, 4),
                  "hbm_frac": round(L.hbm_bytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)})
