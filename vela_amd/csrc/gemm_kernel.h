@@ -1418,17 +1418,28 @@ __global__ void __launch_bounds__(256) splitk_epilogue_kernel(const GemmParams p
                 }
             };
             int y[4] = {0, 0, 0, 0};
+            // the column constants of the thread's columns, loaded together ahead of the sums (columns
+            // past the output read zeros and are not stored)
+            constexpr int NC = EPI == EPI_GEGLU ? 8 : 4;
+            int4 cs[NC];
+            {
+                const __amdgpu_buffer_rsrc_t rC = make_rsrc(p.cst, unsigned(p.Nreal) * 16u);
+                const int cb0 = EPI == EPI_GEGLU ? 2 * c0 : c0;
+#pragma unroll
+                for (int j = 0; j < NC; ++j) {
+                    const v4i t = bload16(rC, cb0 + j < p.Nreal ? unsigned(cb0 + j) * 16u : OOB);
+                    cs[j] = make_int4(t[0], t[1], t[2], t[3]);
+                }
+            }
             if constexpr (EPI == EPI_GEGLU) {
                 v4i h0, l0, h1, l1;
                 sum4(2 * c0, h0, l0);       // columns a0 g0 a1 g1
                 sum4(2 * c0 + 4, h1, l1);   // columns a2 g2 a3 g3
 #pragma unroll
                 for (int v = 0; v < 4; ++v) {
-                    const int c = c0 + v;
-                    if (c >= nout) break;
                     const int ah = v < 2 ? h0[2 * v] : h1[2 * v - 4], al = v < 2 ? l0[2 * v] : l1[2 * v - 4];
                     const int gh = v < 2 ? h0[2 * v + 1] : h1[2 * v - 3], gl = v < 2 ? l0[2 * v + 1] : l1[2 * v - 3];
-                    const int4 ca = p.cst[2 * c], cg = p.cst[2 * c + 1];
+                    const int4 ca = cs[2 * v], cg = cs[2 * v + 1];
                     y[v] = geglu_exact(epi1_exact(ah, al, ca.x, ca.y, ca.z, ca.w, er), epi1_exact(gh, gl, cg.x, cg.y, cg.z, cg.w, er), p.Lphi);
                 }
             } else {
@@ -1436,9 +1447,7 @@ __global__ void __launch_bounds__(256) splitk_epilogue_kernel(const GemmParams p
                 sum4(c0, h, l);
 #pragma unroll
                 for (int v = 0; v < 4; ++v) {
-                    const int c = c0 + v;
-                    if (c >= nout) break;
-                    const int4 cc = p.cst[c];
+                    const int4 cc = cs[v];
                     int yy = epi1_exact(h[v], l[v], cc.x, cc.y, cc.z, cc.w, er);
                     if constexpr (EPI == EPI_GELU) yy = gelu_exact(yy, p.Lphi);
                     y[v] = yy;
