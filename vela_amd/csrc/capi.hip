@@ -196,15 +196,16 @@ void stripe_grid(vk::GemmParams& p) {
 //  * 128x128 tiles win for wide, shallow GEMMs (N >= 960, K <= 1280) with plenty of tiles, where the
 //    epilogue dominates and the larger tile halves its fixed per-tile cost;
 //  * deep K with few tiles splits K so that all tiles' splits fill one round of blocks (two per CU
-//    for 128x128, three for 64x128) with at least 16 K steps per split: very few rows (<= 128
-//    64x128 tiles, K >= 4096) run 64x128 tiles in up to six splits, fewer than 256 128x128 tiles
-//    with K >= 8192 run 128x128 tiles; the int32 partials are reduced in a second pass.
+//    for 128x128, three for 64x128) with at least 16 K steps per split: few rows (at most 192
+//    64x128 tiles, three quarters of the CUs, K >= 4096) run 64x128 tiles in up to six splits (the
+//    stride-2 2048x5760x640 conv, 160 tiles: 49.3 -> 35.0 us in three splits), fewer than 256
+//    128x128 tiles with K >= 8192 run 128x128 tiles; the int32 partials are reduced in a second pass.
 enum SplitRule { SPLIT_NONE, SPLIT_SMALL, SPLIT_DEEP };
 
 SplitRule split_rule(int M, int N, int Kp) {
     const long long tiles0 = (long long)cdiv(M, TILES[0].BM) * cdiv(N, TILES[0].BN);
     const long long tiles1 = (long long)cdiv(M, TILES[1].BM) * cdiv(N, TILES[1].BN);
-    if (Kp >= 4096 && tiles1 <= 128) return SPLIT_SMALL;
+    if (Kp >= 4096 && tiles1 <= 3 * NCU / 4) return SPLIT_SMALL;
     if (Kp >= 8192 && tiles0 < NCU) return SPLIT_DEEP;
     return SPLIT_NONE;
 }
