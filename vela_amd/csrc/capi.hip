@@ -162,22 +162,39 @@ bool kwave_applies(int src, int epi, const vk::GemmParams& p) {
 // 512 x 1280 x 2560 linears 23.3 -> 21.0 us; wider or taller shapes stay on the tiled kernels).
 bool kwave_auto(const vk::GemmParams& p) { return p.Mreal <= 640 && p.Nreal <= 1280 && p.Kp >= 1024; }
 
-// Automatic use: many rows (the kernel keeps a block's rows in registers and streams all of its
-// columns, so it needs a few hundred row stripes to fill the GPU) and no per-row shifts (rows with
-// e != 0 leave the kernel's integer epilogue for its slow int64 form; the tile kernels cover them).
-// Residual calls qualify: the kernel loads a batch's residuals ahead of its arithmetic (UNet
-// 32768 x 320 x 320 residual layers: 23.1 us against 28.0 us on the tile kernels).
-bool stripe_auto(const vk::GemmParams& p) { return cdiv(p.Mreal, STRIPE_BM) >= 2 * NCU / 4 && p.Mreal >= 16384 && !p.e; }
-
 // Blocks = row stripes x column ranges: as few column ranges as the table allows, raised until
-// there are two blocks per CU.
-constexpr int STRIPE_PRIO_PCT = 55;
-void stripe_grid(vk::GemmParams& p) {
+// there are two blocks per CU. Returns the column ranges and the chunks of each.
+void stripe_ranges(const vk::GemmParams& p, int& cs, int& kper) {
     const int nch = cdiv(p.Nreal, STRIPE_CH);
     const int mt = cdiv(p.Mreal, STRIPE_BM);
-    int cs = std::max(cdiv(nch, STRIPE_NCOLS / STRIPE_CH), std::min(nch, cdiv(2 * NCU, mt)));
-    const int kper = cdiv(nch, cs);
+    cs = std::max(cdiv(nch, STRIPE_NCOLS / STRIPE_CH), std::min(nch, cdiv(2 * NCU, mt)));
+    kper = cdiv(nch, cs);
     cs = cdiv(nch, kper);
+}
+
+// Automatic use, with no per-row shifts (rows with e != 0 leave the kernels' integer epilogue for
+// their slow int64 form; the tile kernels cover them):
+//  * many rows (a block keeps its rows in registers and streams its columns, so the kernels need a
+//    few hundred row stripes to fill the GPU); residual calls qualify, the kernel loading a batch's
+//    residuals ahead of its arithmetic (UNet 32768 x 320 x 320 residual layers: 23.1 us against
+//    28.0 us on the tile kernels);
+//  * or a grid of at most one block per CU (few rows: each block then one or a few chunks), where
+//    the row-stationary set-up is shorter than the tile kernels' (C1 4096 x 320 x 320 7.40 -> 7.14 us,
+//    1024..2048 x 320 x 320..1280 4 % faster; grids of 320 blocks stay on the tile kernels, which are
+//    faster there: 4096 x 320 x 640 8.8 against 10.5 us).
+bool stripe_auto(const vk::GemmParams& p) {
+    if (p.e) return false;
+    if (cdiv(p.Mreal, STRIPE_BM) >= 2 * NCU / 4 && p.Mreal >= 16384) return true;
+    int cs, kper;
+    stripe_ranges(p, cs, kper);
+    return (long long)cdiv(p.Mreal, STRIPE_BM) * cs <= NCU;
+}
+
+constexpr int STRIPE_PRIO_PCT = 55;
+void stripe_grid(vk::GemmParams& p) {
+    const int mt = cdiv(p.Mreal, STRIPE_BM);
+    int cs, kper;
+    stripe_ranges(p, cs, kper);
     p.mtiles = mt;
     p.ntiles = cs;
     p.kper = kper;
