@@ -18,9 +18,11 @@ namespace vk {
 
 using TileKW = Tile<64, 64, 4, 1>;   // the epilogue's view: wave w owns rows 16 w .. 16 w + 15, all 64 columns
 
-template <int EPI>
+// PL planes of partial sums exchanged at once: both for the one-block-per-CU int16 sources, one at a
+// time for int8 planes (two blocks per CU share the LDS)
+template <int EPI, int PL>
 struct KwShared {
-    v4i red[4][3][4][64];   // [owner wave][other wave][column subtile][lane]: one plane of partial sums at a time
+    v4i red[PL][4][3][4][64];   // [plane][owner wave][other wave][column subtile][lane]: partial sums
     EpiShared<64, EPI == EPI_GEGLU || EPI == EPI_GELU, false> sh;
 };
 
@@ -38,7 +40,8 @@ template <int SRC, int EPI>
 __global__ void __launch_bounds__(256, SRC == SRC_I8 ? 2 : 1) kwave_kernel(const GemmParams p) {
     constexpr int NS = 4, MS = 4;
     constexpr bool NEEDLUT = EPI == EPI_GEGLU || EPI == EPI_GELU;
-    __shared__ __attribute__((aligned(16))) KwShared<EPI> s;
+    constexpr int PL = SRC == SRC_I8 ? 1 : 2;
+    __shared__ __attribute__((aligned(16))) KwShared<EPI, PL> s;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int fr = lane & 15, fg = lane >> 4;
@@ -188,15 +191,33 @@ __global__ void __launch_bounds__(256, SRC == SRC_I8 ? 2 : 1) kwave_kernel(const
     };
 
     // ---- K loop over this wave's steps kt = wave, wave + 4, ...: two operand sets in flight
-    // (ping-pong buffers, no register copies, so each step waits only for its own loads)
+    // (ping-pong buffers, no register copies, so each step waits only for its own loads). For the
+    // int16 sources (one block per CU, registers to spare) the epilogue's set-up (its column and row
+    // tests, the expanded table) runs after the first step's MFMAs, while the later steps' operands
+    // are in flight: the first step's loads were issued after the table DMA and the set-up's own
+    // inputs, and loads complete in order, so those are in by then. The int8 planes' kernel (two
+    // blocks per CU) runs it after the K loop.
+    constexpr bool EARLY = SRC != SRC_I8;
+    EpiFlags fl;
     {
         v4i wa[NS], wb[NS];
         KwA<SRC> aa, ab;
         if (wave < nK) { load_w(wave, wa); load_a(wave, aa); }
         if (wave + 4 < nK) { load_w(wave + 4, wb); load_a(wave + 4, ab); }
+        if (EARLY) {
+            if (wave < nK) {
+                compute(wa, aa);
+                if (wave + 8 < nK) { load_w(wave + 8, wa); load_a(wave + 8, aa); }
+            } else {
+                vm_wait<0>();   // no K step: the table DMA alone
+            }
+            fl = epi_setup<EPI, SRC, 64, 64, 256>(p, pre, L2048, s.sh);
+        }
         for (int kt = wave; kt < nK; kt += 8) {
-            compute(wa, aa);
-            if (kt + 8 < nK) { load_w(kt + 8, wa); load_a(kt + 8, aa); }
+            if (!EARLY || kt > wave) {
+                compute(wa, aa);
+                if (kt + 8 < nK) { load_w(kt + 8, wa); load_a(kt + 8, aa); }
+            }
             if (kt + 4 < nK) {
                 compute(wb, ab);
                 if (kt + 12 < nK) { load_w(kt + 12, wb); load_a(kt + 12, ab); }
@@ -204,19 +225,19 @@ __global__ void __launch_bounds__(256, SRC == SRC_I8 ? 2 : 1) kwave_kernel(const
         }
     }
 
-    // ---- reduce-scatter: wave w ends with the sums of column subtiles ns and row subtile w
+    // ---- reduce-scatter (both planes at once, or one at a time): wave w ends with the sums of
+    // column subtiles ns and row subtile w
     v4i fin_h[NS][1], fin_l[NS][1];
-#pragma unroll
-    for (int ns = 0; ns < NS; ++ns) { fin_h[ns][0] = v4i{0, 0, 0, 0}; fin_l[ns][0] = v4i{0, 0, 0, 0}; }
-    auto scatter = [&](v4i (&acc)[NS][MS], v4i (&fin)[NS][1]) {
+    auto scatter = [&](v4i (&acc)[NS][MS], v4i (&fin)[NS][1], int pl) {
 #pragma unroll
         for (int ms = 0; ms < MS; ++ms)
             if (ms != wave) {
                 const int slot = wave - (wave > ms ? 1 : 0);
 #pragma unroll
-                for (int ns = 0; ns < NS; ++ns) s.red[ms][slot][ns][lane] = acc[ns][ms];
+                for (int ns = 0; ns < NS; ++ns) s.red[pl][ms][slot][ns][lane] = acc[ns][ms];
             }
-        __syncthreads();
+    };
+    auto gather = [&](v4i (&acc)[NS][MS], v4i (&fin)[NS][1], int pl) {
 #pragma unroll
         for (int ms = 0; ms < MS; ++ms)
             if (ms == wave)
@@ -224,22 +245,36 @@ __global__ void __launch_bounds__(256, SRC == SRC_I8 ? 2 : 1) kwave_kernel(const
                 for (int ns = 0; ns < NS; ++ns) {
                     v4i t = acc[ns][ms];
 #pragma unroll
-                    for (int o = 0; o < 3; ++o) t += s.red[ms][o][ns][lane];
+                    for (int o = 0; o < 3; ++o) t += s.red[pl][ms][o][ns][lane];
                     fin[ns][0] = t;
                 }
-        __syncthreads();
     };
-    scatter(acc_h, fin_h);
-    scatter(acc_l, fin_l);
+    if constexpr (PL == 2) {
+        scatter(acc_h, fin_h, 0);
+        scatter(acc_l, fin_l, 1);
+        __syncthreads();
+        gather(acc_h, fin_h, 0);
+        gather(acc_l, fin_l, 1);
+    } else {
+        scatter(acc_h, fin_h, 0);
+        __syncthreads();
+        gather(acc_h, fin_h, 0);
+        __syncthreads();
+        scatter(acc_l, fin_l, 0);
+        __syncthreads();
+        gather(acc_l, fin_l, 0);
+    }
 
-    // the table DMA above is outside the compiler's counts: wait for it before the set-up reads it
-    if constexpr (NEEDLUT) vm_wait<0>();
-    __syncthreads();
+    if constexpr (!EARLY) {
+        // the table DMA above is outside the compiler's counts: wait for it before the set-up reads it
+        if constexpr (NEEDLUT) vm_wait<0>();
+        __syncthreads();
+        fl = epi_setup<EPI, SRC, 64, 64, 256>(p, pre, L2048, s.sh);
+    }
     int er[1] = {0};
 #pragma unroll
     for (int ms = 0; ms < MS; ++ms)
         if (ms == wave) er[0] = er4[ms];
-    const EpiFlags fl = epi_setup<EPI, SRC, 64, 64, 256>(p, pre, L2048, s.sh);
     fused_epilogue<EPI, SRC, TileKW>(p, fin_h, fin_l, m0 + 16 * wave, n0, 0, s.sh, fl, er);
 }
 
