@@ -73,6 +73,8 @@ def test_stripe_epilogues(epi, K):
         ("left shifts", dict(s_range=(-6, 3), m_range=(1, 1 << 10), e_max=5)),
         ("deep shifts", dict(s_range=(50, 70))),
         ("wrapping m", dict(s_range=(20, 40), m_range=((1 << 30), (1 << 31) - 1))),
+        # 2 |m| >= 2^s with no possible saturation at Kp = 320: the int64 form
+        ("m at 2^(s-1)", dict(s_range=(16, 16), m_range=(1 << 15, 50000))),
     ]
     for i, (name, kw) in enumerate(forms):
         Case(vg.SRC_I16, 384, 256, K, epi=epi, seed=80 + i, rowmax=True, residual=epi == vg.EPI_PLAIN, **kw).check(what=f"{name} epi {epi} K {K}")

@@ -172,25 +172,25 @@ __global__ void __launch_bounds__(512, 4) stripe16_kernel(const GemmParams p) {
             int y;
             unsigned ay;
             if constexpr (GEGLU) {
-                const int yg = stripe_req(X[u + NSUB / 2][v], k.kg[u]);
+                const int yg = stripe_req<NEEDLUT>(X[u + NSUB / 2][v], k.kg[u]);
                 unsigned h0;
                 const int ge = stripe_mulsh16(yg, stripe_phi(sh.lut, yg), h0);
                 // (ya ge + 2^15) >> 16 with 2^47 added: hb is the high word + 2^15, at most 65535
                 // exactly when y fits in int32; otherwise y saturates to the product's sign
                 unsigned hb;
-                unsigned yb = stripe_mulsh16b(stripe_req(X[u][v], k.ka[u]), ge, hb);
+                unsigned yb = stripe_mulsh16b(stripe_req<NEEDLUT>(X[u][v], k.ka[u]), ge, hb);
                 asm("" : "+v"(hb));   // keep the tests on the 32-bit high word
                 yb = hb > 65535u ? ~unsigned(int(hb) >> 31) : yb;   // biased INT_MAX / INT_MIN
                 y = int(yb ^ 0x80000000u);
                 // |y| = |(y ^ 2^31) - 2^31| as an unsigned difference, also for INT_MIN
                 if constexpr (RMAX) asm("v_sad_u32 %0, %1, %2, 0" : "=v"(ay) : "v"(yb), "s"(0x80000000u));
             } else if constexpr (EPI == EPI_GELU) {
-                const int ya = stripe_req(X[u][v], k.ka[u]);
+                const int ya = stripe_req<NEEDLUT>(X[u][v], k.ka[u]);
                 unsigned h0;
                 y = stripe_mulsh16(ya, stripe_phi(sh.lut, ya), h0);
                 ay = unsigned(max(y, int(0u - unsigned(y))));
             } else {
-                y = stripe_req(X[u][v], k.ka[u]);
+                y = stripe_req<NEEDLUT>(X[u][v], k.ka[u]);
                 ay = unsigned(max(y, int(0u - unsigned(y))));
             }
             const unsigned soff = unsigned(v) * ldy4;
@@ -202,20 +202,28 @@ __global__ void __launch_bounds__(512, 4) stripe16_kernel(const GemmParams p) {
 #pragma unroll
             for (int o = 0; o < NO; ++o) epi_one(k, o, rmax, full);
         };
-        // the MFMAs of the chunk in LDS stage `stage`, subtile by subtile, folded into X
+        // the MFMAs of the chunk in LDS stage `stage`, two subtiles at a time (four independent
+        // accumulator chains per K step; all four subtiles at once would not fit in the registers),
+        // folded into X
         auto mfma_chunk = [&](int stage) __attribute__((always_inline)) {
             const unsigned char* sW = sh.w[stage];
+            static_assert(NSUB % 2 == 0, "subtile pairs");
 #pragma unroll
-            for (int u = 0; u < NSUB; ++u) {
-                v4i ah = vzero, al = vzero;
+            for (int h = 0; h < NSUB; h += 2) {
+                v4i ah[2] = {vzero, vzero}, al[2] = {vzero, vzero};
 #pragma unroll
                 for (int t = 0; t < NKS; ++t) {
-                    const v4i wf = wfrag(sW, t, u);
-                    ah = __builtin_amdgcn_mfma_i32_16x16x64_i8(hf[t], wf, ah, 0, 0, 0);
-                    al = __builtin_amdgcn_mfma_i32_16x16x64_i8(lf[t], wf, al, 0, 0, 0);
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) {
+                        const v4i wf = wfrag(sW, t, h + j);
+                        ah[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(hf[t], wf, ah[j], 0, 0, 0);
+                        al[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(lf[t], wf, al[j], 0, 0, 0);
+                    }
                 }
 #pragma unroll
-                for (int v = 0; v < 4; ++v) X[u][v] = (ah[v] << 8) + al[v];
+                for (int j = 0; j < 2; ++j)
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) X[h + j][v] = (ah[j][v] << 8) + al[j][v];
                 __builtin_amdgcn_sched_barrier(0);
             }
         };

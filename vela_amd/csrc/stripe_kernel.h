@@ -17,7 +17,9 @@
 //  * integer: every row has e == 0, every shift s lies in [0, 31] and no element can saturate
 //    (checked from max |m| 2^-s and max |b|). Then y = (A m + C) >> s with A = 256 Chi + Clo
 //    (int32, Kp <= 496) and C = 128 wsum m + 2^(s-1) + b 2^s, one v_mad_i64_i32 and one funnel
-//    shift; GELU/GEGLU take phi(g) from the table as (1024 L[i] + (L[i+1] - L[i]) f) >> 10, then
+//    shift; for GELU/GEGLU, whose epilogue is VALU-bound, 2 |m| < 2^s as well (the reference's
+//    multipliers lie in [2^14, 2^15), its shifts at 16 and above), and y is the high word of one
+//    v_mad_i64_i32 of A, m 2^(32-s) and C 2^(32-s) (the table holds both pre-shifted); GELU/GEGLU take phi(g) from the table as (1024 L[i] + (L[i+1] - L[i]) f) >> 10, then
 //    ge = (g phi + 2^15) >> 16 (never saturates, phi <= 65536) and y = sat32((a ge + 2^15) >> 16).
 //  * otherwise the reference's int64 formula element by element (one element per loop iteration,
 //    so that this rarely used form adds few registers to the kernel). The host sends calls with
@@ -68,7 +70,7 @@ struct StripeCfg {
 template <bool LUT>
 struct StripeShared {
     unsigned char w[2][StripeCfg::STAGE];
-    int4 tab[StripeCfg::NCOLS];   // per column {m, s, C lo, C hi} of the integer form
+    int4 tab[StripeCfg::NCOLS];   // per column {m, s, C lo, hi} of the integer form (GELU/GEGLU: m and C times 2^(32-s))
     // lut[i + 1] = (1024 L[i] - d 1024 (i - 1024) mod 2^32, d = L[i+1] - L[i]); lut[0] below, lut[2049]
     // above the table: 1024 phi(x) = lut[j].x + lut[j].y x (mod 2^32) for x in entry j's range
     int2 lut[LUT ? 2050 : 1];
@@ -118,8 +120,8 @@ __device__ __forceinline__ void stripe_lut_dma(const GemmParams& p, StripeShared
 
 // Once the column constants, the raw table and the row shifts are in: the expanded GELU table, the
 // integer form's column table and the block's epilogue form (uniform), which is the integer form
-// when every row has e = 0 and every column satisfies, with 32-bit tests: 0 <= s <= 31, |m| Kp <
-// 2^30, |wsum| <= 128 Kp, |b| < 2^30 and 2^22 Kp |m| 2^-s < 2^30 (so that no element saturates:
+// when every row has e = 0 and every column satisfies, with 32-bit tests: 0 <= s <= 31 (GELU/GEGLU:
+// 2 |m| < 2^s), |m| Kp < 2^30, |wsum| <= 128 Kp, |b| < 2^30 and 2^22 Kp |m| 2^-s < 2^30 (so that no element saturates:
 // |y| <= 2^22 Kp |m| 2^-s + 1 + |b| < 2^31, as |acc| <= 32768 * 128 * Kp), and the table lies in
 // [0, 65536]. Each thread tests its own columns, rows and table entries; a ballot per wave and one
 // LDS word per wave carry the result through the barrier that the table expansion needs anyway.
@@ -165,7 +167,11 @@ __device__ __forceinline__ int stripe_setup(const GemmParams& p, StripeShared<EP
         // 2^22 Kp |m| 2^-s < 2^30  <=>  Kp |m| < 2^(8 + s), with Kp |m| < 2^30
         // (for s >= 23 the shift by 31 holds too, as Kp |m| < 2^30)
         const bool umok = am < mlim && ((am * unsigned(p.Kp)) >> (sok ? min(8 + c.y, 31) : 0)) == 0u;
-        bad |= !(sok && umok && uabs(c.w) <= 128u * unsigned(p.Kp) && uabs(c.z) < (1u << 30));
+        // GELU/GEGLU: 2 |m| < 2^s, so that m 2^(32-s) fits in int32: the table then holds the
+        // multiplier and the constant pre-shifted by 32 - s and the result is the high word of the
+        // product (s = 0 passes with m = 0 only, as in the unused slots)
+        const bool hiok = !NEEDLUT || (sok && (u64(am) << 1) < (u64(1) << c.y));
+        bad |= !(sok && umok && hiok && uabs(c.w) <= 128u * unsigned(p.Kp) && uabs(c.z) < (1u << 30));
     }
     if (tid < BM) {
         sh.erow[tid] = erv;
@@ -192,9 +198,13 @@ __device__ __forceinline__ int stripe_setup(const GemmParams& p, StripeShared<EP
             const int j = tid + NT * q;
             if (j < ncols) {
                 const int4 c = cc[q];
-                // C = 128 wsum m + 2^(s-1) + b 2^s (|C| < 2^63: |wsum| <= 128 Kp, s <= 31)
+                // C = 128 wsum m + 2^(s-1) + b 2^s (|C| < 2^63: |wsum| <= 128 Kp, s <= 31); GELU/GEGLU:
+                // the multiplier and C times 2^(32-s) (C's product wraps modulo 2^64; m = 0 when s = 0)
                 const i64 C = 128LL * i64(c.w) * i64(c.x) + (c.y ? (1LL << (c.y - 1)) : 0) + i64(c.z) * (1LL << c.y);
-                sh.tab[j] = make_int4(c.x, c.y, int(unsigned(u64(C))), int(unsigned(u64(C) >> 32)));
+                const int sh32 = NEEDLUT ? 32 - c.y : 0;
+                const u64 Cs = u64(C) << sh32;
+                const unsigned ms = sh32 < 32 ? unsigned(c.x) << sh32 : 0u;
+                sh.tab[j] = make_int4(int(ms), c.y, int(unsigned(Cs)), int(unsigned(Cs >> 32)));
             }
         }
     }
@@ -270,10 +280,14 @@ __device__ __forceinline__ unsigned stripe_mulsh16b(int a, int b, unsigned& hi) 
     hi = unsigned(u64(t) >> 32);
     return __builtin_amdgcn_alignbit(hi, unsigned(u64(t)), 16);
 }
-// the integer requantisation (A m + C) >> s of an element with table entry k = {m, s, C lo, C hi},
-// exact when it fits in int32
+// the integer requantisation (A m + C) >> s of an element, exact when it fits in int32. HI (the
+// GELU/GEGLU tables): table entry k = {m 2^(32-s), s, C 2^(32-s) lo, hi} with 2 |m| < 2^s, whose
+// product's high word is the result (bits s..s+31 of A m + C are bits 32..63 of (A m + C) 2^(32-s),
+// also modulo 2^64); otherwise k = {m, s, C lo, hi} and a funnel shift by s
+template <bool HI>
 __device__ __forceinline__ int stripe_req(int A, const int4& k) {
     const i64 t = i64(A) * i64(k.x) + i64((u64(unsigned(k.w)) << 32) | unsigned(k.z));
+    if constexpr (HI) return int(unsigned(u64(t) >> 32));
     return int(__builtin_amdgcn_alignbit(unsigned(u64(t) >> 32), unsigned(u64(t)), unsigned(k.y)));
 }
 
@@ -391,7 +405,7 @@ __global__ void __launch_bounds__(256, 2) stripe_kernel(const GemmParams p) {
     auto phi = [&](int x) -> int { return stripe_phi(sh.lut, x); };
     auto mulsh16 = [&](int a, int b, unsigned& hi) -> int { return stripe_mulsh16(a, b, hi); };
     auto mulsh16b = [&](int a, int b, unsigned& hi) -> unsigned { return stripe_mulsh16b(a, b, hi); };
-    auto req = [&](int A, const int4& k) -> int { return stripe_req(A, k); };
+    auto req = [&](int A, const int4& k) -> int { return stripe_req<NEEDLUT>(A, k); };
 
     bool pipelined = false;
     if constexpr (!RES && !VIEW) {
@@ -479,7 +493,7 @@ __global__ void __launch_bounds__(256, 2) stripe_kernel(const GemmParams p) {
             // otherwise: the 16 outputs of subtile u), so only one subtile's accumulators are live.
             // W fragments are read PFB steps ahead of their MFMAs.
             constexpr int NO = NOUT * 16, NOH = NO / 2;
-            constexpr int VPM = GEGLU ? 10 : (EPI == EPI_GELU ? 7 : 4);
+            constexpr int VPM = GEGLU ? 8 : (EPI == EPI_GELU ? 7 : 4);
             constexpr int PFB = 2;
             auto wfrag = [&](const unsigned char* sW, int t, int u) __attribute__((always_inline)) {
                 return *reinterpret_cast<const v4i*>(sW + (t >> 1) * S::KSTEP + pswz(32 * u + lc, 2 * (t & 1) + lh));
