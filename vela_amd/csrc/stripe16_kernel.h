@@ -141,6 +141,7 @@ __global__ void __launch_bounds__(512, 4) stripe16_kernel(const GemmParams p) {
     // this lane's rows are rbase + 4 fg + v
     const unsigned rowoff = unsigned(rbase + 4 * fg) * ldy4;
     unsigned yabs[4] = {0u, 0u, 0u, 0u};   // running max |y| of the lane's four rows
+    int ymx[4] = {0, 0, 0, 0}, ymn[4] = {0, 0, 0, 0};   // GEGLU: running max and min of y (0 included)
     const bool lut_lds = NEEDLUT && lut_ok;
     const v4i vzero = {0, 0, 0, 0};
     // W fragment of K step t, subtile u of the chunk in LDS stage sW (B operand: lane column fr)
@@ -165,26 +166,13 @@ __global__ void __launch_bounds__(512, 4) stripe16_kernel(const GemmParams p) {
             }
             return k;
         };
-        // output o = 4 u + v of the chunk held in X: requantise, store, row maximum
+        // output o = 4 u + v of the chunk held in X (PLAIN, GELU): requantise, store, row maximum
         auto epi_one = [&](const EpiC& k, int o, auto rmax, auto full) __attribute__((always_inline)) {
             constexpr bool RMAX = decltype(rmax)::value, FULL = decltype(full)::value;
             const int u = o >> 2, v = o & 3;
             int y;
             unsigned ay;
-            if constexpr (GEGLU) {
-                const int yg = stripe_req<NEEDLUT>(X[u + NSUB / 2][v], k.kg[u]);
-                unsigned h0;
-                const int ge = stripe_mulsh16(yg, stripe_phi(sh.lut, yg), h0);
-                // (ya ge + 2^15) >> 16 with 2^47 added: hb is the high word + 2^15, at most 65535
-                // exactly when y fits in int32; otherwise y saturates to the product's sign
-                unsigned hb;
-                unsigned yb = stripe_mulsh16b(stripe_req<NEEDLUT>(X[u][v], k.ka[u]), ge, hb);
-                asm("" : "+v"(hb));   // keep the tests on the 32-bit high word
-                yb = hb > 65535u ? ~unsigned(int(hb) >> 31) : yb;   // biased INT_MAX / INT_MIN
-                y = int(yb ^ 0x80000000u);
-                // |y| = |(y ^ 2^31) - 2^31| as an unsigned difference, also for INT_MIN
-                if constexpr (RMAX) asm("v_sad_u32 %0, %1, %2, 0" : "=v"(ay) : "v"(yb), "s"(0x80000000u));
-            } else if constexpr (EPI == EPI_GELU) {
+            if constexpr (EPI == EPI_GELU) {
                 const int ya = stripe_req<NEEDLUT>(X[u][v], k.ka[u]);
                 unsigned h0;
                 y = stripe_mulsh16(ya, stripe_phi(sh.lut, ya), h0);
@@ -197,10 +185,63 @@ __global__ void __launch_bounds__(512, 4) stripe16_kernel(const GemmParams p) {
             __builtin_amdgcn_raw_buffer_store_b32(y, rY, int(FULL ? k.vbase[u] : k.vbase[u] + soff), FULL ? int(soff) : 0, 0);
             if constexpr (RMAX) yabs[v] = max(yabs[v], ay);
         };
-        auto epilogue = [&](int tb, int ocol0, auto rmax, auto full) __attribute__((always_inline)) {
-            const EpiC k = epi_consts(tb, ocol0);
+        // GEGLU: the chunk's outputs computed and stored without the saturation test: y is the low
+        // word of (ya ge + 2^15) >> 16, exact when the product's high word lies in [-2^15, 2^15).
+        // One test per four outputs (the high words' max and min, a ballot) sends the rare group with
+        // a product outside that range to a second pass that stores the saturated values again
+        // (a lane's stores to one address stay in order). The row maximum then follows from each
+        // row's max and min of y.
+        auto epilogue_geglu = [&](int tb, int ocol0, auto rmax, auto full) __attribute__((always_inline)) {
+            constexpr bool RMAX = decltype(rmax)::value, FULL = decltype(full)::value;
+            int yv[NO];
 #pragma unroll
-            for (int o = 0; o < NO; ++o) epi_one(k, o, rmax, full);
+            for (int u = 0; u < NOUT; ++u) {
+                // the lane's a and g table entries and output offset for this subtile pair
+                const StripeK3 ka = stripe_tab3(sh.tab, tb + 16 * u + fr), kg = stripe_tab3(sh.tab, tb + CH / 2 + 16 * u + fr);
+                const int ncol = ocol0 + 16 * u + fr;
+                const unsigned vbase = ncol < nlim ? rowoff + unsigned(ncol) * 4u : OOB;
+                auto store = [&](int y, int v) __attribute__((always_inline)) {
+                    const unsigned soff = unsigned(v) * ldy4;
+                    __builtin_amdgcn_raw_buffer_store_b32(y, rY, int(FULL ? vbase : vbase + soff), FULL ? int(soff) : 0, 0);
+                };
+                int hv[4];
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const int yg = stripe_req_hi(X[u + NSUB / 2][v], kg);
+                    unsigned h0, hi;
+                    const int ge = stripe_mulsh16(yg, stripe_phi(sh.lut, yg), h0);
+                    yv[4 * u + v] = stripe_mulsh16(stripe_req_hi(X[u][v], ka), ge, hi);
+                    hv[v] = int(hi);
+                    store(yv[4 * u + v], v);
+                }
+                const int hmx = max(max(hv[0], hv[1]), max(hv[2], hv[3]));
+                const int hmn = min(min(hv[0], hv[1]), min(hv[2], hv[3]));
+                if (__builtin_amdgcn_ballot_w64(hmx > 32767 || hmn < -32768)) {
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) {
+                        if (hv[v] > 32767 || hv[v] < -32768) {
+                            yv[4 * u + v] = (hv[v] >> 31) ^ 0x7fffffff;   // INT_MAX or INT_MIN, the product's sign
+                            store(yv[4 * u + v], v);
+                        }
+                    }
+                }
+            }
+            if constexpr (RMAX) {
+#pragma unroll
+                for (int o = 0; o < NO; ++o) {
+                    ymx[o & 3] = max(ymx[o & 3], yv[o]);
+                    ymn[o & 3] = min(ymn[o & 3], yv[o]);
+                }
+            }
+        };
+        auto epilogue = [&](int tb, int ocol0, auto rmax, auto full) __attribute__((always_inline)) {
+            if constexpr (GEGLU) {
+                epilogue_geglu(tb, ocol0, rmax, full);
+            } else {
+                const EpiC k = epi_consts(tb, ocol0);
+#pragma unroll
+                for (int o = 0; o < NO; ++o) epi_one(k, o, rmax, full);
+            }
         };
         // the MFMAs of the chunk in LDS stage `stage`, two subtiles at a time (four independent
         // accumulator chains per K step; all four subtiles at once would not fit in the registers),
@@ -259,7 +300,8 @@ __global__ void __launch_bounds__(512, 4) stripe16_kernel(const GemmParams p) {
             // lanes with the same fg hold the same four rows: reduce over the 16 columns, one atomic per row
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
-                unsigned m = yabs[v];
+                // GEGLU: |y| max from the max and min (0 - INT_MIN is 2^31 as unsigned)
+                unsigned m = GEGLU ? max(unsigned(ymx[v]), 0u - unsigned(ymn[v])) : yabs[v];
 #pragma unroll
                 for (int o = 1; o < 16; o <<= 1) m = max(m, unsigned(__shfl_xor(int(m), o)));
                 const int r = rbase + 4 * fg + v;

@@ -70,7 +70,7 @@ struct StripeCfg {
 template <bool LUT>
 struct StripeShared {
     unsigned char w[2][StripeCfg::STAGE];
-    int4 tab[StripeCfg::NCOLS];   // per column {m, s, C lo, hi} of the integer form (GELU/GEGLU: m and C times 2^(32-s))
+    int4 tab[StripeCfg::NCOLS];   // per column {m, C lo, C hi, s} of the integer form (GELU/GEGLU: m and C times 2^(32-s))
     // lut[i + 1] = (1024 L[i] - d 1024 (i - 1024) mod 2^32, d = L[i+1] - L[i]); lut[0] below, lut[2049]
     // above the table: 1024 phi(x) = lut[j].x + lut[j].y x (mod 2^32) for x in entry j's range
     int2 lut[LUT ? 2050 : 1];
@@ -204,7 +204,7 @@ __device__ __forceinline__ int stripe_setup(const GemmParams& p, StripeShared<EP
                 const int sh32 = NEEDLUT ? 32 - c.y : 0;
                 const u64 Cs = u64(C) << sh32;
                 const unsigned ms = sh32 < 32 ? unsigned(c.x) << sh32 : 0u;
-                sh.tab[j] = make_int4(int(ms), c.y, int(unsigned(Cs)), int(unsigned(Cs >> 32)));
+                sh.tab[j] = make_int4(int(ms), int(unsigned(Cs)), int(unsigned(Cs >> 32)), c.y);
             }
         }
     }
@@ -281,14 +281,24 @@ __device__ __forceinline__ unsigned stripe_mulsh16b(int a, int b, unsigned& hi) 
     return __builtin_amdgcn_alignbit(hi, unsigned(u64(t)), 16);
 }
 // the integer requantisation (A m + C) >> s of an element, exact when it fits in int32. HI (the
-// GELU/GEGLU tables): table entry k = {m 2^(32-s), s, C 2^(32-s) lo, hi} with 2 |m| < 2^s, whose
+// GELU/GEGLU tables): table entry k = {m 2^(32-s), C 2^(32-s) lo, hi, s} with 2 |m| < 2^s, whose
 // product's high word is the result (bits s..s+31 of A m + C are bits 32..63 of (A m + C) 2^(32-s),
-// also modulo 2^64); otherwise k = {m, s, C lo, hi} and a funnel shift by s
+// also modulo 2^64); otherwise k = {m, C lo, hi, s} and a funnel shift by s
 template <bool HI>
 __device__ __forceinline__ int stripe_req(int A, const int4& k) {
-    const i64 t = i64(A) * i64(k.x) + i64((u64(unsigned(k.w)) << 32) | unsigned(k.z));
+    const i64 t = i64(A) * i64(k.x) + i64((u64(unsigned(k.z)) << 32) | unsigned(k.y));
     if constexpr (HI) return int(unsigned(u64(t) >> 32));
-    return int(__builtin_amdgcn_alignbit(unsigned(u64(t) >> 32), unsigned(u64(t)), unsigned(k.y)));
+    return int(__builtin_amdgcn_alignbit(unsigned(u64(t) >> 32), unsigned(u64(t)), unsigned(k.w)));
+}
+// the first three words of a HI table entry (all that the high-word form reads)
+struct StripeK3 { int m, lo, hi; };
+__device__ __forceinline__ StripeK3 stripe_tab3(const int4* tab, int j) {
+    const int3 v = *reinterpret_cast<const int3*>(tab + j);
+    return {v.x, v.y, v.z};
+}
+__device__ __forceinline__ int stripe_req_hi(int A, const StripeK3& k) {
+    const i64 t = i64(A) * i64(k.m) + i64((u64(unsigned(k.hi)) << 32) | unsigned(k.lo));
+    return int(unsigned(u64(t) >> 32));
 }
 
 // RES: the PLAIN instantiation for calls with a residual (its own kernel, so that the residual
