@@ -277,10 +277,14 @@ __global__ void __launch_bounds__(512, 4) stripe16_kernel(const GemmParams p) {
             for (int c = cb; c < ce; ++c) {
                 prio_step(c);
                 const int stage = (c - cb) & 1;
-                // chunk c's DMA is done once at most the previous chunk's stores are outstanding
-                if (c == cb) vm_wait<0>();
-                else vm_wait<STORES>();
-                block_barrier();
+                // chunk c's DMA is done once at most the previous chunk's stores are outstanding.
+                // Chunk cb needs neither wait nor barrier: every wave's W DMA of chunk cb was
+                // complete before the set-up, which ends with a barrier, and the wave's own rows are
+                // in (split above), so each wave starts as soon as its rows are.
+                if (c > cb) {
+                    vm_wait<STORES>();
+                    block_barrier();
+                }
                 if (c + 1 < ce) issue(c + 1, stage ^ 1);
                 if (lagging && c > cb) epilogue((c - 1 - cb) * CH, GEGLU ? (c - 1) * (CH / 2) : (c - 1) * CH, rmax, full);
                 mfma_chunk(stage);
