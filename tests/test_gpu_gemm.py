@@ -288,6 +288,20 @@ def test_conv32_dma_tiles(geom, variant):
     c2.e = rng(44).integers(0, 18, c2.M).astype(np.int32)
     c2.e[::5] = 0
     c2.check(what=f"conv32 e {geom} v{variant}")
+    # shifts in [0, 16] only (whole waves take the three-instruction form), with values at and just
+    # below INT_MAX, where v + 2^(e-1) saturates, and INT_MIN + 1
+    c3 = Case(vg.SRC_CONV32, B * Ho * Wo, 192, 9 * C, seed=45 + C, conv=geom, residual=True)
+    big = rng(46).integers(-(2**31) + 1, 2**31, c3.img.shape, dtype=np.int64).astype(np.int32)
+    flat = big.reshape(-1)
+    flat[::7] = 2**31 - 1
+    flat[3::11] = 2**31 - 2**15
+    flat[5::13] = 2**31 - 3
+    flat[6::17] = -(2**31) + 1
+    c3.img = big
+    c3.kw["img"] = big
+    c3.e = rng(47).integers(0, 17, c3.M).astype(np.int32)
+    c3.e[::6] = 16
+    c3.check(what=f"conv32 e <= 16, extremes {geom} v{variant}")
 
 
 # (B, H, W, C) of stride-1 SRC_CONV16 problems that run the halo kernel (128-row tiles of whole

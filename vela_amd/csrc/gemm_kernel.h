@@ -129,6 +129,20 @@ __device__ __forceinline__ void quant_pack16(const v4i* x, int e, unsigned* d) {
     }
 }
 
+// quant16_32(v, e) for 0 <= e <= 16 in three instructions: with r = 2^(e-1) (0 for e = 0),
+// clamp(sat(v + r) >> e). Where v + r does not saturate, floor((v + r) / 2^e) is exactly
+// (v >> e) + ((v >> (e-1)) & 1); where it does, both forms clamp to 32767 (INT_MAX >> e >= 32767
+// for e <= 16). e = 17 (a row holding INT_MIN) keeps quant_pack16.
+__device__ __forceinline__ void quant_pack16_e16(const v4i* x, int e, unsigned* d) {
+    const int r = e > 0 ? 1 << (e - 1) : 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int q0 = min(max(__builtin_elementwise_add_sat(x[j >> 1][(2 * j) & 3], r) >> e, -32767), 32767);
+        const int q1 = min(max(__builtin_elementwise_add_sat(x[j >> 1][(2 * j + 1) & 3], r) >> e, -32767), 32767);
+        d[j] = __builtin_amdgcn_perm(unsigned(q1), unsigned(q0), 0x05040100u);
+    }
+}
+
 // 16 int32 values quantised with shift 0 (quant16_32(v, 0) = v clamped to +-32767), packed to int16 pairs
 __device__ __forceinline__ void clamp_pack16(const v4i* x, unsigned* d) {
 #pragma unroll
@@ -1119,6 +1133,11 @@ __global__ void __launch_bounds__(T::NT, (dma_waves_per_simd<T, EPI>())) gemm_dm
 #pragma unroll
     for (int ms = 0; ms < MS; ++ms) e_any |= er[ms] != 0;
     const bool wave_e0 = SRC == SRC_CONV16 || D::RAW32 ? __builtin_amdgcn_ballot_w64(e_any) == 0 : true;
+    // raw int32 rows: every row of the wave with e <= 16 (the three-instruction quantisation)
+    bool e_big = false;
+#pragma unroll
+    for (int ms = 0; ms < MS; ++ms) e_big |= er[ms] > 16;
+    const bool wave_e16 = D::RAW32 ? __builtin_amdgcn_ballot_w64(e_big) == 0 : true;
 
     v4i acc_h[NS][MS], acc_l[TWO ? NS : 1][TWO ? MS : 1];
 #pragma unroll
@@ -1144,6 +1163,7 @@ __global__ void __launch_bounds__(T::NT, (dma_waves_per_simd<T, EPI>())) gemm_dm
                 for (int q = 0; q < 4; ++q) x[q] = *reinterpret_cast<const v4i*>(sA + swz32(row, 4 * fg + q));
                 unsigned d[8];
                 if (wave_e0) clamp_pack16(x, d);
+                else if (wave_e16) quant_pack16_e16(x, er[ms], d);
                 else quant_pack16(x, er[ms], d);
                 split16x16(d, hf[ms], lf[ms]);
             } else if constexpr (D::RAW16) {
