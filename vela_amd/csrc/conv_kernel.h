@@ -45,6 +45,7 @@ inline bool halo_fits(int H, int W, int C, int stride, int Ho, int Wo) {
 
 template <int EPI>
 __global__ void __launch_bounds__(256, 2) conv_halo_kernel(const GemmParams p) {
+    prefetch_args();
     using HC = HaloCfg;
     constexpr int BM = HC::BM;
     using T = typename HC::T;

@@ -851,6 +851,15 @@ __device__ __forceinline__ void store_raw(const GemmParams& p, const v4i (&acc)[
 struct TileIdx {
     int ks, mt, nt;
 };
+// The kernel arguments, one 64-byte line at a time, in one round of scalar loads at kernel entry:
+// the argument block is read cold from memory, and the prologue's own argument loads sit between
+// branches, each round waiting for the last; with the lines in the scalar cache they hit.
+__device__ __forceinline__ void prefetch_args() {
+    static_assert(sizeof(GemmParams) <= 8 * 64, "eight lines of kernel arguments");
+    const auto k = (const __attribute__((address_space(4))) int*)__builtin_amdgcn_kernarg_segment_ptr();
+    asm volatile("" ::"s"(k[0]), "s"(k[16]), "s"(k[32]), "s"(k[48]), "s"(k[64]), "s"(k[80]), "s"(k[96]), "s"(k[112]));
+}
+
 __device__ __forceinline__ TileIdx tile_index(const GemmParams& p) {
     const int nblk = gridDim.x, bid = blockIdx.x;
     const int q8 = nblk >> 3, r8 = nblk & 7, xcd = bid & 7, slot = bid >> 3;
@@ -915,6 +924,7 @@ constexpr int dma_waves_per_simd() {
 
 template <int SRC, int EPI, class T>
 __global__ void __launch_bounds__(T::NT, (dma_waves_per_simd<T, EPI>())) gemm_dma_kernel(const GemmParams p) {
+    prefetch_args();
     using D = DmaCfg<SRC, EPI, T>;
     constexpr int BM = T::BM, BN = T::BN, MS = T::MS, NS = T::NS, NST = D::NST;
     constexpr bool TWO = D::TWO, FUSED = D::FUSED;
@@ -1231,6 +1241,7 @@ __global__ void __launch_bounds__(T::NT, (dma_waves_per_simd<T, EPI>())) gemm_dm
 
 template <int SRC, int EPI, class T>
 __global__ void __launch_bounds__(256) gemm_hl_kernel(const GemmParams p) {
+    prefetch_args();
     constexpr int BM = T::BM, BN = T::BN, MS = T::MS, NS = T::NS;
     constexpr bool FUSED = EPI != EPI_PARTIAL;
     constexpr bool NEEDLUT = EPI == EPI_GEGLU || EPI == EPI_GELU;
@@ -1414,6 +1425,7 @@ __global__ void __launch_bounds__(256) gemm_hl_kernel(const GemmParams p) {
 // partials of all K ranges and applies the exact int64 epilogue.
 template <int EPI>
 __global__ void __launch_bounds__(256) splitk_epilogue_kernel(const GemmParams p) {
+    prefetch_args();
     const int nout = EPI == EPI_GEGLU ? (p.Nreal >> 1) : p.Nreal;
     const int tpr = (nout + 3) >> 2;   // threads per row
     const unsigned total = unsigned(p.Mreal) * unsigned(tpr);

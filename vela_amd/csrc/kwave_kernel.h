@@ -38,6 +38,7 @@ struct KwA {
 // need the whole register file of one block per CU
 template <int SRC, int EPI>
 __global__ void __launch_bounds__(256, SRC == SRC_I8 ? 2 : 1) kwave_kernel(const GemmParams p) {
+    prefetch_args();
     constexpr int NS = 4, MS = 4;
     constexpr bool NEEDLUT = EPI == EPI_GEGLU || EPI == EPI_GELU;
     constexpr int PL = SRC == SRC_I8 ? 1 : 2;

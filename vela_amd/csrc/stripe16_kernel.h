@@ -55,6 +55,7 @@ __global__ void __launch_bounds__(512, 4) stripe16_kernel(const GemmParams p) {
 
     __shared__ __attribute__((aligned(16))) StripeShared<NEEDLUT> sh;
 
+    prefetch_args();
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int fr = lane & 15, fg = lane >> 4;   // MFMA column / row group of this lane
     const TileIdx ti = tile_index(p);

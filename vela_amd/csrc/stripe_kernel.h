@@ -306,6 +306,7 @@ __device__ __forceinline__ int stripe_req_hi(int A, const StripeK3& k) {
 // view loop below).
 template <int SRC, int EPI, bool RES = false, bool VIEW = false>
 __global__ void __launch_bounds__(256, 2) stripe_kernel(const GemmParams p) {
+    prefetch_args();
     using S = StripeCfg;
     constexpr int CH = S::CH, NKS = S::NKS, BM = S::BM;
     constexpr bool NEEDLUT = EPI == EPI_GEGLU || EPI == EPI_GELU;
