@@ -198,6 +198,21 @@ def test_i16_plain(variant, shape):
     Case(vg.SRC_I16, M, N, K, seed=7 + variant, s_range=(16, 24)).check(what=f"I16 {shape} v{variant}")
 
 
+# Shallow calls that the automatic dispatch sends to the row-stationary kernels by their tile count
+# (at least 960 tiles of 64x128, from 1024 rows, no residual): few rows over many columns, partial
+# row stripes and W chunks, K below 320, each epilogue; the residual call stays on the tile kernels.
+AUTO_MID = [(vg.SRC_I16, 8192, 960, 160, vg.EPI_PLAIN, False), (vg.SRC_I8, 1030, 9600, 320, vg.EPI_PLAIN, False),
+            (vg.SRC_I16, 4100, 2560, 320, vg.EPI_GEGLU, False), (vg.SRC_I16, 6150, 1288, 200, vg.EPI_GELU, False),
+            (vg.SRC_I16, 8192, 1280, 320, vg.EPI_PLAIN, True)]
+
+
+@pytest.mark.parametrize("case", AUTO_MID, ids=lambda c: f"{c[1]}x{c[2]}x{c[3]}-epi{c[4]}{'-res' if c[5] else ''}")
+def test_auto_shallow_tile_count(case):
+    src, M, N, K, epi, res = case
+    Case(src, M, N, K, epi=epi, seed=M % 101 + epi, residual=res, rowmax=M % 2 == 0, s_range=(16, 24)).check(
+        what=f"auto {M}x{N}x{K} epi {epi} res {res}")
+
+
 @pytest.mark.parametrize("epi", [vg.EPI_PLAIN, vg.EPI_GEGLU, vg.EPI_GELU])
 @pytest.mark.parametrize("variant", [0, 1, 2, 3])
 def test_i16_epilogues_rowmax(epi, variant):

@@ -181,10 +181,17 @@ void stripe_ranges(const vk::GemmParams& p, int& cs, int& kper) {
 //  * or a grid of at most one block per CU (few rows: each block then one or a few chunks), where
 //    the row-stationary set-up is shorter than the tile kernels' (C1 4096 x 320 x 320 7.40 -> 7.14 us,
 //    1024..2048 x 320 x 320..1280 4 % faster; grids of 320 blocks stay on the tile kernels, which are
-//    faster there: 4096 x 320 x 640 8.8 against 10.5 us).
+//    faster there: 4096 x 320 x 640 8.8 against 10.5 us);
+//  * or, without a residual, from 1024 rows, a 64x128 tile grid of at least 3.75 tiles per CU
+//    (960), where the tile kernels run several rounds of short blocks while the row-stationary
+//    kernels stream the columns through resident blocks (8192 x 320 x 2560 PLAIN 31.0 -> 21.4 us,
+//    4096 x 320 x 2560 GEGLU 20.0 -> 16.0, 8192 x 160 x 1280 PLAIN 18.1 -> 13.2, 960 tiles 4-16 %
+//    faster; at 640 and 768 tiles the tile kernels stay ahead, 4096 x 320 x 1280 PLAIN 11.2 against
+//    12.1 us).
 bool stripe_auto(const vk::GemmParams& p) {
     if (p.e) return false;
     if (cdiv(p.Mreal, STRIPE_BM) >= 2 * NCU / 4 && p.Mreal >= 16384) return true;
+    if (!p.R && p.Mreal >= 1024 && (long long)cdiv(p.Mreal, 64) * cdiv(p.Nreal, 128) >= 15LL * NCU / 4) return true;
     int cs, kper;
     stripe_ranges(p, cs, kper);
     return (long long)cdiv(p.Mreal, STRIPE_BM) * cs <= NCU;
