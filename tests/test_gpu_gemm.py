@@ -199,11 +199,14 @@ def test_i16_plain(variant, shape):
 
 
 # Shallow calls that the automatic dispatch sends to the row-stationary kernels by their tile count
-# (at least 960 tiles of 64x128, from 1024 rows, no residual): few rows over many columns, partial
-# row stripes and W chunks, K below 320, each epilogue; the residual call stays on the tile kernels.
+# (at least 960 tiles of 64x128, from 1024 rows): few rows over many columns, partial row stripes and
+# W chunks, K below 320, each epilogue, a residual; and deeper calls of few rows that it sends to the
+# K-split-over-waves kernel by its grid (at most 1024 rows and 1280 columns, Kp >= 768, at most one
+# 64x64 block per CU).
 AUTO_MID = [(vg.SRC_I16, 8192, 960, 160, vg.EPI_PLAIN, False), (vg.SRC_I8, 1030, 9600, 320, vg.EPI_PLAIN, False),
             (vg.SRC_I16, 4100, 2560, 320, vg.EPI_GEGLU, False), (vg.SRC_I16, 6150, 1288, 200, vg.EPI_GELU, False),
-            (vg.SRC_I16, 8192, 1280, 320, vg.EPI_PLAIN, True)]
+            (vg.SRC_I16, 8200, 1280, 320, vg.EPI_PLAIN, True), (vg.SRC_I16, 700, 1270, 1280, vg.EPI_PLAIN, True),
+            (vg.SRC_I8, 616, 1280, 768, vg.EPI_PLAIN, False), (vg.SRC_I16, 1000, 640, 1000, vg.EPI_GELU, False)]
 
 
 @pytest.mark.parametrize("case", AUTO_MID, ids=lambda c: f"{c[1]}x{c[2]}x{c[3]}-epi{c[4]}{'-res' if c[5] else ''}")

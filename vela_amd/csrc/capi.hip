@@ -159,8 +159,14 @@ bool kwave_applies(int src, int epi, const vk::GemmParams& p) {
 
 // Automatic use, for unsplit calls only: at most 640 rows and 1280 columns over Kp >= 1024 (measured:
 // the 512-row 3x3 convolutions of 1280 channels 99 -> 65 us and 191 -> 115 us without a workspace,
-// 512 x 1280 x 2560 linears 23.3 -> 21.0 us; wider or taller shapes stay on the tiled kernels).
-bool kwave_auto(const vk::GemmParams& p) { return p.Mreal <= 640 && p.Nreal <= 1280 && p.Kp >= 1024; }
+// 512 x 1280 x 2560 linears 23.3 -> 21.0 us; wider or taller shapes stay on the tiled kernels), or at
+// most 1024 rows and 1280 columns over Kp >= 768 with a grid of at most one 64x64 block per CU
+// (768 x 1280 x 1280 13.1 -> 12.6 us, 616 x 768 x 1280 9.8 -> 9.4; grids of 320 blocks and more are
+// up to 1.8x slower there: 1024 x 1280 x 1280 23.3 against 13.3 us).
+bool kwave_auto(const vk::GemmParams& p) {
+    if (p.Mreal <= 640 && p.Nreal <= 1280 && p.Kp >= 1024) return true;
+    return p.Mreal <= 1024 && p.Nreal <= 1280 && p.Kp >= 768 && (long long)cdiv(p.Mreal, 64) * cdiv(p.Nreal, 64) <= NCU;
+}
 
 // Blocks = row stripes x column ranges: as few column ranges as the table allows, raised until
 // there are two blocks per CU. Returns the column ranges and the chunks of each.
@@ -182,16 +188,16 @@ void stripe_ranges(const vk::GemmParams& p, int& cs, int& kper) {
 //    the row-stationary set-up is shorter than the tile kernels' (C1 4096 x 320 x 320 7.40 -> 7.14 us,
 //    1024..2048 x 320 x 320..1280 4 % faster; grids of 320 blocks stay on the tile kernels, which are
 //    faster there: 4096 x 320 x 640 8.8 against 10.5 us);
-//  * or, without a residual, from 1024 rows, a 64x128 tile grid of at least 3.75 tiles per CU
-//    (960), where the tile kernels run several rounds of short blocks while the row-stationary
-//    kernels stream the columns through resident blocks (8192 x 320 x 2560 PLAIN 31.0 -> 21.4 us,
-//    4096 x 320 x 2560 GEGLU 20.0 -> 16.0, 8192 x 160 x 1280 PLAIN 18.1 -> 13.2, 960 tiles 4-16 %
-//    faster; at 640 and 768 tiles the tile kernels stay ahead, 4096 x 320 x 1280 PLAIN 11.2 against
-//    12.1 us).
+//  * or, from 1024 rows, a 64x128 tile grid of at least 3.75 tiles per CU (960), where the tile
+//    kernels run several rounds of short blocks while the row-stationary kernels stream the columns
+//    through resident blocks (8192 x 320 x 2560 PLAIN 31.0 -> 21.4 us, 4096 x 320 x 2560 GEGLU
+//    20.0 -> 16.0, 8192 x 160 x 1280 PLAIN 18.1 -> 13.2, with a residual 8192 x 320 x 1280
+//    29.4 -> 21.1, 960 tiles 4-16 % faster; at 640 and 768 tiles the tile kernels stay ahead,
+//    4096 x 320 x 1280 PLAIN 11.2 against 12.1 us).
 bool stripe_auto(const vk::GemmParams& p) {
     if (p.e) return false;
     if (cdiv(p.Mreal, STRIPE_BM) >= 2 * NCU / 4 && p.Mreal >= 16384) return true;
-    if (!p.R && p.Mreal >= 1024 && (long long)cdiv(p.Mreal, 64) * cdiv(p.Nreal, 128) >= 15LL * NCU / 4) return true;
+    if (p.Mreal >= 1024 && (long long)cdiv(p.Mreal, 64) * cdiv(p.Nreal, 128) >= 15LL * NCU / 4) return true;
     int cs, kper;
     stripe_ranges(p, cs, kper);
     return (long long)cdiv(p.Mreal, STRIPE_BM) * cs <= NCU;
