@@ -159,13 +159,15 @@ bool kwave_applies(int src, int epi, const vk::GemmParams& p) {
 
 // Automatic use, for unsplit calls only: at most 640 rows and 1280 columns over Kp >= 1024 (measured:
 // the 512-row 3x3 convolutions of 1280 channels 99 -> 65 us and 191 -> 115 us without a workspace,
-// 512 x 1280 x 2560 linears 23.3 -> 21.0 us; wider or taller shapes stay on the tiled kernels), or at
-// most 1024 rows and 1280 columns over Kp >= 768 with a grid of at most one 64x64 block per CU
-// (768 x 1280 x 1280 13.1 -> 12.6 us, 616 x 768 x 1280 9.8 -> 9.4; grids of 320 blocks and more are
-// up to 1.8x slower there: 1024 x 1280 x 1280 23.3 against 13.3 us).
+// 512 x 1280 x 2560 linears 23.3 -> 21.0 us; wider or taller shapes stay on the tiled kernels), or,
+// for row sources (p.C == 0: the sweep behind this measured linears only), at most 1024 rows and
+// 1280 columns over Kp >= 768 with a grid of at most one 64x64 block per CU (768 x 1280 x 1280
+// 13.1 -> 12.6 us, 616 x 768 x 1280 9.8 -> 9.4; grids of 320 blocks and more are up to 1.8x slower
+// there: 1024 x 1280 x 1280 23.3 against 13.3 us).
 bool kwave_auto(const vk::GemmParams& p) {
     if (p.Mreal <= 640 && p.Nreal <= 1280 && p.Kp >= 1024) return true;
-    return p.Mreal <= 1024 && p.Nreal <= 1280 && p.Kp >= 768 && (long long)cdiv(p.Mreal, 64) * cdiv(p.Nreal, 64) <= NCU;
+    return p.C == 0 && p.Mreal <= 1024 && p.Nreal <= 1280 && p.Kp >= 768 &&
+           (long long)cdiv(p.Mreal, 64) * cdiv(p.Nreal, 64) <= NCU;
 }
 
 // Blocks = row stripes x column ranges: as few column ranges as the table allows, raised until

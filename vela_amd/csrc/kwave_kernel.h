@@ -213,11 +213,15 @@ __global__ void __launch_bounds__(256, SRC == SRC_I8 ? 2 : 1) kwave_kernel(const
             // the set-up's first phase reads the whole raw table, a quarter of it DMA'd by each wave:
             // each wave waits for its own DMA, older than every K-step load issued since (twelve per
             // step: four W, eight A; those of steps wave + 4 and wave + 8 stay in flight), then the
-            // barrier makes all four parts visible
-            if (wave + 8 < nK) vm_wait<24>();
-            else if (wave + 4 < nK) vm_wait<12>();
-            else vm_wait<0>();
-            block_barrier();
+            // barrier makes all four parts visible (the other epilogues have no table)
+            if constexpr (NEEDLUT) {
+                if (wave + 8 < nK) vm_wait<24>();
+                else if (wave + 4 < nK) vm_wait<12>();
+                else vm_wait<0>();
+                block_barrier();
+            } else {
+                if (wave >= nK) vm_wait<0>();
+            }
             fl = epi_setup<EPI, SRC, 64, 64, 256>(p, pre, L2048, s.sh);
         }
         for (int kt = wave; kt < nK; kt += 8) {
